@@ -1,0 +1,162 @@
+/*
+ * mamba_selective_scan.h — C ABI of the MI355X (gfx950) Mamba-1 selective-scan engine.
+ *
+ * Library: libmamba_selective_scan_hip.so (built from jax-mambas_amd/csrc/).
+ *
+ * Everything here is plain C: pointers, sizes and int32 flags. Tensors are device
+ * pointers, contiguous, in the physical layout the reference's kernel boundary uses
+ * (reference mamba/selective_scan_cuda.py:135-147 declares XLA layouts (0,2,1), i.e.
+ * channel-major [B][D][L] for u/delta/z/out and [B][N][L] for B/C):
+ *
+ *   u, delta, z, out, du, ddelta, dz, dout : [batch][dim][seqlen]
+ *   B, C, dB, dC                          : [batch][dstate][seqlen]
+ *   A, dA                                 : [dim][dstate]            (float32)
+ *   D, dD, delta_bias, ddelta_bias        : [dim]                    (float32)
+ *   initial_state, last_state, dlast_state, dinitial_state : [batch][dim][dstate] (float32)
+ *   seq_lens                              : [batch] int32 (optional variable lengths)
+ *   carries                               : [batch][dim][ceil(seqlen/1024)][dstate] float32
+ *                                           state h at the end of every 1024-step chunk
+ *
+ * All entry points are asynchronous on the given stream (a hipStream_t passed as
+ * void*; NULL = the default stream), re-entrant, and validate every argument before
+ * any HIP call, returning an mss_status code (never throwing across the ABI).
+ *
+ * Semantics (per batch b, channel d, state n, step t):
+ *   delta_t = delta_raw_t + bias_d;  if delta_softplus: delta_t = softplus(delta_t)
+ *             (identity above 20);  delta_t = 0 for t >= seq_lens[b]
+ *   a_bar   = exp(delta_t * A_dn)
+ *   Euler:  bu = delta_t * B_nt * u_t      ZOH: bu = expm1(delta_t*A_dn)/A_dn * B_nt * u_t
+ *   h_t     = a_bar * h_{t-1} + bu,  h_{-1} = initial_state (0 if NULL)
+ *   y_t     = sum_n C_nt h_t + D_d u_t;   out_t = y_t * silu(z_t) (if z);  out_t = 0 for t >= len
+ *   last_state = h at the final step.
+ */
+#ifndef MAMBA_SELECTIVE_SCAN_H_
+#define MAMBA_SELECTIVE_SCAN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSS_ABI_VERSION 1
+#define MSS_MAX_DSTATE 16
+#define MSS_CARRY_CHUNK 1024 /* step granularity of the `carries` residual */
+#define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
+
+typedef enum mss_status {
+  MSS_OK = 0,
+  MSS_ERR_INVALID_ARGUMENT = 1, /* bad shape, null required pointer, bad flag */
+  MSS_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
+  MSS_ERR_HIP = 3,              /* a HIP runtime call failed; see mss_last_hip_error */
+  MSS_ERR_WORKSPACE = 4         /* caller workspace too small */
+} mss_status;
+
+typedef enum mss_dtype { MSS_F32 = 0, MSS_BF16 = 1 } mss_dtype;
+typedef enum mss_discretization { MSS_EULER = 0, MSS_ZOH = 1 } mss_discretization;
+
+/* Forward of the fused scan (no counterpart symbol in the reference: it generalises
+ * MambaSelectiveScan, native/selective_scan_cuda.cu:554-573, with the fusions the
+ * reference model applies around the scan, mamba/mamba1.py:160-198, 300-337). */
+typedef struct mss_fwd_args {
+  int32_t batch, dim, seqlen, dstate;
+  int32_t discretization; /* mss_discretization */
+  int32_t delta_softplus; /* 0 / 1 */
+  int32_t io_dtype;       /* dtype of u, delta, z, out */
+  int32_t bc_dtype;       /* dtype of B, C */
+  const void* u;
+  const void* delta;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;             /* optional */
+  const void* z;              /* optional */
+  const float* delta_bias;    /* optional */
+  const float* initial_state; /* optional */
+  const int32_t* seq_lens;    /* optional */
+  void* out;
+  float* last_state; /* optional */
+  float* carries;    /* optional; required by mss_bwd */
+} mss_fwd_args;
+
+/* Backward of the fused scan. Outputs are fully overwritten (no accumulation).
+ * dA/dD/dB/dC/ddelta_bias are deterministic sums over batch and channels up to the
+ * order of fp32 adds inside one workgroup. */
+typedef struct mss_bwd_args {
+  int32_t batch, dim, seqlen, dstate;
+  int32_t discretization;
+  int32_t delta_softplus;
+  int32_t io_dtype; /* dtype of u, delta, z, dout, du, ddelta, dz */
+  int32_t bc_dtype; /* dtype of B, C, dB, dC */
+  const void* u;
+  const void* delta;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;
+  const void* z;
+  const float* delta_bias;
+  const float* initial_state;
+  const int32_t* seq_lens;
+  const float* carries;     /* from mss_fwd with the same inputs; required */
+  const void* dout;
+  const float* dlast_state; /* optional cotangent of last_state */
+  void* du;
+  void* ddelta;
+  float* dA;
+  void* dB;
+  void* dC;
+  float* dD;             /* required iff D given */
+  void* dz;              /* required iff z given */
+  float* ddelta_bias;    /* required iff delta_bias given */
+  float* dinitial_state; /* optional */
+  void* workspace;       /* device scratch; NULL = library allocates stream-ordered */
+  size_t workspace_bytes;
+} mss_bwd_args;
+
+/* Size of the scratch mss_bwd needs for these shapes (0 on invalid arguments). */
+size_t mss_bwd_workspace_bytes(const mss_bwd_args* args);
+
+int mss_fwd(const mss_fwd_args* args, void* stream);
+int mss_bwd(const mss_bwd_args* args, void* stream);
+
+/* --- Reference-compatible entry points (float32, no fusions). ---------------------
+ * Same argument order, attribute meaning and buffer shapes as the reference's XLA-FFI
+ * handlers; physical layouts as listed at the top of this file. */
+
+/* Replaces MambaSelectiveScan (reference native/selective_scan_cuda.cu:554-573).
+ * discretization: 0 Euler, 1 ZOH. chunk_states: [B][D][ceil(L/2048)][N][2] holding
+ * (prod a_bar over [0, chunk end], h at chunk end), as selective_scan_cuda.cu:306-320. */
+int mss_scan_fwd(void* stream, int32_t discretization, int32_t batch, int32_t length,
+                 int32_t dim, int32_t dstate, const float* A, const float* deltas,
+                 const float* B, const float* C, const float* u, const float* initial_x,
+                 float* y, float* final_x, float* chunk_states);
+
+/* Replaces MambaSelectiveScanBenchmark (reference native/selective_scan_cuda.cu:578-598):
+ * the forward launched `repeats` times back to back. */
+int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,
+                        int32_t length, int32_t dim, int32_t dstate, const float* A,
+                        const float* deltas, const float* B, const float* C, const float* u,
+                        const float* initial_x, float* y, float* final_x, float* chunk_states);
+
+/* Replaces MambaSelectiveScanBackward (reference native/selective_scan_bwd.cu:166-190),
+ * Euler discretization. chunk_states is accepted for signature compatibility and
+ * shape-checked; the states this kernel needs are recomputed from initial_x. */
+int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
+                 const float* A, const float* deltas, const float* B, const float* C,
+                 const float* u, const float* initial_x, const float* chunk_states,
+                 const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
+                 float* dC, float* du, float* dinitial_x);
+
+/* Human-readable text for a status code. */
+const char* mss_strerror(int status);
+/* Text of the last HIP error seen by this thread (for MSS_ERR_HIP). */
+const char* mss_last_hip_error(void);
+int mss_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA_SELECTIVE_SCAN_H_ */

@@ -1,0 +1,393 @@
+// Backward selective scan for gfx950 (MI355X).
+//
+// Reference behaviour followed (not its structure):
+// native/upstream_mamba/selective_scan_bwd_kernel.cuh:136-299 (reverse chunk loop, forward
+// recompute from chunk-start states, reverse adjoint scan seeded by the final-state
+// cotangent, du/ddelta/dA/dB/dC formulas) and its dormant fused branches :151-203,
+// :442-485 (softplus, z gate, D, delta bias, initial-state gradient).
+//
+// Mapping: one wave per channel, lane = segment of kT steps, chunk = 64*kT = 1024 steps
+// (the granularity of the forward's `carries` residual, so no forward recompute across
+// chunks is needed). A workgroup of kW waves walks K rounds of kW channels of one batch
+// row ("channel block") and every chunk from last to first. Per chunk, per state n:
+//   forward  local aggregate + 64-lane DPP scan from the stored chunk-start state, then a
+//            re-run that keeps h_t and a_bar*h_{t-1} in registers
+//   reverse  local aggregate of the adjoint + 64-lane reverse scan seeded by the carry from
+//            the chunk to the right (or dlast), then a re-run producing lambda_t and all
+//            per-step gradient terms
+// dB/dC are sums over channels: each wave adds its per-(n, t) terms into an LDS
+// accumulator shared by the workgroup (ds_add_f32), flushed once per chunk to a
+// per-channel-block partial; a second kernel sums the partials in a fixed order.
+// This replaces the reference's one-global-atomic-per-(b,d,n,t) scheme
+// (selective_scan_bwd_kernel.cuh:295-318).
+#include "mss_common.h"
+
+namespace mss {
+
+constexpr int kBwdT = 16;
+constexpr int kBwdW = 8;
+constexpr int kMaxChanPerBlock = 64;
+
+template <int kT, int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
+__global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
+  constexpr int kChunk = 64 * kT;
+  static_assert(kChunk == kCarryChunk, "backward chunk must match the carry residual");
+  constexpr int kStride = kT + 4;
+  __shared__ __attribute__((aligned(16))) float sB[64 * kStride];
+  __shared__ __attribute__((aligned(16))) float sC[64 * kStride];
+  __shared__ float acc[2 * kMaxN * kChunk];  // [which][n][j*64 + (lane ^ j)]
+  __shared__ float s_mu[kMaxChanPerBlock][kMaxN];
+  __shared__ float s_dA[kMaxChanPerBlock][kMaxN];
+  __shared__ float s_dD[kMaxChanPerBlock];
+  __shared__ float s_db[kMaxChanPerBlock];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.y;
+  const int blk = blockIdx.x;
+  const int L = p.seqlen;
+  const int N = p.dstate;
+  const int K = p.chan_per_block / kW;
+  const int len = p.seq_lens ? min(max(p.seq_lens[b], 0), L) : L;
+  const bool vec_io = p.vec_io != 0;
+  const bool vec_bc = p.vec_bc != 0;
+  const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + static_cast<size_t>(b) * N * L;
+  const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + static_cast<size_t>(b) * N * L;
+
+  for (int i = tid; i < 2 * kMaxN * kChunk; i += kW * 64) acc[i] = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const int cl = k * kW + w;
+    const int d = blk * p.chan_per_block + cl;
+    if (lane < kMaxN) {
+      float mu0 = 0.f;
+      if (d < p.dim && lane < N && p.dlast) mu0 = p.dlast[(static_cast<size_t>(b) * p.dim + d) * N + lane];
+      s_mu[cl][lane] = mu0;
+      s_dA[cl][lane] = 0.f;
+    }
+    if (lane == 0) {
+      s_dD[cl] = 0.f;
+      s_db[cl] = 0.f;
+    }
+  }
+  __syncthreads();
+
+  const int n_chunks = (L + kChunk - 1) / kChunk;
+  for (int c = n_chunks - 1; c >= 0; --c) {
+    const int t0 = c * kChunk;
+    const int tl = t0 + lane * kT;
+    for (int k = 0; k < K; ++k) {
+      const int cl = k * kW + w;
+      const int d_raw = blk * p.chan_per_block + cl;
+      const bool active = d_raw < p.dim;
+      const int d = active ? d_raw : p.dim - 1;
+      const size_t chan = static_cast<size_t>(b) * p.dim + d;
+      const size_t row = chan * L;
+      io_t* __restrict__ du_row = static_cast<io_t*>(p.du) + row;
+      io_t* __restrict__ dd_row = static_cast<io_t*>(p.ddelta) + row;
+
+      if (t0 >= len) {  // whole chunk past this row's length: zero gradients, carry passes
+        if (active) {
+          float zero[kT];
+#pragma unroll
+          for (int j = 0; j < kT; ++j) zero[j] = 0.f;
+          store_seg<kT>(du_row, tl, L, vec_io, zero);
+          store_seg<kT>(dd_row, tl, L, vec_io, zero);
+          if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, vec_io, zero);
+          if (c == 0 && p.dinit && lane < N) {
+            // len == 0: h_0 is never used, but x0 flows through identity steps to last.
+            p.dinit[chan * N + lane] = s_mu[cl][lane];
+          }
+        }
+        continue;
+      }
+
+      const float Dv = p.D ? p.D[d] : 0.f;
+      const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+      float dlt[kT], dlu[kT], uu[kT], g[kT], s1[kT], s2[kT];
+      float wz[kT], y[kT];
+      float ssum = 0.f;
+      {
+        float zr[kT];
+        load_seg<kT>(static_cast<const io_t*>(p.delta) + row, tl, L, vec_io, dlt);
+        load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, vec_io, uu);
+        load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, vec_io, g);
+        if constexpr (kHasZ) load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, vec_io, zr);
+#pragma unroll
+        for (int j = 0; j < kT; ++j) {
+          const bool valid = tl + j < len;
+          const float x = dlt[j] + bias;
+          float dv = p.delta_softplus ? softplus(x) : x;
+          dv = valid ? dv : 0.f;
+          const float uv = valid ? uu[j] : 0.f;
+          float go = valid ? g[j] : 0.f;
+          if constexpr (kHasZ) {
+            const float sz = sigmoid(zr[j]);
+            wz[j] = go * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);  // dz = wz * y
+            go = go * zr[j] * sz;
+            y[j] = Dv * uv;
+          }
+          dlt[j] = dv;
+          uu[j] = uv;
+          dlu[j] = dv * uv;
+          g[j] = go;
+          s1[j] = 0.f;
+          s2[j] = 0.f;
+          ssum += dv;
+        }
+      }
+
+      for (int n = 0; n < N; ++n) {
+        __syncthreads();
+        stage_row<kT>(Bb + static_cast<size_t>(n) * L, t0, L, vec_bc, sB, tid, kW * 64);
+        stage_row<kT>(Cb + static_cast<size_t>(n) * L, t0, L, vec_bc, sC, tid, kW * 64);
+        __syncthreads();
+        if (!active) continue;
+        const float An = p.A[d * N + n];
+        const float a2 = An * kLog2e;
+        float bv[kT], cv[kT], a[kT];
+        lds_read_seg<kT>(sB, lane, bv);
+        lds_read_seg<kT>(sC, lane, cv);
+        // ---- forward: local aggregate, scan, re-run from the true carry-in
+        float H = 0.f;
+#pragma unroll
+        for (int j = 0; j < kT; ++j) {
+          a[j] = fast_exp2(dlt[j] * a2);
+          const float bu = kZOH ? (expm1f(dlt[j] * An) / An) * bv[j] * uu[j] : dlu[j] * bv[j];
+          H = __builtin_fmaf(a[j], H, bu);
+        }
+        const float pseg = fast_exp2(a2 * ssum);
+        float P = pseg;
+        wave_scan_affine_fwd(P, H);
+        const float run = c == 0 ? (p.x0 ? p.x0[chan * N + n] : 0.f)
+                                 : p.carries[(chan * p.n_carry + (c - 1)) * N + n];
+        const float hend = __builtin_fmaf(P, run, H);
+        float h = dpp_mov<kWaveShr1, 0xF>(run, hend);
+        float ah[kT], hh[kT];
+#pragma unroll
+        for (int j = 0; j < kT; ++j) {
+          const float bu = kZOH ? (expm1f(dlt[j] * An) / An) * bv[j] * uu[j] : dlu[j] * bv[j];
+          ah[j] = a[j] * h;
+          h = ah[j] + bu;
+          hh[j] = h;
+          if constexpr (kHasZ) y[j] = __builtin_fmaf(cv[j], h, y[j]);
+        }
+        // ---- reverse: local aggregate of lambda, reverse scan, re-run with true lambda
+        float lam = cv[kT - 1] * g[kT - 1];
+#pragma unroll
+        for (int j = kT - 2; j >= 0; --j) lam = __builtin_fmaf(a[j + 1], lam, cv[j] * g[j]);
+        float ra = pseg, rb = a[0] * lam;
+        wave_scan_affine_rev(ra, rb, lane);
+        const float mu_in = s_mu[cl][n];
+        const float mu_out = readlane(__builtin_fmaf(ra, mu_in, rb), 0);
+        const float ra_s = dpp_mov<kWaveShl1, 0xF>(1.f, ra);
+        const float rb_s = dpp_mov<kWaveShl1, 0xF>(0.f, rb);
+        lam = __builtin_fmaf(ra_s, mu_in, rb_s) + cv[kT - 1] * g[kT - 1];
+        float dA_acc = 0.f;
+        float* accB = acc + n * kChunk;
+        float* accC = acc + (kMaxN + n) * kChunk;
+#pragma unroll
+        for (int j = kT - 1; j >= 0; --j) {
+          if (j < kT - 1) lam = __builtin_fmaf(a[j + 1], lam, cv[j] * g[j]);
+          const float q = lam * ah[j];
+          float dBv;
+          if constexpr (kZOH) {
+            const float e = expm1f(dlt[j] * An) / An;
+            const float lb = lam * bv[j];
+            s1[j] = __builtin_fmaf(lb, e, s1[j]);
+            s2[j] = __builtin_fmaf(An, q, __builtin_fmaf(lb * uu[j], a[j], s2[j]));
+            const float dedA = (dlt[j] * a[j] - e) / An;
+            dA_acc = __builtin_fmaf(dlt[j], q, __builtin_fmaf(lb * uu[j], dedA, dA_acc));
+            dBv = lam * e * uu[j];
+          } else {
+            s1[j] = __builtin_fmaf(lam, bv[j], s1[j]);
+            s2[j] = __builtin_fmaf(An, q, s2[j]);
+            dA_acc = __builtin_fmaf(dlt[j], q, dA_acc);
+            dBv = lam * dlu[j];
+          }
+          const int slot = j * 64 + (lane ^ j);
+          atomicAdd(accB + slot, dBv);
+          atomicAdd(accC + slot, g[j] * hh[j]);
+        }
+        const float dA_sum = wave_sum(dA_acc);
+        if (lane == 0) {
+          s_mu[cl][n] = mu_out;
+          s_dA[cl][n] += dA_sum;
+          if (c == 0 && p.dinit) p.dinit[chan * N + n] = mu_out;
+        }
+      }
+      if (!active) continue;
+
+      // ---- per-step gradients of the row
+      float dD_acc = 0.f, db_acc = 0.f;
+      float duv[kT], ddv[kT];
+#pragma unroll
+      for (int j = 0; j < kT; ++j) {
+        const bool valid = tl + j < len;
+        float du_j, dd_j;
+        if constexpr (kZOH) {
+          du_j = __builtin_fmaf(Dv, g[j], s1[j]);
+          dd_j = s2[j];
+        } else {
+          du_j = __builtin_fmaf(dlt[j], s1[j], Dv * g[j]);
+          dd_j = __builtin_fmaf(uu[j], s1[j], s2[j]);
+        }
+        if (p.delta_softplus) {
+          // d softplus(x)/dx = sigmoid(x) = 1 - exp(-softplus(x)); identity above 20.
+          const float x_sig = -expm1f(-dlt[j]);
+          const bool ident = dlt[j] > 20.f;
+          dd_j = ident ? dd_j : dd_j * x_sig;
+        }
+        du_j = valid ? du_j : 0.f;
+        dd_j = valid ? dd_j : 0.f;
+        dD_acc = __builtin_fmaf(g[j], uu[j], dD_acc);
+        db_acc += dd_j;
+        duv[j] = du_j;
+        ddv[j] = dd_j;
+        if constexpr (kHasZ) y[j] = valid ? wz[j] * y[j] : 0.f;
+      }
+      store_seg<kT>(du_row, tl, L, vec_io, duv);
+      store_seg<kT>(dd_row, tl, L, vec_io, ddv);
+      if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, vec_io, y);
+      const float dD_sum = wave_sum(dD_acc);
+      const float db_sum = wave_sum(db_acc);
+      if (lane == 0) {
+        s_dD[cl] += dD_sum;
+        s_db[cl] += db_sum;
+      }
+    }
+
+    // ---- flush this chunk's dB/dC sums over the block's channels
+    __syncthreads();
+    const size_t nl = static_cast<size_t>(N) * L;
+    float* part = p.part_dBC + (static_cast<size_t>(blk) * p.batch + b) * 2 * nl;
+    for (int e = tid; e < 2 * N * kChunk; e += kW * 64) {
+      const int which = e / (N * kChunk);
+      const int rem = e - which * N * kChunk;
+      const int n = rem / kChunk;
+      const int toff = rem - n * kChunk;
+      const int ln = toff / kT, j = toff - ln * kT;
+      float* src = acc + (which * kMaxN + n) * kChunk + j * 64 + (ln ^ j);
+      const int t = t0 + toff;
+      if (t < L) part[which * nl + static_cast<size_t>(n) * L + t] = *src;
+      *src = 0.f;
+    }
+    __syncthreads();
+  }
+
+  // ---- per-channel partial sums (over this row's steps)
+  for (int k = 0; k < K; ++k) {
+    const int cl = k * kW + w;
+    const int d = blk * p.chan_per_block + cl;
+    if (d >= p.dim) continue;
+    const size_t chan = static_cast<size_t>(b) * p.dim + d;
+    if (lane < N) p.part_dA[chan * N + lane] = s_dA[cl][lane];
+    if (lane == 0) {
+      p.part_dD[chan] = s_dD[cl];
+      p.part_dbias[chan] = s_db[cl];
+    }
+  }
+}
+
+// dB/dC[b][n][t] = sum over channel blocks of the partials, fixed order.
+template <typename bc_t>
+__global__ __launch_bounds__(256) void reduce_bc_kernel(const float* __restrict__ part, int n_blk,
+                                                        int batch, size_t nl, bc_t* __restrict__ dB,
+                                                        bc_t* __restrict__ dC) {
+  const size_t total = static_cast<size_t>(batch) * 2 * nl;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    float s = 0.f;
+    for (int k = 0; k < n_blk; ++k) s += part[static_cast<size_t>(k) * total + i];
+    const size_t bb = i / (2 * nl);
+    const size_t rem = i - bb * 2 * nl;
+    const int which = rem >= nl;
+    const size_t off = bb * nl + (rem - which * nl);
+    store_as(which ? dC + off : dB + off, s);
+  }
+}
+
+// dA[d][n] = sum_b part_dA[b][d][n]; dD[d], dbias[d] likewise (fixed order).
+__global__ __launch_bounds__(256) void reduce_small_kernel(const float* __restrict__ part_dA,
+                                                           const float* __restrict__ part_dD,
+                                                           const float* __restrict__ part_db,
+                                                           int batch, int dim, int dstate,
+                                                           float* dA, float* dD, float* dbias) {
+  const int dn = dim * dstate;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dn + 2 * dim;
+       i += gridDim.x * blockDim.x) {
+    if (i < dn) {
+      float s = 0.f;
+      for (int bb = 0; bb < batch; ++bb) s += part_dA[static_cast<size_t>(bb) * dn + i];
+      dA[i] = s;
+    } else {
+      const int which = (i - dn) / dim;
+      const int dd = (i - dn) - which * dim;
+      const float* src = which == 0 ? part_dD : part_db;
+      float* dst = which == 0 ? dD : dbias;
+      if (dst == nullptr) continue;
+      float s = 0.f;
+      for (int bb = 0; bb < batch; ++bb) s += src[static_cast<size_t>(bb) * dim + dd];
+      dst[dd] = s;
+    }
+  }
+}
+
+template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
+static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
+  dim3 grid(p.n_blocks_d, p.batch);
+  hipLaunchKernelGGL((bwd_kernel<kBwdT, kBwdW, kZOH, kHasZ, io_t, bc_t>), grid, dim3(kBwdW * 64), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+template <typename io_t, typename bc_t>
+static hipError_t launch_bwd_io(const BwdParams& p, int zoh, hipStream_t stream) {
+  const bool hz = p.z != nullptr;
+  if (zoh) return hz ? launch_bwd_t<true, true, io_t, bc_t>(p, stream)
+                     : launch_bwd_t<true, false, io_t, bc_t>(p, stream);
+  return hz ? launch_bwd_t<false, true, io_t, bc_t>(p, stream)
+            : launch_bwd_t<false, false, io_t, bc_t>(p, stream);
+}
+
+int bwd_chan_per_block(int batch, int dim) {
+  // Enough channel rounds per workgroup that ~one workgroup per CU (256 CUs) covers the
+  // problem, bounded by the LDS bookkeeping size. Depends on shapes only.
+  const long long octets = (static_cast<long long>(batch) * dim + kBwdW - 1) / kBwdW;
+  long long k = octets / 256;
+  if (k < 1) k = 1;
+  if (k > kMaxChanPerBlock / kBwdW) k = kMaxChanPerBlock / kBwdW;
+  const long long per_row = (dim + kBwdW - 1) / kBwdW;
+  if (k > per_row) k = per_row;
+  return static_cast<int>(k) * kBwdW;
+}
+
+hipError_t launch_bwd(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, void* dA, void* dB,
+                      void* dC, float* dD, float* dbias, hipStream_t stream) {
+  hipError_t e;
+  if (io_bf16) e = bc_bf16 ? launch_bwd_io<bf16_t, bf16_t>(p, zoh, stream)
+                           : launch_bwd_io<bf16_t, float>(p, zoh, stream);
+  else e = bc_bf16 ? launch_bwd_io<float, bf16_t>(p, zoh, stream)
+                   : launch_bwd_io<float, float>(p, zoh, stream);
+  if (e != hipSuccess) return e;
+  const size_t nl = static_cast<size_t>(p.dstate) * p.seqlen;
+  const size_t total = static_cast<size_t>(p.batch) * 2 * nl;
+  int grid = static_cast<int>((total + 255) / 256);
+  if (grid > 4096) grid = 4096;
+  if (bc_bf16) {
+    hipLaunchKernelGGL(reduce_bc_kernel<bf16_t>, dim3(grid), dim3(256), 0, stream, p.part_dBC,
+                       p.n_blocks_d, p.batch, nl, static_cast<bf16_t*>(dB), static_cast<bf16_t*>(dC));
+  } else {
+    hipLaunchKernelGGL(reduce_bc_kernel<float>, dim3(grid), dim3(256), 0, stream, p.part_dBC,
+                       p.n_blocks_d, p.batch, nl, static_cast<float*>(dB), static_cast<float*>(dC));
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int small = p.dim * p.dstate + 2 * p.dim;
+  hipLaunchKernelGGL(reduce_small_kernel, dim3((small + 255) / 256), dim3(256), 0, stream, p.part_dA,
+                     p.part_dD, p.part_dbias, p.batch, p.dim, p.dstate, static_cast<float*>(dA), dD,
+                     dbias);
+  return hipGetLastError();
+}
+
+}  // namespace mss

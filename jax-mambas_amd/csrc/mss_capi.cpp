@@ -1,0 +1,334 @@
+// C ABI of the selective-scan engine: argument validation, parameter packing, dispatch.
+//
+// Every check runs on the host before the first HIP call, so each error path is
+// reachable (and tested) without a GPU. Error contract mirrors the reference handlers:
+// invalid shapes/attributes -> MSS_ERR_INVALID_ARGUMENT (reference returns
+// ffi::Error::InvalidArgument, native/selective_scan_cuda.cu:400-440 and
+// native/selective_scan_bwd.cu:45-79); runtime failures -> MSS_ERR_HIP with the HIP
+// error text kept per thread (reference: ffi::Error::Internal with cudaGetErrorString,
+// native/selective_scan_cuda.cu:334-337).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "../../include/mamba_selective_scan.h"
+#include "mss_common.h"
+
+namespace mss {
+hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
+hipError_t launch_bwd(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, void* dA, void* dB,
+                      void* dC, float* dD, float* dbias, hipStream_t stream);
+int bwd_chan_per_block(int batch, int dim);
+}  // namespace mss
+
+namespace {
+
+thread_local std::string g_last_hip_error;
+
+int hip_fail(hipError_t e, const char* what) {
+  g_last_hip_error = std::string(what) + ": " + hipGetErrorString(e);
+  return MSS_ERR_HIP;
+}
+
+size_t dtype_size(int dt) { return dt == MSS_BF16 ? 2 : 4; }
+
+bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_dims(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate) {
+  if (batch <= 0 || dim <= 0 || seqlen <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (dstate <= 0 || dstate > 256) return MSS_ERR_INVALID_ARGUMENT;
+  if (dstate > MSS_MAX_DSTATE) return MSS_ERR_UNSUPPORTED;
+  // Index arithmetic inside the kernels uses 64-bit offsets; per-row steps are int.
+  return MSS_OK;
+}
+
+int check_common(int32_t discretization, int32_t softplus, int32_t io_dtype, int32_t bc_dtype) {
+  if (discretization != MSS_EULER && discretization != MSS_ZOH) return MSS_ERR_INVALID_ARGUMENT;
+  if (softplus != 0 && softplus != 1) return MSS_ERR_INVALID_ARGUMENT;
+  if ((io_dtype != MSS_F32 && io_dtype != MSS_BF16) || (bc_dtype != MSS_F32 && bc_dtype != MSS_BF16))
+    return MSS_ERR_INVALID_ARGUMENT;
+  return MSS_OK;
+}
+
+int n_carry_of(int32_t seqlen) { return (seqlen + MSS_CARRY_CHUNK - 1) / MSS_CARRY_CHUNK; }
+
+struct BwdLayout {
+  int chan_per_block = 0, n_blocks_d = 0;
+  size_t off_dA = 0, off_dD = 0, off_db = 0, total = 0;
+};
+
+BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate) {
+  BwdLayout l;
+  l.chan_per_block = mss::bwd_chan_per_block(batch, dim);
+  l.n_blocks_d = (dim + l.chan_per_block - 1) / l.chan_per_block;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t bc = static_cast<size_t>(l.n_blocks_d) * batch * 2 * dstate * seqlen * sizeof(float);
+  l.off_dA = up(bc);
+  l.off_dD = l.off_dA + up(static_cast<size_t>(batch) * dim * dstate * sizeof(float));
+  l.off_db = l.off_dD + up(static_cast<size_t>(batch) * dim * sizeof(float));
+  l.total = l.off_db + up(static_cast<size_t>(batch) * dim * sizeof(float));
+  return l;
+}
+
+int validate_fwd(const mss_fwd_args* a) {
+  if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
+  int s = check_dims(a->batch, a->dim, a->seqlen, a->dstate);
+  if (s != MSS_OK) return s;
+  s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
+  if (s != MSS_OK) return s;
+  if (!a->u || !a->delta || !a->A || !a->B || !a->C || !a->out) return MSS_ERR_INVALID_ARGUMENT;
+  return MSS_OK;
+}
+
+int validate_bwd(const mss_bwd_args* a) {
+  if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
+  int s = check_dims(a->batch, a->dim, a->seqlen, a->dstate);
+  if (s != MSS_OK) return s;
+  s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
+  if (s != MSS_OK) return s;
+  if (!a->u || !a->delta || !a->A || !a->B || !a->C || !a->carries || !a->dout) return MSS_ERR_INVALID_ARGUMENT;
+  if (!a->du || !a->ddelta || !a->dA || !a->dB || !a->dC) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->D && !a->dD) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->z && !a->dz) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->delta_bias && !a->ddelta_bias) return MSS_ERR_INVALID_ARGUMENT;
+  return MSS_OK;
+}
+
+int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
+  mss::FwdParams p{};
+  p.batch = a->batch;
+  p.dim = a->dim;
+  p.seqlen = a->seqlen;
+  p.dstate = a->dstate;
+  p.delta_softplus = a->delta_softplus;
+  const size_t io_row = static_cast<size_t>(a->seqlen) * dtype_size(a->io_dtype);
+  const size_t bc_row = static_cast<size_t>(a->seqlen) * dtype_size(a->bc_dtype);
+  p.vec_io = (io_row % 16 == 0) && aligned16(a->u) && aligned16(a->delta) && aligned16(a->z) &&
+             aligned16(a->out);
+  p.vec_bc = (bc_row % 16 == 0) && aligned16(a->B) && aligned16(a->C);
+  p.n_carry = n_carry_of(a->seqlen);
+  p.n_ref = (a->seqlen + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK;
+  p.u = a->u;
+  p.delta = a->delta;
+  p.A = a->A;
+  p.B = a->B;
+  p.C = a->C;
+  p.D = a->D;
+  p.z = a->z;
+  p.delta_bias = a->delta_bias;
+  p.x0 = a->initial_state;
+  p.seq_lens = a->seq_lens;
+  p.out = a->out;
+  p.last = a->last_state;
+  p.carries = a->carries;
+  p.ref_states = ref_states;
+  const hipError_t e = mss::launch_fwd(p, a->discretization == MSS_ZOH, a->io_dtype == MSS_BF16,
+                                       a->bc_dtype == MSS_BF16, stream);
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching selective scan forward");
+}
+
+int run_bwd(const mss_bwd_args* a, hipStream_t stream) {
+  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate);
+  char* ws = static_cast<char*>(a->workspace);
+  bool owned = false;
+  if (ws == nullptr) {
+    const hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), l.total, stream);
+    if (e != hipSuccess) return hip_fail(e, "allocating backward workspace");
+    owned = true;
+  } else if (a->workspace_bytes < l.total) {
+    return MSS_ERR_WORKSPACE;
+  }
+  mss::BwdParams p{};
+  p.batch = a->batch;
+  p.dim = a->dim;
+  p.seqlen = a->seqlen;
+  p.dstate = a->dstate;
+  p.delta_softplus = a->delta_softplus;
+  const size_t io_row = static_cast<size_t>(a->seqlen) * dtype_size(a->io_dtype);
+  const size_t bc_row = static_cast<size_t>(a->seqlen) * dtype_size(a->bc_dtype);
+  p.vec_io = (io_row % 16 == 0) && aligned16(a->u) && aligned16(a->delta) && aligned16(a->z) &&
+             aligned16(a->dout) && aligned16(a->du) && aligned16(a->ddelta) && aligned16(a->dz);
+  p.vec_bc = (bc_row % 16 == 0) && aligned16(a->B) && aligned16(a->C);
+  p.n_carry = n_carry_of(a->seqlen);
+  p.chan_per_block = l.chan_per_block;
+  p.n_blocks_d = l.n_blocks_d;
+  p.u = a->u;
+  p.delta = a->delta;
+  p.A = a->A;
+  p.B = a->B;
+  p.C = a->C;
+  p.D = a->D;
+  p.z = a->z;
+  p.delta_bias = a->delta_bias;
+  p.x0 = a->initial_state;
+  p.seq_lens = a->seq_lens;
+  p.carries = a->carries;
+  p.dout = a->dout;
+  p.dlast = a->dlast_state;
+  p.du = a->du;
+  p.ddelta = a->ddelta;
+  p.dz = a->dz;
+  p.dinit = a->dinitial_state;
+  p.part_dBC = reinterpret_cast<float*>(ws);
+  p.part_dA = reinterpret_cast<float*>(ws + l.off_dA);
+  p.part_dD = reinterpret_cast<float*>(ws + l.off_dD);
+  p.part_dbias = reinterpret_cast<float*>(ws + l.off_db);
+  hipError_t e = mss::launch_bwd(p, a->discretization == MSS_ZOH, a->io_dtype == MSS_BF16,
+                                 a->bc_dtype == MSS_BF16, a->dA, a->dB, a->dC, a->dD,
+                                 a->ddelta_bias, stream);
+  if (owned) {
+    const hipError_t f = hipFreeAsync(ws, stream);
+    if (e == hipSuccess) e = f;
+  }
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching selective scan backward");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mss_abi_version(void) { return MSS_ABI_VERSION; }
+
+const char* mss_strerror(int status) {
+  switch (status) {
+    case MSS_OK: return "ok";
+    case MSS_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case MSS_ERR_UNSUPPORTED: return "unsupported configuration (dstate must be <= 16)";
+    case MSS_ERR_HIP: return "HIP runtime error";
+    case MSS_ERR_WORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}
+
+const char* mss_last_hip_error(void) { return g_last_hip_error.c_str(); }
+
+size_t mss_bwd_workspace_bytes(const mss_bwd_args* a) {
+  if (a == nullptr || check_dims(a->batch, a->dim, a->seqlen, a->dstate) != MSS_OK) return 0;
+  return bwd_layout(a->batch, a->dim, a->seqlen, a->dstate).total;
+}
+
+int mss_fwd(const mss_fwd_args* args, void* stream) {
+  const int s = validate_fwd(args);
+  if (s != MSS_OK) return s;
+  return run_fwd(args, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int mss_bwd(const mss_bwd_args* args, void* stream) {
+  const int s = validate_bwd(args);
+  if (s != MSS_OK) return s;
+  return run_bwd(args, static_cast<hipStream_t>(stream));
+}
+
+int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,
+                        int32_t length, int32_t dim, int32_t dstate, const float* A,
+                        const float* deltas, const float* B, const float* C, const float* u,
+                        const float* initial_x, float* y, float* final_x, float* chunk_states) {
+  if (repeats <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  int s = check_dims(batch, dim, length, dstate);
+  if (s != MSS_OK) return s;
+  if (discretization != MSS_EULER && discretization != MSS_ZOH) return MSS_ERR_INVALID_ARGUMENT;
+  if (!A || !deltas || !B || !C || !u || !initial_x || !y || !final_x || !chunk_states)
+    return MSS_ERR_INVALID_ARGUMENT;
+  mss_fwd_args a{};
+  a.batch = batch;
+  a.dim = dim;
+  a.seqlen = length;
+  a.dstate = dstate;
+  a.discretization = discretization;
+  a.io_dtype = MSS_F32;
+  a.bc_dtype = MSS_F32;
+  a.u = u;
+  a.delta = deltas;
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.initial_state = initial_x;
+  a.out = y;
+  a.last_state = final_x;
+  for (int r = 0; r < repeats; ++r) {
+    s = run_fwd(&a, chunk_states, static_cast<hipStream_t>(stream));
+    if (s != MSS_OK) return s;
+  }
+  return MSS_OK;
+}
+
+int mss_scan_fwd(void* stream, int32_t discretization, int32_t batch, int32_t length, int32_t dim,
+                 int32_t dstate, const float* A, const float* deltas, const float* B,
+                 const float* C, const float* u, const float* initial_x, float* y, float* final_x,
+                 float* chunk_states) {
+  return mss_scan_fwd_repeat(stream, discretization, 1, batch, length, dim, dstate, A, deltas, B, C,
+                             u, initial_x, y, final_x, chunk_states);
+}
+
+int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
+                 const float* A, const float* deltas, const float* B, const float* C,
+                 const float* u, const float* initial_x, const float* chunk_states,
+                 const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
+                 float* dC, float* du, float* dinitial_x) {
+  int s = check_dims(batch, dim, length, dstate);
+  if (s != MSS_OK) return s;
+  if (!A || !deltas || !B || !C || !u || !initial_x || !chunk_states || !dout || !dfinal_x || !dA ||
+      !ddeltas || !dB || !dC || !du || !dinitial_x)
+    return MSS_ERR_INVALID_ARGUMENT;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  // The backward needs the state at every 1024-step boundary; the reference residual
+  // only holds 2048-step ones, so a states-only forward refreshes them.
+  const size_t carry_bytes =
+      static_cast<size_t>(batch) * dim * n_carry_of(length) * dstate * sizeof(float);
+  float* carries = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&carries), carry_bytes, st);
+  if (e != hipSuccess) return hip_fail(e, "allocating carry states");
+  mss::FwdParams p{};
+  p.batch = batch;
+  p.dim = dim;
+  p.seqlen = length;
+  p.dstate = dstate;
+  const size_t row = static_cast<size_t>(length) * sizeof(float);
+  p.vec_io = (row % 16 == 0) && aligned16(u) && aligned16(deltas);
+  p.vec_bc = (row % 16 == 0) && aligned16(B) && aligned16(C);
+  p.n_carry = n_carry_of(length);
+  p.n_ref = (length + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK;
+  p.u = u;
+  p.delta = deltas;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.x0 = initial_x;
+  p.out = nullptr;  // states only
+  p.carries = carries;
+  e = mss::launch_fwd(p, 0, 0, 0, st);
+  if (e != hipSuccess) {
+    (void)hipFreeAsync(carries, st);
+    return hip_fail(e, "launching carry refresh");
+  }
+  mss_bwd_args a{};
+  a.batch = batch;
+  a.dim = dim;
+  a.seqlen = length;
+  a.dstate = dstate;
+  a.io_dtype = MSS_F32;
+  a.bc_dtype = MSS_F32;
+  a.u = u;
+  a.delta = deltas;
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.initial_state = initial_x;
+  a.carries = carries;
+  a.dout = dout;
+  a.dlast_state = dfinal_x;
+  a.du = du;
+  a.ddelta = ddeltas;
+  a.dA = dA;
+  a.dB = dB;
+  a.dC = dC;
+  a.dinitial_state = dinitial_x;
+  s = run_bwd(&a, st);
+  e = hipFreeAsync(carries, st);
+  if (s != MSS_OK) return s;
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "freeing carry states");
+}
+
+}  // extern "C"

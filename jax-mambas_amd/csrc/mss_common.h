@@ -1,0 +1,354 @@
+// Device-side helpers shared by the forward and backward selective-scan kernels.
+//
+// Work mapping used by both kernels: one wavefront (64 lanes) owns one (batch, channel)
+// row; its 64 lanes own 64 consecutive segments of kT steps each, so one wave covers a
+// chunk of 64*kT steps and walks the sequence chunk by chunk. Inside a segment a lane
+// runs the recurrence sequentially; segments are joined with a 64-lane affine scan on
+// DPP lane shifts. The state loop (n) is outermost inside a chunk so only one state's
+// per-step coefficients live in registers at a time.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mss {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kMaxN = 16;
+constexpr int kCarryChunk = 1024;
+constexpr int kRefChunk = 2048;
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+__device__ __forceinline__ void store_as(float* p, float v) { *p = v; }
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  bf16_t r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
+    r.bits = static_cast<uint16_t>(u >> 16);
+  }
+  return r;
+}
+__device__ __forceinline__ void store_as(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+
+// ---------------------------------------------------------------------------------
+// Cross-lane moves (gfx9 DPP). Lanes whose source is outside the pattern keep `old`.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                         kCtrl, kRowMask, 0xF, false));
+}
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowShl1 = 0x101, kRowShl2 = 0x102, kRowShl4 = 0x104, kRowShl8 = 0x108;
+constexpr int kWaveShr1 = 0x138, kWaveShl1 = 0x130;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Inclusive scan over the 64 lanes (lane order = time order) of affine maps
+// h -> P*h + H. Combining an earlier element (Pl, Hl) with a later one (Pr, Hr) gives
+// (Pl*Pr, Pr*Hl + Hr): the operator of reference native/selective_scan_cuda.cu:58-63.
+__device__ __forceinline__ void wave_scan_affine_fwd(float& P, float& H) {
+#define MSS_FWD_STEP(CTRL, RM)                   \
+  {                                              \
+    const float ps = dpp_mov<CTRL, RM>(1.f, P);  \
+    const float hs = dpp_mov<CTRL, RM>(0.f, H);  \
+    H = __builtin_fmaf(P, hs, H);                \
+    P = P * ps;                                  \
+  }
+  MSS_FWD_STEP(kRowShr1, 0xF)
+  MSS_FWD_STEP(kRowShr2, 0xF)
+  MSS_FWD_STEP(kRowShr4, 0xF)
+  MSS_FWD_STEP(kRowShr8, 0xF)
+  MSS_FWD_STEP(kRowBcast15, 0xA)
+  MSS_FWD_STEP(kRowBcast31, 0xC)
+#undef MSS_FWD_STEP
+}
+
+// Inclusive reverse scan (lane 63 is applied first) of affine maps m -> a*m + b:
+// lane i ends with R_i = f_i o f_{i+1} o ... o f_63.
+__device__ __forceinline__ void wave_scan_affine_rev(float& a, float& b, int lane) {
+#define MSS_REV_STEP(CTRL)                        \
+  {                                               \
+    const float as = dpp_mov<CTRL, 0xF>(1.f, a);  \
+    const float bs = dpp_mov<CTRL, 0xF>(0.f, b);  \
+    b = __builtin_fmaf(a, bs, b);                 \
+    a = a * as;                                   \
+  }
+  MSS_REV_STEP(kRowShl1)
+  MSS_REV_STEP(kRowShl2)
+  MSS_REV_STEP(kRowShl4)
+  MSS_REV_STEP(kRowShl8)
+#undef MSS_REV_STEP
+  // Row r (lanes 16r..16r+15) now holds suffixes within the row; lane 16r holds the
+  // whole row's map. Compose with the rows to the right.
+  const float a1 = readlane(a, 16), b1 = readlane(b, 16);
+  const float a2 = readlane(a, 32), b2 = readlane(b, 32);
+  const float a3 = readlane(a, 48), b3 = readlane(b, 48);
+  // S2 = R2 o R3, S1 = R1 o S2 (uniform values).
+  const float s2a = a2 * a3, s2b = __builtin_fmaf(a2, b3, b2);
+  const float s1a = a1 * s2a, s1b = __builtin_fmaf(a1, s2b, b1);
+  const int row = lane >> 4;
+  const float sa = row == 0 ? s1a : (row == 1 ? s2a : (row == 2 ? a3 : 1.f));
+  const float sb = row == 0 ? s1b : (row == 1 ? s2b : (row == 2 ? b3 : 0.f));
+  b = __builtin_fmaf(a, sb, b);
+  a = a * sa;
+}
+
+// Sum over the 64 lanes; the result is returned uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<kRowShr1, 0xF>(0.f, v);
+  v += dpp_mov<kRowShr2, 0xF>(0.f, v);
+  v += dpp_mov<kRowShr4, 0xF>(0.f, v);
+  v += dpp_mov<kRowShr8, 0xF>(0.f, v);
+  v += dpp_mov<kRowBcast15, 0xA>(0.f, v);
+  v += dpp_mov<kRowBcast31, 0xC>(0.f, v);
+  return readlane(v, 63);
+}
+
+// ---------------------------------------------------------------------------------
+// Scalar math.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// log1p(w) for w >= 0 via Goldberg's correction: log(1+w) * w / ((1+w)-1).
+__device__ __forceinline__ float log1p_pos(float w) {
+  const float u = 1.f + w;
+  const float d = u - 1.f;
+  const float l = fast_log2(u) * kLn2;
+  return d == 0.f ? w : l * (w / d);
+}
+
+// softplus(x) = log(1 + e^x), identity above 20 (threshold of the reference kernel,
+// native/upstream_mamba/selective_scan_bwd_kernel.cuh:157).
+__device__ __forceinline__ float softplus(float x) {
+  const float w = fast_exp2(-fabsf(x) * kLog2e);
+  const float r = fmaxf(x, 0.f) + log1p_pos(w);
+  return x > 20.f ? x : r;
+}
+
+__device__ __forceinline__ float sigmoid(float x) {
+  return fast_rcp(1.f + fast_exp2(-x * kLog2e));
+}
+
+// ---------------------------------------------------------------------------------
+// Segment loads/stores. `row` points at element 0 of a [.. ][L] row; the segment is
+// elements [t, t+N). Elements at or beyond `L` read as 0 and are not written.
+template <int N>
+__device__ __forceinline__ void load_seg(const float* __restrict__ row, int t, int L, bool vec,
+                                         float (&v)[N]) {
+  if (vec && t + N <= L) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(row + t);
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const f32x4 x = __builtin_nontemporal_load(p + q);
+      v[4 * q + 0] = x.x;
+      v[4 * q + 1] = x.y;
+      v[4 * q + 2] = x.z;
+      v[4 * q + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = (t + j < L) ? row[t + j] : 0.f;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void load_seg(const bf16_t* __restrict__ row, int t, int L, bool vec,
+                                         float (&v)[N]) {
+  if (vec && t + N <= L) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(row + t);
+#pragma unroll
+    for (int q = 0; q < N / 8; ++q) {
+      const u32x4 x = __builtin_nontemporal_load(p + q);
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[8 * q + 2 * k + 0] = __uint_as_float(w[k] << 16);
+        v[8 * q + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = (t + j < L) ? to_f32(row[t + j]) : 0.f;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_seg(float* __restrict__ row, int t, int L, bool vec,
+                                          const float (&v)[N]) {
+  if (vec && t + N <= L) {
+    f32x4* p = reinterpret_cast<f32x4*>(row + t);
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const f32x4 x = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+      __builtin_nontemporal_store(x, p + q);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (t + j < L) row[t + j] = v[j];
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L, bool vec,
+                                          const float (&v)[N]) {
+  if (vec && t + N <= L) {
+    u32x4* p = reinterpret_cast<u32x4*>(row + t);
+#pragma unroll
+    for (int q = 0; q < N / 8; ++q) {
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        w[k] = static_cast<uint32_t>(f32_to_bf16(v[8 * q + 2 * k]).bits) |
+               (static_cast<uint32_t>(f32_to_bf16(v[8 * q + 2 * k + 1]).bits) << 16);
+      }
+      const u32x4 x = {w[0], w[1], w[2], w[3]};
+      __builtin_nontemporal_store(x, p + q);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (t + j < L) store_as(row + t + j, v[j]);
+  }
+}
+
+// Stage elements [t0, t0 + 64*kT) of a [..][L] row into LDS with a padded segment
+// stride of (kT + 4) floats (lane-strided reads then hit distinct banks). Cooperative
+// over `nthreads` threads starting at `tid`.
+template <int kT>
+__device__ __forceinline__ void stage_row(const float* __restrict__ row, int t0, int L, bool vec,
+                                          float* __restrict__ lds, int tid, int nthreads) {
+  constexpr int kChunk = 64 * kT;
+  constexpr int kStride = kT + 4;
+  if (vec && t0 + kChunk <= L) {
+    const float4* p = reinterpret_cast<const float4*>(row + t0);
+    for (int q = tid; q < kChunk / 4; q += nthreads) {
+      const float4 x = p[q];
+      const int e = 4 * q;
+      *reinterpret_cast<float4*>(lds + (e / kT) * kStride + (e % kT)) = x;
+    }
+  } else {
+    for (int e = tid; e < kChunk; e += nthreads) {
+      const int t = t0 + e;
+      lds[(e / kT) * kStride + (e % kT)] = t < L ? row[t] : 0.f;
+    }
+  }
+}
+
+template <int kT>
+__device__ __forceinline__ void stage_row(const bf16_t* __restrict__ row, int t0, int L, bool vec,
+                                          float* __restrict__ lds, int tid, int nthreads) {
+  constexpr int kChunk = 64 * kT;
+  constexpr int kStride = kT + 4;
+  if (vec && t0 + kChunk <= L) {
+    const uint4* p = reinterpret_cast<const uint4*>(row + t0);
+    for (int q = tid; q < kChunk / 8; q += nthreads) {
+      const uint4 x = p[q];
+      const int e = 8 * q;
+      float* dst = lds + (e / kT) * kStride + (e % kT);
+      *reinterpret_cast<float4*>(dst) =
+          make_float4(__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u),
+                      __uint_as_float(x.y << 16), __uint_as_float(x.y & 0xffff0000u));
+      *reinterpret_cast<float4*>(dst + 4) =
+          make_float4(__uint_as_float(x.z << 16), __uint_as_float(x.z & 0xffff0000u),
+                      __uint_as_float(x.w << 16), __uint_as_float(x.w & 0xffff0000u));
+    }
+  } else {
+    for (int e = tid; e < kChunk; e += nthreads) {
+      const int t = t0 + e;
+      lds[(e / kT) * kStride + (e % kT)] = t < L ? to_f32(row[t]) : 0.f;
+    }
+  }
+}
+
+// Read a lane's kT staged values (16-byte LDS reads).
+template <int kT>
+__device__ __forceinline__ void lds_read_seg(const float* __restrict__ lds, int lane,
+                                             float (&v)[kT]) {
+  const float4* p = reinterpret_cast<const float4*>(lds + lane * (kT + 4));
+#pragma unroll
+  for (int q = 0; q < kT / 4; ++q) {
+    const float4 x = p[q];
+    v[4 * q + 0] = x.x;
+    v[4 * q + 1] = x.y;
+    v[4 * q + 2] = x.z;
+    v[4 * q + 3] = x.w;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Kernel parameter blocks (host fills them after validation).
+struct FwdParams {
+  int batch, dim, seqlen, dstate;
+  int delta_softplus;
+  int vec_io;  // 16-byte vector access legal for u/delta/z/out rows
+  int vec_bc;  // ... for B/C rows
+  int n_carry;  // ceil(L / 1024)
+  int n_ref;    // ceil(L / 2048)
+  const void* u;
+  const void* delta;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;
+  const void* z;
+  const float* delta_bias;
+  const float* x0;
+  const int* seq_lens;
+  void* out;
+  float* last;
+  float* carries;
+  float* ref_states;
+};
+
+struct BwdParams {
+  int batch, dim, seqlen, dstate;
+  int delta_softplus;
+  int vec_io, vec_bc;
+  int n_carry;
+  int chan_per_block;  // channels one workgroup walks (multiple of the wave count)
+  int n_blocks_d;      // ceil(dim / chan_per_block)
+  const void* u;
+  const void* delta;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;
+  const void* z;
+  const float* delta_bias;
+  const float* x0;
+  const int* seq_lens;
+  const float* carries;
+  const void* dout;
+  const float* dlast;
+  void* du;
+  void* ddelta;
+  void* dz;
+  float* dinit;
+  // workspace partials
+  float* part_dBC;   // [n_blocks_d][batch][2][dstate][L]
+  float* part_dA;    // [batch][dim][dstate]
+  float* part_dD;    // [batch][dim]
+  float* part_dbias; // [batch][dim]
+};
+
+}  // namespace mss

@@ -1,0 +1,132 @@
+"""ctypes binding of libmamba_selective_scan_hip.so (the C ABI in include/mamba_selective_scan.h).
+
+Loader behaviour mirrors the reference's ``register_cuda_kernel``
+(``mamba/selective_scan_cuda.py:18-53``): an explicit path or a fixed candidate list,
+``FileNotFoundError`` naming every searched path when nothing is built, idempotent
+registration. There is no fallback: without the library nothing in this package runs.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIBRARY_NAME = "libmamba_selective_scan_hip.so"
+
+MSS_OK = 0
+MSS_ERR_INVALID_ARGUMENT = 1
+MSS_ERR_UNSUPPORTED = 2
+MSS_ERR_HIP = 3
+MSS_ERR_WORKSPACE = 4
+MSS_F32 = 0
+MSS_BF16 = 1
+MSS_EULER = 0
+MSS_ZOH = 1
+MSS_MAX_DSTATE = 16
+MSS_CARRY_CHUNK = 1024
+MSS_REF_CHUNK = 2048
+
+# Every symbol include/mamba_selective_scan.h declares.
+EXPORTED_SYMBOLS = (
+    "mss_bwd_workspace_bytes",
+    "mss_fwd",
+    "mss_bwd",
+    "mss_scan_fwd",
+    "mss_scan_fwd_repeat",
+    "mss_scan_bwd",
+    "mss_strerror",
+    "mss_last_hip_error",
+    "mss_abi_version",
+)
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i32), ("dim", _i32), ("seqlen", _i32), ("dstate", _i32),
+        ("discretization", _i32), ("delta_softplus", _i32), ("io_dtype", _i32), ("bc_dtype", _i32),
+        ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
+        ("D", _p), ("z", _p), ("delta_bias", _p), ("initial_state", _p), ("seq_lens", _p),
+        ("out", _p), ("last_state", _p), ("carries", _p),
+    ]
+
+
+class BwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i32), ("dim", _i32), ("seqlen", _i32), ("dstate", _i32),
+        ("discretization", _i32), ("delta_softplus", _i32), ("io_dtype", _i32), ("bc_dtype", _i32),
+        ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
+        ("D", _p), ("z", _p), ("delta_bias", _p), ("initial_state", _p), ("seq_lens", _p),
+        ("carries", _p), ("dout", _p), ("dlast_state", _p),
+        ("du", _p), ("ddelta", _p), ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("dz", _p),
+        ("ddelta_bias", _p), ("dinitial_state", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+_LIBRARY = None
+_LIBRARY_PATH = None
+
+
+def library_candidates():
+    env = os.environ.get("MSS_LIBRARY")
+    if env:
+        yield Path(env)
+    pkg_root = Path(__file__).resolve().parents[1]  # jax-mambas_amd/
+    yield pkg_root / "build" / LIBRARY_NAME
+    yield pkg_root / LIBRARY_NAME
+
+
+def register_hip_kernel(library_path=None):
+    """Load the HIP library once; raise FileNotFoundError if it is not built."""
+    global _LIBRARY, _LIBRARY_PATH
+    if _LIBRARY is not None:
+        return _LIBRARY
+    candidates = [Path(library_path)] if library_path is not None else list(library_candidates())
+    path = next((c for c in candidates if c.is_file()), None)
+    if path is None:
+        searched = ", ".join(str(c) for c in candidates)
+        raise FileNotFoundError(f"The selective-scan HIP library is not built; searched: {searched}")
+    lib = ctypes.CDLL(str(path))
+    lib.mss_fwd.argtypes = [ctypes.POINTER(FwdArgs), _p]
+    lib.mss_fwd.restype = ctypes.c_int
+    lib.mss_bwd.argtypes = [ctypes.POINTER(BwdArgs), _p]
+    lib.mss_bwd.restype = ctypes.c_int
+    lib.mss_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
+    lib.mss_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.mss_scan_fwd.argtypes = [_p, _i32, _i32, _i32, _i32, _i32] + [_p] * 9
+    lib.mss_scan_fwd.restype = ctypes.c_int
+    lib.mss_scan_fwd_repeat.argtypes = [_p, _i32, _i32, _i32, _i32, _i32, _i32] + [_p] * 9
+    lib.mss_scan_fwd_repeat.restype = ctypes.c_int
+    lib.mss_scan_bwd.argtypes = [_p, _i32, _i32, _i32, _i32] + [_p] * 15
+    lib.mss_scan_bwd.restype = ctypes.c_int
+    lib.mss_strerror.argtypes = [ctypes.c_int]
+    lib.mss_strerror.restype = ctypes.c_char_p
+    lib.mss_last_hip_error.argtypes = []
+    lib.mss_last_hip_error.restype = ctypes.c_char_p
+    lib.mss_abi_version.argtypes = []
+    lib.mss_abi_version.restype = ctypes.c_int
+    _LIBRARY = lib
+    _LIBRARY_PATH = path
+    return lib
+
+
+def library_path():
+    return _LIBRARY_PATH
+
+
+class MSSError(RuntimeError):
+    def __init__(self, status, op):
+        lib = register_hip_kernel()
+        msg = lib.mss_strerror(status).decode()
+        if status == MSS_ERR_HIP:
+            msg += ": " + lib.mss_last_hip_error().decode()
+        super().__init__(f"{op} failed with status {status}: {msg}")
+        self.status = status
+
+
+def check(status, op):
+    if status != MSS_OK:
+        raise MSSError(status, op)

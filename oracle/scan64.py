@@ -1,0 +1,227 @@
+"""Float64 CPU oracle for the fused Mamba-1 selective scan — TEST INFRASTRUCTURE ONLY.
+
+Restates, in numpy float64 with a sequential loop over L (vectorised over batch,
+channel and state), the math of the reference's scan and of the fusions its model
+applies around it:
+
+* recurrence, discretisation and state threading — ``mamba/selective_scan_cuda.py:56-90``
+  (``selective_scan_reference``: ``a_bar = exp(delta*A)``; Euler ``b_bar = delta*B``;
+  ZOH ``b_bar = expm1(delta*A)/A*B``; ``bu[:,0] += a_bar[:,0]*x0``; compose
+  ``(a_r*a_l, a_r*h_l + h_r)``; ``y = sum_n C*h``; ``final = h[:, -1]``), which is the
+  same recurrence the reference's own CPU test writes as a Python loop
+  (``tests/test_selective_scan_cuda.py:35-52``);
+* fused extras from the caller — delta = softplus(dt_proj(x) + bias)
+  (``mamba/mamba1.py:117-126, 165``), mask multiply on delta (``mamba/mamba1.py:167-168``),
+  ``y += D*u`` (``mamba/mamba1.py:195-196``), ``out = y*silu(z)``
+  (``mamba/mamba1.py:308, 332``); the softplus threshold 20 of the reference kernel
+  (``native/upstream_mamba/selective_scan_bwd_kernel.cuh:157``);
+* reference chunk residual ``(prod a_bar, h)`` at 2048-step chunk ends
+  (``native/selective_scan_cuda.cu:306-320``);
+* backward: hand-derived adjoint recurrence following
+  ``native/upstream_mamba/selective_scan_bwd_kernel.cuh:175-203, 244-299, 442-485``
+  (dz, g, lambda, du, ddelta, dA, dB, dC, dD, dx0, softplus chain rule, dbias).
+
+Variable-length contract (build's own, a superset of the reference's delta mask):
+for ``t >= seq_lens[b]`` the step is the identity (a_bar = 1, b_bar = 0), ``out`` is 0,
+``dout`` is ignored and every gradient contribution from those steps is 0.
+
+Pinning (see tests/test_oracle.py): sequential loop vs an independent torch
+associative-scan restatement of the reference; closed forms (delta = 0, u = 0,
+A = 0 cumsum, constant-coefficient geometric series, L = 1); split invariance via
+initial/final state; varlen = per-row unpadded runs; backward vs torch float64
+autograd of an independent loop and vs central finite differences.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+SOFTPLUS_THRESHOLD = 20.0
+REF_CHUNK = 2048
+
+
+def softplus64(x):
+    x = np.asarray(x, np.float64)
+    return np.where(x > SOFTPLUS_THRESHOLD, x, np.log1p(np.exp(np.minimum(x, SOFTPLUS_THRESHOLD))))
+
+
+def sigmoid64(x):
+    x = np.asarray(x, np.float64)
+    return 0.5 * (1.0 + np.tanh(0.5 * x))
+
+
+def _f64(a):
+    return None if a is None else np.asarray(a, np.float64)
+
+
+def _prepare(u, delta, A, B, C, D, z, delta_bias, delta_softplus, initial_state, seq_lens):
+    u, delta, A, B, C = (_f64(a) for a in (u, delta, A, B, C))
+    bsz, dim, L = u.shape
+    n = A.shape[1]
+    assert delta.shape == (bsz, dim, L) and A.shape == (dim, n)
+    assert B.shape == (bsz, n, L) and C.shape == (bsz, n, L)
+    bias = np.zeros(dim) if delta_bias is None else _f64(delta_bias)
+    x = delta + bias[None, :, None]
+    dl = softplus64(x) if delta_softplus else x.copy()
+    if seq_lens is None:
+        lens = np.full(bsz, L, np.int64)
+    else:
+        lens = np.clip(np.asarray(seq_lens, np.int64), 0, L)
+    mask = (np.arange(L)[None, :] < lens[:, None]).astype(np.float64)  # (B, L)
+    dl = dl * mask[:, None, :]
+    x0 = np.zeros((bsz, dim, n)) if initial_state is None else _f64(initial_state).copy()
+    Dv = None if D is None else _f64(D)
+    zz = None if z is None else _f64(z)
+    return u, dl, x, A, B, C, Dv, zz, x0, mask, lens
+
+
+def _discretize(dl_t, u_t, A, B_t, zoh):
+    """dl_t, u_t: (B, D); A: (D, N); B_t: (B, N) -> a_bar, bu, E (each (B, D, N))."""
+    dA = dl_t[:, :, None] * A[None]
+    a_bar = np.exp(dA)
+    if zoh:
+        E = np.expm1(dA) / A[None]
+    else:
+        E = np.broadcast_to(dl_t[:, :, None], dA.shape)
+    bu = E * B_t[:, None, :] * u_t[:, :, None]
+    return a_bar, bu, E
+
+
+def forward(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+            initial_state=None, seq_lens=None, discretization="euler", checkpoint_every=0):
+    """Returns dict(out, y, last_state, ref_chunk_states[, checkpoints]).
+
+    Layouts: u, delta, z, out, y: (B, D, L); B, C: (B, N, L); A: (D, N); D, delta_bias:
+    (D,); initial_state / last_state: (B, D, N); ref_chunk_states:
+    (B, D, ceil(L/2048), N, 2) holding (prod a_bar over [0, chunk end], h at chunk end).
+    """
+    zoh = discretization == "zoh"
+    u, dl, x, A, B, C, Dv, zz, h, mask, lens = _prepare(
+        u, delta, A, B, C, D, z, delta_bias, delta_softplus, initial_state, seq_lens)
+    bsz, dim, L = u.shape
+    n = A.shape[1]
+    y = np.empty((bsz, dim, L))
+    n_ref = (L + REF_CHUNK - 1) // REF_CHUNK
+    ref_states = np.empty((bsz, dim, n_ref, n, 2))
+    prod = np.ones((bsz, dim, n))
+    ckpt = {}
+    for t in range(L):
+        if checkpoint_every and t % checkpoint_every == 0:
+            ckpt[t] = h.copy()
+        a_bar, bu, _ = _discretize(dl[:, :, t], u[:, :, t], A, B[:, :, t], zoh)
+        h = a_bar * h + bu
+        prod = prod * a_bar
+        y[:, :, t] = np.einsum("bn,bdn->bd", C[:, :, t], h)
+        if (t + 1) % REF_CHUNK == 0 or t == L - 1:
+            c = t // REF_CHUNK
+            ref_states[:, :, c, :, 0] = prod
+            ref_states[:, :, c, :, 1] = h
+    if Dv is not None:
+        y = y + Dv[None, :, None] * u
+    out = y * (zz * sigmoid64(zz)) if zz is not None else y.copy()
+    out = out * mask[:, None, :]
+    res = dict(out=out, y=y, last_state=h, ref_chunk_states=ref_states)
+    if checkpoint_every:
+        res["checkpoints"] = ckpt
+    return res
+
+
+def backward(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_softplus=False,
+             initial_state=None, seq_lens=None, discretization="euler", dlast_state=None,
+             segment=64):
+    """Gradients of out (and last_state) w.r.t. every input, float64.
+
+    Returns dict(du, ddelta, dA, dB, dC, dD, dz, ddelta_bias, dinitial_state); entries for
+    absent optional inputs are None. Forward states are recomputed from checkpoints every
+    ``segment`` steps, so memory stays O(B*D*N*(L/segment + segment)).
+    """
+    zoh = discretization == "zoh"
+    fw = forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, initial_state, seq_lens,
+                 discretization, checkpoint_every=segment)
+    u, dl, x, A, B, C, Dv, zz, _, mask, lens = _prepare(
+        u, delta, A, B, C, D, z, delta_bias, delta_softplus, initial_state, seq_lens)
+    bsz, dim, L = u.shape
+    n = A.shape[1]
+    dout = _f64(dout) * mask[:, None, :]
+    if zz is not None:
+        sz = sigmoid64(zz)
+        g = dout * zz * sz
+        dz = dout * fw["y"] * sz * (1.0 + zz * (1.0 - sz))
+    else:
+        g = dout
+        dz = None
+    mu = np.zeros((bsz, dim, n)) if dlast_state is None else _f64(dlast_state).copy()
+    du = np.zeros((bsz, dim, L))
+    ddl = np.zeros((bsz, dim, L))
+    dA = np.zeros((dim, n))
+    dB = np.zeros((bsz, n, L))
+    dC = np.zeros((bsz, n, L))
+    ckpt = fw["checkpoints"]
+    seg_starts = sorted(ckpt.keys())
+    for s0 in reversed(seg_starts):
+        s1 = min(s0 + segment, L)
+        # recompute states h_{t-1} (prev) and h_t for t in [s0, s1)
+        hs_prev = []
+        h = ckpt[s0].copy()
+        disc = []
+        for t in range(s0, s1):
+            a_bar, bu, E = _discretize(dl[:, :, t], u[:, :, t], A, B[:, :, t], zoh)
+            hs_prev.append(h)
+            h = a_bar * h + bu
+            disc.append((a_bar, E, h))
+        for i in range(s1 - s0 - 1, -1, -1):
+            t = s0 + i
+            a_bar, E, h_t = disc[i]
+            h_prev = hs_prev[i]
+            lam = C[:, None, :, t] * g[:, :, t, None] + mu  # (B, D, N)
+            dl_t = dl[:, :, t]
+            u_t = u[:, :, t]
+            B_t = B[:, None, :, t]
+            if zoh:
+                du[:, :, t] += np.sum(lam * B_t * E, axis=2)
+                ddl[:, :, t] += np.sum(lam * (A[None] * a_bar * h_prev + B_t * u_t[:, :, None] * a_bar), axis=2)
+                dEdA = (dl_t[:, :, None] * A[None] * a_bar - np.expm1(dl_t[:, :, None] * A[None])) / (A[None] ** 2)
+                dA += np.sum(lam * (dl_t[:, :, None] * a_bar * h_prev + B_t * u_t[:, :, None] * dEdA), axis=0)
+                dB[:, :, t] += np.sum(lam * E * u_t[:, :, None], axis=1)
+            else:
+                du[:, :, t] += dl_t * np.sum(lam * B_t, axis=2)
+                ddl[:, :, t] += np.sum(lam * (A[None] * a_bar * h_prev), axis=2) + u_t * np.sum(lam * B_t, axis=2)
+                dA += np.sum(lam * dl_t[:, :, None] * a_bar * h_prev, axis=0)
+                dB[:, :, t] += np.sum(lam * (dl_t * u_t)[:, :, None], axis=1)
+            dC[:, :, t] += np.sum(g[:, :, t, None] * h_t, axis=1)
+            mu = a_bar * lam
+    dinit = mu  # a_bar_0 * lambda_0
+    dD = None
+    if Dv is not None:
+        du += Dv[None, :, None] * g
+        dD = np.sum(g * u, axis=(0, 2))
+    if delta_softplus:
+        dx = np.where(x > SOFTPLUS_THRESHOLD, ddl, ddl * sigmoid64(x))
+    else:
+        dx = ddl
+    dx = dx * mask[:, None, :]
+    du = du * mask[:, None, :]
+    if dz is not None:
+        dz = dz * mask[:, None, :]
+    ddelta_bias = None if delta_bias is None else np.sum(dx, axis=(0, 2))
+    return dict(du=du, ddelta=dx, dA=dA, dB=dB, dC=dC, dD=dD, dz=dz,
+                ddelta_bias=ddelta_bias, dinitial_state=dinit)
+
+
+def reference_api_forward(A, deltas, Bs, Cs, u, initial_x=None, use_euler_barB_approx=True):
+    """The reference's public contract (``mamba/selective_scan_cuda.py:262-308``) in its
+    logical layout: deltas/u (B, L, D), Bs/Cs (B, L, N) -> y (B, L, D), final_x (B, D, N),
+    chunk_states (B, D, ceil(L/2048), N, 2) as the reference's forward FFI returns."""
+    tr = lambda a: np.ascontiguousarray(np.swapaxes(_f64(a), 1, 2))
+    res = forward(tr(u), tr(deltas), A, tr(Bs), tr(Cs), initial_state=initial_x,
+                  discretization="euler" if use_euler_barB_approx else "zoh")
+    return np.swapaxes(res["y"], 1, 2), res["last_state"], res["ref_chunk_states"]
+
+
+def reference_api_backward(A, deltas, Bs, Cs, u, initial_x, dy, dfinal_x, use_euler_barB_approx=True):
+    """Cotangents -> (dA, ddeltas, dBs, dCs, du, dinitial_x) in the reference's layout, as
+    ``_selective_scan_bwd_ffi`` returns them (``mamba/selective_scan_cuda.py:163-214``)."""
+    tr = lambda a: np.ascontiguousarray(np.swapaxes(_f64(a), 1, 2))
+    g = backward(tr(u), tr(deltas), A, tr(Bs), tr(Cs), tr(dy), initial_state=initial_x,
+                 dlast_state=dfinal_x, discretization="euler" if use_euler_barB_approx else "zoh")
+    sw = lambda a: np.swapaxes(a, 1, 2)
+    return g["dA"], sw(g["ddelta"]), sw(g["dB"]), sw(g["dC"]), sw(g["du"]), g["dinitial_state"]

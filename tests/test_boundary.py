@@ -1,0 +1,196 @@
+"""C-ABI and host-API checks that need no GPU.
+
+* the library loads and exports every function declared in include/*.h;
+* every validation error is returned before any HIP call (reference error contract:
+  native/selective_scan_cuda.cu:400-440, native/selective_scan_bwd.cu:45-79,
+  mamba/selective_scan_cuda.py:35-40, 93-121);
+* the Python API raises the reference's exception types, and refuses CPU tensors
+  instead of falling back to a CPU path.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from mamba_amd import _lib
+from mamba_amd.configs import C2, algorithmic_bytes, round_to_bf16
+from mamba_amd.selective_scan_hip import selective_scan, selective_scan_fn
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_functions():
+    names = []
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(mss_[a-z_0-9]+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.register_hip_kernel()
+
+
+def test_header_declares_expected_symbols():
+    assert set(header_functions()) == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_header_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert lib.mss_abi_version() == 1
+
+
+def test_missing_library_raises_file_not_found(tmp_path):
+    saved = _lib._LIBRARY
+    try:
+        _lib._LIBRARY = None
+        with pytest.raises(FileNotFoundError, match="not built"):
+            _lib.register_hip_kernel(tmp_path / "nope.so")
+    finally:
+        _lib._LIBRARY = saved
+
+
+def fwd_args(**kw):
+    base = dict(batch=2, dim=3, seqlen=10, dstate=4, u=1, delta=1, A=1, B=1, C=1, out=1)
+    base.update(kw)
+    return _lib.FwdArgs(**base)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(batch=0), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(dim=-1), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(seqlen=0), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(dstate=0), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(dstate=257), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(dstate=17), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(discretization=2), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(delta_softplus=3), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(io_dtype=7), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(bc_dtype=-1), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(u=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(out=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+])
+def test_fwd_validation(lib, kw, status):
+    assert lib.mss_fwd(fwd_args(**kw), None) == status
+
+
+def test_null_args(lib):
+    assert lib.mss_fwd(None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_bwd(None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_bwd_workspace_bytes(None) == 0
+
+
+def bwd_args(**kw):
+    base = dict(batch=2, dim=3, seqlen=10, dstate=4, u=1, delta=1, A=1, B=1, C=1, carries=1, dout=1,
+                du=1, ddelta=1, dA=1, dB=1, dC=1)
+    base.update(kw)
+    return _lib.BwdArgs(**base)
+
+
+@pytest.mark.parametrize("kw", [
+    dict(carries=None), dict(dout=None), dict(dB=None), dict(D=1), dict(z=1), dict(delta_bias=1),
+    dict(seqlen=0), dict(discretization=5),
+])
+def test_bwd_validation(lib, kw):
+    assert lib.mss_bwd(bwd_args(**kw), None) == _lib.MSS_ERR_INVALID_ARGUMENT
+
+
+def test_bwd_workspace_too_small(lib):
+    a = bwd_args(workspace=1, workspace_bytes=16)
+    assert lib.mss_bwd(a, None) == _lib.MSS_ERR_WORKSPACE
+
+
+def test_workspace_size_depends_on_shapes_only(lib):
+    a = bwd_args(batch=4, dim=1536, seqlen=2048, dstate=16)
+    n1 = lib.mss_bwd_workspace_bytes(a)
+    assert n1 == lib.mss_bwd_workspace_bytes(a) > 0
+    # dB/dC partials: at most one per 8-channel octet, at least one per batch row
+    assert n1 >= 4 * 2 * 16 * 2048 * 4
+
+
+def test_reference_entry_points_validate(lib):
+    p = ctypes.c_void_p(1)
+    assert lib.mss_scan_fwd(None, 0, 0, 10, 3, 4, *[p] * 9) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_scan_fwd(None, 2, 1, 10, 3, 4, *[p] * 9) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_scan_fwd(None, 0, 1, 10, 3, 4, *[p] * 8, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_scan_fwd_repeat(None, 0, 0, 1, 10, 3, 4, *[p] * 9) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_scan_bwd(None, 1, 10, 3, 32, *[p] * 15) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_scan_bwd(None, 1, 10, 3, 4, *[p] * 14, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+
+
+def test_strerror(lib):
+    assert lib.mss_strerror(0) == b"ok"
+    assert b"invalid" in lib.mss_strerror(1)
+    assert lib.mss_strerror(99) == b"unknown status"
+
+
+# ------------------------------------------------------------------ Python API errors
+def ref_inputs(dtype=torch.float32, b=2, l=17, d=8, n=16):
+    g = torch.Generator().manual_seed(7)
+    A = -torch.exp(torch.randn(d, n, generator=g))
+    return (A.to(dtype), torch.randn(b, l, d, generator=g).to(dtype), torch.randn(b, l, n, generator=g).to(dtype),
+            torch.randn(b, l, n, generator=g).to(dtype), torch.randn(b, l, d, generator=g).to(dtype),
+            torch.randn(b, d, n, generator=g).to(dtype))
+
+
+def test_reference_api_rejects_non_float32():
+    with pytest.raises(TypeError, match="float32"):
+        selective_scan(*ref_inputs(torch.float64))
+
+
+@pytest.mark.parametrize("n", [3, 32])
+def test_reference_api_rejects_state_size(n):
+    args = ref_inputs(n=n)
+    with pytest.raises(ValueError, match="N must be one of"):
+        selective_scan(*args)
+
+
+def test_reference_api_rejects_zero_length_and_shapes():
+    A, d, B, C, u, x0 = ref_inputs()
+    with pytest.raises(ValueError, match="positive"):
+        selective_scan(A, d[:, :0], B[:, :0], C[:, :0], u[:, :0], x0)
+    with pytest.raises(ValueError, match="Bs must have shape"):
+        selective_scan(A, d, B[:, :5], C, u, x0)
+    with pytest.raises(ValueError, match="initial_x must have shape"):
+        selective_scan(A, d, B, C, u, x0[:1])
+
+
+def test_no_cpu_fallback():
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        selective_scan(*ref_inputs())
+    u = torch.randn(1, 2, 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        selective_scan_fn(u, u, -torch.ones(2, 4), torch.randn(1, 4, 8), torch.randn(1, 4, 8))
+
+
+def test_fused_api_validation():
+    u = torch.randn(1, 2, 8)
+    A = -torch.ones(2, 4)
+    Bm = torch.randn(1, 4, 8)
+    with pytest.raises(TypeError):
+        selective_scan_fn(u, u.double(), A, Bm, Bm)
+    with pytest.raises(ValueError, match="N must be"):
+        selective_scan_fn(u, u, -torch.ones(2, 17), torch.randn(1, 17, 8), torch.randn(1, 17, 8))
+    with pytest.raises(ValueError, match="discretization"):
+        selective_scan_fn(u, u, A, Bm, Bm, discretization="rk4")
+    with pytest.raises(TypeError, match="float32"):
+        selective_scan_fn(u, u, A.double(), Bm, Bm)
+    with pytest.raises(ValueError, match="seq_lens"):
+        selective_scan_fn(u, u, A, Bm, Bm, seq_lens=torch.tensor([3]))
+
+
+def test_algorithmic_bytes_match_baseline_table():
+    fwd, bwd = algorithmic_bytes(C2)
+    assert abs(fwd / 1e6 - 202.9) < 0.1 and abs(bwd / 1e6 - 355.0) < 0.1
+
+
+def test_bf16_rounding_matches_torch():
+    x = np.random.default_rng(0).standard_normal(10000).astype(np.float32)
+    ours = round_to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(ours, ref)

@@ -1,0 +1,288 @@
+"""GPU parity: HIP kernels (through the C ABI) vs the float64 oracle on identical inputs.
+
+Bars (stated by the build target): float32 within rtol 1e-4 / atol 1e-5; bfloat16
+inputs with float32 accumulation within rtol 2e-2. Cases follow the reference tests
+(tests/test_selective_scan_cuda.py: lengths {1, 17, 128, 513} forward, {1, 31, 513, 2051}
+VJP, ZOH VJP at 31, reference input recipe) and extend them to the fused extras,
+multi-chunk lengths, ragged tails, variable lengths, bf16 and the full config-2 shape.
+"""
+import ctypes
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mamba_amd import _lib
+from mamba_amd.configs import C2, C3, C4, ScanConfig, make_scan_inputs
+from mamba_amd.selective_scan_hip import selective_scan, selective_scan_fn
+from oracle import scan64
+
+pytestmark = pytest.mark.gpu
+
+F32_RTOL, F32_ATOL = 1e-4, 1e-5
+BF16_RTOL = 2e-2
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def close(name, got, ref, rtol=F32_RTOL, atol=F32_ATOL):
+    got = got.detach().float().cpu().numpy() if torch.is_tensor(got) else np.asarray(got)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    worst = np.argmax(err - bound)
+    ok = bool(np.all(err <= bound))
+    log(f"  {name:16s} max_abs={err.max():.3e} max_rel={(err / np.maximum(np.abs(ref), 1e-30)).max():.3e} "
+        f"worst(got={got.flat[worst]:.6e}, ref={ref.flat[worst]:.6e}) ok={ok}")
+    assert ok, f"{name}: {np.sum(err > bound)} of {err.size} elements outside rtol={rtol}, atol={atol}"
+
+
+dev = "cuda"
+
+
+def T(a, dtype=torch.float32):
+    return torch.as_tensor(np.ascontiguousarray(a)).to(dev, dtype)
+
+
+def ref_recipe(seed, batch=2, length=17, dim=8, n=16):
+    rng = np.random.default_rng(seed)
+    A = -np.exp(rng.standard_normal((dim, n)))
+    deltas = np.log1p(np.exp(rng.standard_normal((batch, length, dim))))
+    Bs = rng.standard_normal((batch, length, n))
+    Cs = rng.standard_normal((batch, length, n))
+    u = rng.standard_normal((batch, length, dim))
+    x0 = rng.standard_normal((batch, dim, n))
+    return [a.astype(np.float32) for a in (A, deltas, Bs, Cs, u, x0)]
+
+
+@pytest.mark.parametrize("length", [1, 17, 128, 513, 2051, 4100])
+@pytest.mark.parametrize("euler", [True, False])
+def test_reference_api_forward(length, euler):
+    log(f"case forward L={length} euler={euler}")
+    args = ref_recipe(7, length=length)
+    y, fin = selective_scan(*[T(a) for a in args], use_euler_barB_approx=euler)
+    torch.cuda.synchronize()
+    ey, efin, _ = scan64.reference_api_forward(*args, use_euler_barB_approx=euler)
+    close("y", y, ey)
+    close("final_x", fin, efin)
+
+
+@pytest.mark.parametrize("length", [1, 31, 513, 2051])
+@pytest.mark.parametrize("euler", [True, False])
+def test_reference_api_vjp(length, euler):
+    log(f"case vjp L={length} euler={euler}")
+    args = ref_recipe(11, batch=1, length=length, dim=4, n=8)
+    ts = [T(a).requires_grad_(True) for a in args]
+    y, fin = selective_scan(*ts, use_euler_barB_approx=euler)
+    loss = (y ** 2).mean() + (fin ** 2).mean()
+    loss.backward()
+    torch.cuda.synchronize()
+    ey, efin, _ = scan64.reference_api_forward(*args, use_euler_barB_approx=euler)
+    dy = 2 * ey / ey.size
+    dfin = 2 * efin / efin.size
+    grads = scan64.reference_api_backward(*args, dy, dfin, use_euler_barB_approx=euler)
+    for name, t, g in zip(["dA", "ddeltas", "dBs", "dCs", "du", "dinitial_x"], ts, grads):
+        close(name, t.grad, g)
+
+
+def fused_case(seed, b, d, l, n, dtype="f32", lens=None, zoh=False, extras=True):
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    x = dict(u=rng.standard_normal((b, d, l)).astype(f), delta=rng.standard_normal((b, d, l)).astype(f),
+             A=(-np.exp(rng.standard_normal((d, n)))).astype(f), B=rng.standard_normal((b, n, l)).astype(f),
+             C=rng.standard_normal((b, n, l)).astype(f))
+    if extras:
+        x.update(D=rng.standard_normal(d).astype(f), z=rng.standard_normal((b, d, l)).astype(f),
+                 delta_bias=(0.5 * rng.standard_normal(d) - 2.0).astype(f),
+                 initial_state=rng.standard_normal((b, d, n)).astype(f))
+    dout = rng.standard_normal((b, d, l)).astype(f)
+    dlast = rng.standard_normal((b, d, n)).astype(f)
+    if dtype == "bf16":
+        from mamba_amd.configs import round_to_bf16
+        for k in ("u", "delta", "B", "C", "z"):
+            if k in x:
+                x[k] = round_to_bf16(x[k])
+        dout = round_to_bf16(dout)
+    if lens is not None:
+        x["seq_lens"] = np.asarray(lens, np.int32)
+    return x, dout, dlast
+
+
+def run_fused(x, dout, dlast, dtype, zoh, softplus=True):
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    io = {"u", "delta", "z", "B", "C"}
+    ts = {}
+    for k, v in x.items():
+        if k == "seq_lens":
+            ts[k] = torch.as_tensor(v).to(dev)
+        else:
+            ts[k] = T(v, tdt if k in io else torch.float32).requires_grad_(True)
+    out, last = selective_scan_fn(ts["u"], ts["delta"], ts["A"], ts["B"], ts["C"], D=ts.get("D"), z=ts.get("z"),
+                                  delta_bias=ts.get("delta_bias"), delta_softplus=softplus,
+                                  return_last_state=True, initial_state=ts.get("initial_state"),
+                                  seq_lens=ts.get("seq_lens"), discretization="zoh" if zoh else "euler")
+    (out.float() * T(dout)).sum().add_((last * T(dlast)).sum()).backward()
+    torch.cuda.synchronize()
+    return ts, out, last
+
+
+def oracle_fused(x, dout, dlast, zoh, softplus=True):
+    kw = dict(D=x.get("D"), z=x.get("z"), delta_bias=x.get("delta_bias"), delta_softplus=softplus,
+              initial_state=x.get("initial_state"), seq_lens=x.get("seq_lens"),
+              discretization="zoh" if zoh else "euler")
+    fw = scan64.forward(x["u"], x["delta"], x["A"], x["B"], x["C"], **kw)
+    g = scan64.backward(x["u"], x["delta"], x["A"], x["B"], x["C"], dout, dlast_state=dlast, **kw)
+    return fw, g
+
+
+GRAD_OF = {"u": "du", "delta": "ddelta", "A": "dA", "B": "dB", "C": "dC", "D": "dD", "z": "dz",
+           "delta_bias": "ddelta_bias", "initial_state": "dinitial_state"}
+
+
+def check_fused(ts, out, last, fw, g, rtol=F32_RTOL, atol=F32_ATOL):
+    close("out", out, fw["out"], rtol, atol)
+    close("last_state", last, fw["last_state"], rtol, atol)
+    for k, gname in GRAD_OF.items():
+        if k in ts:
+            close(gname, ts[k].grad, g[gname], rtol, atol)
+
+
+@pytest.mark.parametrize("l", [1, 7, 250, 1024, 1500, 3000])
+@pytest.mark.parametrize("n", [1, 4, 16])
+def test_fused_fp32(l, n):
+    log(f"case fused fp32 L={l} N={n}")
+    x, dout, dlast = fused_case(100 + l + n, 2, 24, l, n)
+    ts, out, last = run_fused(x, dout, dlast, "f32", False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    check_fused(ts, out, last, fw, g)
+
+
+@pytest.mark.parametrize("l", [5, 300, 2100])
+def test_fused_zoh(l):
+    log(f"case fused zoh L={l}")
+    x, dout, dlast = fused_case(200 + l, 2, 16, l, 8, zoh=True)
+    ts, out, last = run_fused(x, dout, dlast, "f32", True)
+    fw, g = oracle_fused(x, dout, dlast, True)
+    check_fused(ts, out, last, fw, g)
+
+
+def test_fused_no_extras_no_softplus():
+    log("case fused, no extras, raw positive delta")
+    x, dout, dlast = fused_case(300, 2, 16, 700, 16, extras=False)
+    x["delta"] = np.abs(x["delta"]) * 0.1
+    ts, out, last = run_fused(x, dout, dlast, "f32", False, softplus=False)
+    fw, g = oracle_fused(x, dout, dlast, False, softplus=False)
+    check_fused(ts, out, last, fw, g)
+
+
+@pytest.mark.parametrize("lens", [[3000, 1025, 1, 0], [512, 2047, 2048, 2049]])
+def test_varlen_fp32(lens):
+    log(f"case varlen lens={lens}")
+    x, dout, dlast = fused_case(400, 4, 16, 3000, 16, lens=lens)
+    # garbage beyond each row's length must not leak
+    ts, out, last = run_fused(x, dout, dlast, "f32", False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    check_fused(ts, out, last, fw, g)
+
+
+@pytest.mark.parametrize("l", [64, 1000, 2056])
+def test_bf16(l):
+    log(f"case bf16 L={l}")
+    x, dout, dlast = fused_case(500 + l, 2, 32, l, 16, dtype="bf16")
+    ts, out, last = run_fused(x, dout, dlast, "bf16", False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    # bf16 outputs are rounded once; fp32 accumulation inside.
+    check_fused(ts, out, last, fw, g, rtol=BF16_RTOL, atol=BF16_RTOL * 0.05)
+
+
+def test_deterministic_rerun():
+    log("case determinism")
+    x, dout, dlast = fused_case(600, 2, 64, 1500, 16)
+    a = run_fused(x, dout, dlast, "f32", False)
+    b = run_fused(x, dout, dlast, "f32", False)
+    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    for k in ("u", "delta", "z", "A", "D", "delta_bias", "initial_state"):
+        assert torch.equal(a[0][k].grad, b[0][k].grad), k
+    for k in ("B", "C"):  # LDS float atomics: order may differ in the last bits
+        torch.testing.assert_close(a[0][k].grad, b[0][k].grad, rtol=1e-5, atol=1e-6)
+
+
+def test_reference_c_entry_points():
+    """mss_scan_fwd / mss_scan_bwd (the reference FFI handlers' counterparts) via ctypes."""
+    log("case reference C entry points")
+    lib = _lib.register_hip_kernel()
+    A, deltas, Bs, Cs, u, x0 = ref_recipe(13, batch=2, length=2500, dim=8, n=16)
+    b, l, d = u.shape
+    n = A.shape[1]
+    tr = lambda a: T(np.swapaxes(a, 1, 2))  # physical [B][D][L] / [B][N][L]
+    tA, td, tB, tC, tu, tx0 = T(A), tr(deltas), tr(Bs), tr(Cs), tr(u), T(x0)
+    y = torch.empty(b, d, l, device=dev)
+    fin = torch.empty(b, d, n, device=dev)
+    cs = torch.empty(b, d, 2, n, 2, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    _lib.check(lib.mss_scan_fwd(st, 0, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu), P(tx0), P(y), P(fin), P(cs)),
+               "mss_scan_fwd")
+    rng = np.random.default_rng(14)
+    dy = rng.standard_normal((b, l, d)).astype(np.float32)
+    dfin = rng.standard_normal((b, d, n)).astype(np.float32)
+    outs = [torch.empty_like(t) for t in (tA, td, tB, tC, tu, tx0)]
+    _lib.check(lib.mss_scan_bwd(st, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu), P(tx0), P(cs), P(tr(dy)),
+                                P(T(dfin)), *[P(o) for o in outs]), "mss_scan_bwd")
+    torch.cuda.synchronize()
+    ey, efin, ecs = scan64.reference_api_forward(A, deltas, Bs, Cs, u, x0)
+    close("y", y.transpose(1, 2), ey)
+    close("final_x", fin, efin)
+    close("chunk_states", cs, ecs)
+    grads = scan64.reference_api_backward(A, deltas, Bs, Cs, u, x0, dy, dfin)
+    names = ["dA", "ddeltas", "dB", "dC", "du", "dinitial_x"]
+    for name, o, g in zip(names, outs, grads):
+        got = o if o.shape == g.shape else o.transpose(1, 2)
+        close(name, got, g)
+
+
+def config_tensors(cfg, x, dout):
+    tdt = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
+    ts = {}
+    for k, v in x.items():
+        if k == "seq_lens":
+            ts[k] = torch.as_tensor(v).to(dev)
+        else:
+            ts[k] = T(v, tdt if k in ("u", "delta", "z", "B", "C") else torch.float32).requires_grad_(True)
+    return ts
+
+
+@pytest.mark.slow
+def test_config2_full_size():
+    """Config 2 at its full shape, every output and gradient against the oracle."""
+    log("case c2 full size")
+    x = make_scan_inputs(C2, seed=0, with_z=True, with_dout=True)
+    dout = x.pop("dout")
+    dlast = np.random.default_rng(1).standard_normal((C2.batch, C2.dim, C2.dstate)).astype(np.float32)
+    ts, out, last = run_fused(x, dout, dlast, "f32", False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    check_fused(ts, out, last, fw, g)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("cfg", [C3, C4], ids=["c3", "c4"])
+def test_large_config_channel_slice(cfg):
+    """Full L and B of configs 3/4 on a slice of 32 channels (channels are independent;
+    dB/dC of the slice are the slice's own sums)."""
+    log(f"case {cfg.name} channel slice")
+    sl = ScanConfig(cfg.name + "_slice", cfg.batch, 32, cfg.length, cfg.dstate, cfg.dtype, cfg.varlen)
+    x = make_scan_inputs(sl, seed=0, with_z=True, with_dout=True)
+    dout = x.pop("dout")
+    dlast = np.zeros((sl.batch, sl.dim, sl.dstate), np.float32)
+    ts, out, last = run_fused(x, dout, dlast, cfg.dtype, False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    if cfg.dtype == "bf16":
+        check_fused(ts, out, last, fw, g, rtol=BF16_RTOL, atol=BF16_RTOL * 0.05)
+    else:
+        check_fused(ts, out, last, fw, g)
