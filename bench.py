@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X selective scan: config 2 forward + backward on one GPU.
+
+Step = one forward (mss_fwd) and one backward (mss_bwd_scan + mss_bwd_reduce) pass of the
+fused scan over the config-2 batch (fp32, B=4, D=1536, L=2048, N=16; softplus(delta +
+bias), D skip, silu(z) gate, last state), inputs resident in HBM, seeded synthetic data.
+Timing: HIP events recorded on the stream the kernels run on (torch's current stream,
+which the C ABI launches on), W untimed warmup steps, then exactly K timed steps
+bracketed by device synchronisation. Prints ONE JSON line on stdout; progress to stderr.
+
+Fields beyond the driver contract:
+  roofline      dominant kernel: algorithmic bytes / its average event-timed duration
+                vs the 8 TB/s HBM peak; `traffic` = measured HBM bytes per launch from
+                the rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/ (or null)
+  cpu_baseline  torch-CPU restatement of the reference's pure-JAX scan path
+                (oracle/assoc_torch.py) timed on this host on a channel slice
+  fwd_bwd_hbm_frac  (fwd + bwd algorithmic bytes) / step time / 8 TB/s
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "jax-mambas_amd"))
+
+METRIC = "selective_scan fwd+bwd ms & % HBM roofline; Mamba-1 130M train tokens/s"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def read_traffic(kernel_tag):
+    """HBM bytes per launch from profiles/<kernel_tag>_traffic.txt (key=value lines)."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    kv = {}
+    for line in open(path):
+        m = re.match(r"\s*([a-z_]+)\s*=\s*([0-9.eE+-]+)\s*$", line)
+        if m:
+            kv[m.group(1)] = float(m.group(2))
+    if "hbm_bytes_per_launch" in kv:
+        return kv["hbm_bytes_per_launch"]
+    return None
+
+
+def gpu_step_setup(torch, cfg):
+    from mamba_amd import _lib
+    from mamba_amd.configs import make_scan_inputs
+
+    lib = _lib.register_hip_kernel()
+    x = make_scan_inputs(cfg, seed=0, with_z=True, with_dout=True)
+    dev = "cuda"
+    t = {k: torch.from_numpy(v).to(dev) for k, v in x.items()}
+    b, d, l, n = cfg.batch, cfg.dim, cfg.length, cfg.dstate
+    n_carry = (l + _lib.MSS_CARRY_CHUNK - 1) // _lib.MSS_CARRY_CHUNK
+    t["out"] = torch.empty_like(t["u"])
+    t["last"] = torch.empty(b, d, n, device=dev)
+    t["carries"] = torch.empty(b, d, n_carry, n, device=dev)
+    t["dlast"] = torch.zeros(b, d, n, device=dev)
+    for k in ("u", "delta", "z"):
+        t["d" + k] = torch.empty_like(t[k])
+    for k in ("A", "B", "C", "D", "delta_bias"):
+        t["d" + k] = torch.empty_like(t[k])
+    P = lambda k: t[k].data_ptr()
+    fa = _lib.FwdArgs(batch=b, dim=d, seqlen=l, dstate=n, discretization=_lib.MSS_EULER, delta_softplus=1,
+                      io_dtype=_lib.MSS_F32, bc_dtype=_lib.MSS_F32, u=P("u"), delta=P("delta"), A=P("A"),
+                      B=P("B"), C=P("C"), D=P("D"), z=P("z"), delta_bias=P("delta_bias"),
+                      out=P("out"), last_state=P("last"), carries=P("carries"))
+    ba = _lib.BwdArgs(batch=b, dim=d, seqlen=l, dstate=n, discretization=_lib.MSS_EULER, delta_softplus=1,
+                      io_dtype=_lib.MSS_F32, bc_dtype=_lib.MSS_F32, u=P("u"), delta=P("delta"), A=P("A"),
+                      B=P("B"), C=P("C"), D=P("D"), z=P("z"), delta_bias=P("delta_bias"),
+                      carries=P("carries"), dout=P("dout"), dlast_state=P("dlast"), du=P("du"),
+                      ddelta=P("ddelta"), dA=P("dA"), dB=P("dB"), dC=P("dC"), dD=P("dD"), dz=P("dz"),
+                      ddelta_bias=P("ddelta_bias"))
+    ws_bytes = int(lib.mss_bwd_workspace_bytes(ba))
+    t["ws"] = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    ba.workspace = t["ws"].data_ptr()
+    ba.workspace_bytes = ws_bytes
+    return lib, t, fa, ba
+
+
+def run_gpu(torch, cfg, steps, warmup):
+    from mamba_amd import _lib
+
+    lib, t, fa, ba = gpu_step_setup(torch, cfg)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(evs=None):
+        if evs:
+            evs[0].record(stream)
+        _lib.check(lib.mss_fwd(fa, sp), "mss_fwd")
+        if evs:
+            evs[1].record(stream)
+        _lib.check(lib.mss_bwd_scan(ba, sp), "mss_bwd_scan")
+        if evs:
+            evs[2].record(stream)
+        _lib.check(lib.mss_bwd_reduce(ba, sp), "mss_bwd_reduce")
+        if evs:
+            evs[3].record(stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done ({warmup} steps)")
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        step(evs[i])
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    fwd = [e[0].elapsed_time(e[1]) for e in evs]
+    bws = [e[1].elapsed_time(e[2]) for e in evs]
+    red = [e[2].elapsed_time(e[3]) for e in evs]
+    log(f"[bench] timed {steps} steps: {total_ms / steps:.4f} ms/step "
+        f"(fwd {np.mean(fwd):.4f}, bwd_scan {np.mean(bws):.4f}, bwd_reduce {np.mean(red):.4f} ms)")
+    return total_ms / steps, float(np.mean(fwd)), float(np.mean(bws)), float(np.mean(red))
+
+
+def cpu_baseline(torch, cfg, target_s):
+    """Reference composition on the CPU: softplus(delta + bias) -> pure-JAX-style scan
+    (oracle/assoc_torch.py, mamba/selective_scan_cuda.py:56-90) -> + D*u -> * silu(z);
+    loss-weighted backward through autograd. Timed on a slice of channels (channels are
+    independent) and scaled to the full channel count."""
+    from mamba_amd.configs import make_scan_inputs, ScanConfig
+    from oracle.assoc_torch import selective_scan_reference
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+
+    def run(dslice):
+        sub = ScanConfig("slice", cfg.batch, dslice, cfg.length, cfg.dstate, "f32")
+        x = make_scan_inputs(sub, seed=0, with_z=True, with_dout=True)
+        tr = lambda a: torch.from_numpy(np.ascontiguousarray(np.swapaxes(a, 1, 2)))
+        u, dr, z, dout = (tr(x[k]) for k in ("u", "delta", "z", "dout"))
+        Bs, Cs = tr(x["B"]), tr(x["C"])
+        A = torch.from_numpy(x["A"]).requires_grad_(True)
+        bias = torch.from_numpy(x["delta_bias"]).requires_grad_(True)
+        D = torch.from_numpy(x["D"]).requires_grad_(True)
+        for v in (u, dr, z, Bs, Cs):
+            v.requires_grad_(True)
+        t0 = time.perf_counter()
+        deltas = torch.nn.functional.softplus(dr + bias)
+        y, last = selective_scan_reference(A, deltas, Bs, Cs, u)
+        out = (y + D * u) * torch.nn.functional.silu(z)
+        loss = (out * dout).sum() + last.sum() * 0.0
+        loss.backward()
+        return time.perf_counter() - t0
+
+    d0 = 32
+    run(d0)
+    t_probe = run(d0)
+    dslice = int(np.clip(d0 * (target_s / 4.0) / max(t_probe, 1e-3), d0, cfg.dim)) // 8 * 8
+    log(f"[bench] cpu baseline probe D={d0}: {t_probe:.2f} s; timing slice D={dslice} x3 on {threads} threads")
+    run(dslice)
+    times = []
+    for i in range(3):
+        times.append(run(dslice))
+        log(f"[bench] cpu baseline rep {i}: {times[-1]:.2f} s")
+    t_med = float(np.median(times))
+    t_full = t_med * cfg.dim / dslice
+    tokens = cfg.batch * cfg.length
+    return {
+        "value": tokens / t_full,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"B={cfg.batch} L={cfg.length} N={cfg.dstate} fp32, {dslice} of {cfg.dim} channels, "
+                   f"fwd+bwd (autograd) median of 3 = {t_med:.3f} s, scaled x{cfg.dim / dslice:.1f} "
+                   f"to all channels ({t_full:.2f} s per step)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="approximate CPU work for the CPU baseline (0 disables it)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "this build has no multi-GPU path.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from mamba_amd.configs import C2, algorithmic_bytes
+
+    cfg = C2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    ms, fwd_ms, bwd_ms, red_ms = run_gpu(torch, cfg, args.steps, args.warmup)
+    fwd_bytes, bwd_bytes = algorithmic_bytes(cfg)
+    tokens = cfg.batch * cfg.length
+    # Dominant kernel: the backward scan (backward algorithmic bytes attributed to it; the
+    # reduction kernels that finish dB/dC/dA/dD/dbias are timed separately).
+    if bwd_ms >= fwd_ms:
+        tag, bytes_, dur = "bwd_scan_c2", bwd_bytes, bwd_ms
+    else:
+        tag, bytes_, dur = "fwd_c2", fwd_bytes, fwd_ms
+    achieved = bytes_ / (dur * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(tag),
+                "kernel": tag, "algorithmic_bytes": bytes_, "avg_launch_ms": round(dur, 5)}
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(torch, cfg, args.cpu_seconds)
+    step_bytes = fwd_bytes + bwd_bytes
+    result = {
+        "metric": METRIC,
+        "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "c2: selective_scan fwd+bwd fp32, softplus(delta+bias), D skip, silu(z) gate, "
+                               "last state", "batch": cfg.batch, "dim": cfg.dim, "seq_len": cfg.length,
+                   "dstate": cfg.dstate, "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "fwd_bwd_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernels_ms": {"fwd": round(fwd_ms, 5), "bwd_scan": round(bwd_ms, 5), "bwd_reduce": round(red_ms, 5)},
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -121,6 +121,15 @@ size_t mss_bwd_workspace_bytes(const mss_bwd_args* args);
 int mss_fwd(const mss_fwd_args* args, void* stream);
 int mss_bwd(const mss_bwd_args* args, void* stream);
 
+/* mss_bwd in two stream-ordered phases sharing a caller-provided workspace (NULL ->
+ * MSS_ERR_WORKSPACE): mss_bwd_scan writes du/ddelta/dz/dinitial_state and per-block
+ * partial sums of dA/dB/dC/dD/ddelta_bias into the workspace; mss_bwd_reduce sums the
+ * partials in a fixed order into dA/dB/dC/dD/ddelta_bias. mss_bwd == scan then reduce.
+ * (The reference backward, native/selective_scan_bwd.cu:166-190, is one call; the split
+ * lets a caller time or defer the cross-channel reduction.) */
+int mss_bwd_scan(const mss_bwd_args* args, void* stream);
+int mss_bwd_reduce(const mss_bwd_args* args, void* stream);
+
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------
  * Same argument order, attribute meaning and buffer shapes as the reference's XLA-FFI
  * handlers; physical layouts as listed at the top of this file. */

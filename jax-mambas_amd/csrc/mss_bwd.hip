@@ -32,14 +32,17 @@ template <int kT, int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
 __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   constexpr int kChunk = 64 * kT;
   static_assert(kChunk == kCarryChunk, "backward chunk must match the carry residual");
-  constexpr int kStride = kT + 4;
-  __shared__ __attribute__((aligned(16))) float sB[64 * kStride];
-  __shared__ __attribute__((aligned(16))) float sC[64 * kStride];
-  __shared__ float acc[2 * kMaxN * kChunk];  // [which][n][j*64 + (lane ^ j)]
+  // dB/dC partial sums of the workgroup's channels for one chunk: [copy][which][n][slot],
+  // slot = j*64 + (lane ^ j). At state iteration i wave w owns row n = (i + w) mod N of
+  // copy w / N, so rows are updated with plain read-add-write in a fixed order
+  // (LDS float atomics run ~40x slower than stores on gfx950 and are avoided).
+  __shared__ float acc[2 * kMaxN * kChunk];
   __shared__ float s_mu[kMaxChanPerBlock][kMaxN];
   __shared__ float s_dA[kMaxChanPerBlock][kMaxN];
   __shared__ float s_dD[kMaxChanPerBlock];
   __shared__ float s_db[kMaxChanPerBlock];
+  __shared__ float s_a[kW][kMaxN];
+  __shared__ float s_h0[kW][kMaxN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -55,6 +58,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + static_cast<size_t>(b) * N * L;
   const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + static_cast<size_t>(b) * N * L;
 
+  const int n_copy = (kW + N - 1) / N;  // n_copy * N <= 2 * kMaxN for N <= kMaxN
+  float* const acc_w = acc + (w / N) * 2 * N * kChunk;
   for (int i = tid; i < 2 * kMaxN * kChunk; i += kW * 64) acc[i] = 0.f;
   for (int k = 0; k < K; ++k) {
     const int cl = k * kW + w;
@@ -87,21 +92,25 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       io_t* __restrict__ dd_row = static_cast<io_t*>(p.ddelta) + row;
 
       if (t0 >= len) {  // whole chunk past this row's length: zero gradients, carry passes
-        if (active) {
-          float zero[kT];
+        if (!active) continue;
+        float zero[kT];
 #pragma unroll
-          for (int j = 0; j < kT; ++j) zero[j] = 0.f;
-          store_seg<kT>(du_row, tl, L, vec_io, zero);
-          store_seg<kT>(dd_row, tl, L, vec_io, zero);
-          if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, vec_io, zero);
-          if (c == 0 && p.dinit && lane < N) {
-            // len == 0: h_0 is never used, but x0 flows through identity steps to last.
-            p.dinit[chan * N + lane] = s_mu[cl][lane];
-          }
+        for (int j = 0; j < kT; ++j) zero[j] = 0.f;
+        store_seg<kT>(du_row, tl, L, vec_io, zero);
+        store_seg<kT>(dd_row, tl, L, vec_io, zero);
+        if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, vec_io, zero);
+        if (c == 0 && p.dinit && lane < N) {
+          // len == 0: x0 flows through identity steps to the last state.
+          p.dinit[chan * N + lane] = s_mu[cl][lane];
         }
         continue;
       }
 
+      if (lane < N) {
+        s_a[w][lane] = p.A[static_cast<size_t>(d) * N + lane];
+        s_h0[w][lane] = c == 0 ? (p.x0 ? p.x0[chan * N + lane] : 0.f)
+                               : p.carries[(chan * p.n_carry + (c - 1)) * N + lane];
+      }
       const float Dv = p.D ? p.D[d] : 0.f;
       const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
       float dlt[kT], dlu[kT], uu[kT], g[kT], s1[kT], s2[kT];
@@ -137,40 +146,41 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         }
       }
 
-      for (int n = 0; n < N; ++n) {
-        __syncthreads();
-        stage_row<kT>(Bb + static_cast<size_t>(n) * L, t0, L, vec_bc, sB, tid, kW * 64);
-        stage_row<kT>(Cb + static_cast<size_t>(n) * L, t0, L, vec_bc, sC, tid, kW * 64);
+      // States in a per-wave rotated order (see the accumulator above); the barrier per
+      // iteration keeps every wave inside the same iteration.
+      for (int i = 0; i < N; ++i) {
+        const int n = (i + w) % N;
         __syncthreads();
         if (!active) continue;
-        const float An = p.A[d * N + n];
+        const float An = s_a[w][n];
         const float a2 = An * kLog2e;
         float bv[kT], cv[kT], a[kT];
-        lds_read_seg<kT>(sB, lane, bv);
-        lds_read_seg<kT>(sC, lane, cv);
+        load_seg_cached<kT>(Bb + static_cast<size_t>(n) * L, tl, L, vec_bc, bv);
+        load_seg_cached<kT>(Cb + static_cast<size_t>(n) * L, tl, L, vec_bc, cv);
         // ---- forward: local aggregate, scan, re-run from the true carry-in
         float H = 0.f;
 #pragma unroll
         for (int j = 0; j < kT; ++j) {
           a[j] = fast_exp2(dlt[j] * a2);
-          const float bu = kZOH ? (expm1f(dlt[j] * An) / An) * bv[j] * uu[j] : dlu[j] * bv[j];
+          const float bu = kZOH ? (expm1f(dlt[j] * An) * fast_rcp(An)) * bv[j] * uu[j] : dlu[j] * bv[j];
           H = __builtin_fmaf(a[j], H, bu);
         }
         const float pseg = fast_exp2(a2 * ssum);
         float P = pseg;
         wave_scan_affine_fwd(P, H);
-        const float run = c == 0 ? (p.x0 ? p.x0[chan * N + n] : 0.f)
-                                 : p.carries[(chan * p.n_carry + (c - 1)) * N + n];
+        const float run = s_h0[w][n];
         const float hend = __builtin_fmaf(P, run, H);
-        float h = dpp_mov<kWaveShr1, 0xF>(run, hend);
-        float ah[kT], hh[kT];
+        const float hin = dpp_mov<kWaveShr1, 0xF>(run, hend);  // state before the lane's first step
+        float hh[kT];
+        {
+          float h = hin;
 #pragma unroll
-        for (int j = 0; j < kT; ++j) {
-          const float bu = kZOH ? (expm1f(dlt[j] * An) / An) * bv[j] * uu[j] : dlu[j] * bv[j];
-          ah[j] = a[j] * h;
-          h = ah[j] + bu;
-          hh[j] = h;
-          if constexpr (kHasZ) y[j] = __builtin_fmaf(cv[j], h, y[j]);
+          for (int j = 0; j < kT; ++j) {
+            const float bu = kZOH ? (expm1f(dlt[j] * An) * fast_rcp(An)) * bv[j] * uu[j] : dlu[j] * bv[j];
+            h = __builtin_fmaf(a[j], h, bu);
+            hh[j] = h;
+            if constexpr (kHasZ) y[j] = __builtin_fmaf(cv[j], h, y[j]);
+          }
         }
         // ---- reverse: local aggregate of lambda, reverse scan, re-run with true lambda
         float lam = cv[kT - 1] * g[kT - 1];
@@ -184,19 +194,20 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         const float rb_s = dpp_mov<kWaveShl1, 0xF>(0.f, rb);
         lam = __builtin_fmaf(ra_s, mu_in, rb_s) + cv[kT - 1] * g[kT - 1];
         float dA_acc = 0.f;
-        float* accB = acc + n * kChunk;
-        float* accC = acc + (kMaxN + n) * kChunk;
+        float* accB = acc_w + n * kChunk;
+        float* accC = acc_w + (N + n) * kChunk;
 #pragma unroll
         for (int j = kT - 1; j >= 0; --j) {
           if (j < kT - 1) lam = __builtin_fmaf(a[j + 1], lam, cv[j] * g[j]);
-          const float q = lam * ah[j];
+          const float ah = a[j] * (j > 0 ? hh[j - 1] : hin);  // a_bar_t * h_{t-1}
+          const float q = lam * ah;
           float dBv;
           if constexpr (kZOH) {
-            const float e = expm1f(dlt[j] * An) / An;
+            const float e = expm1f(dlt[j] * An) * fast_rcp(An);
             const float lb = lam * bv[j];
             s1[j] = __builtin_fmaf(lb, e, s1[j]);
             s2[j] = __builtin_fmaf(An, q, __builtin_fmaf(lb * uu[j], a[j], s2[j]));
-            const float dedA = (dlt[j] * a[j] - e) / An;
+            const float dedA = (dlt[j] * a[j] - e) * fast_rcp(An);
             dA_acc = __builtin_fmaf(dlt[j], q, __builtin_fmaf(lb * uu[j], dedA, dA_acc));
             dBv = lam * e * uu[j];
           } else {
@@ -206,8 +217,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
             dBv = lam * dlu[j];
           }
           const int slot = j * 64 + (lane ^ j);
-          atomicAdd(accB + slot, dBv);
-          atomicAdd(accC + slot, g[j] * hh[j]);
+          accB[slot] += dBv;
+          accC[slot] += g[j] * hh[j];
         }
         const float dA_sum = wave_sum(dA_acc);
         if (lane == 0) {
@@ -216,8 +227,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
           if (c == 0 && p.dinit) p.dinit[chan * N + n] = mu_out;
         }
       }
-      if (!active) continue;
 
+      if (!active) continue;
       // ---- per-step gradients of the row
       float dD_acc = 0.f, db_acc = 0.f;
       float duv[kT], ddv[kT];
@@ -234,9 +245,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         }
         if (p.delta_softplus) {
           // d softplus(x)/dx = sigmoid(x) = 1 - exp(-softplus(x)); identity above 20.
-          const float x_sig = -expm1f(-dlt[j]);
-          const bool ident = dlt[j] > 20.f;
-          dd_j = ident ? dd_j : dd_j * x_sig;
+          dd_j = dlt[j] > 20.f ? dd_j : dd_j * one_minus_exp_neg(dlt[j]);
         }
         du_j = valid ? du_j : 0.f;
         dd_j = valid ? dd_j : 0.f;
@@ -267,10 +276,14 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       const int n = rem / kChunk;
       const int toff = rem - n * kChunk;
       const int ln = toff / kT, j = toff - ln * kT;
-      float* src = acc + (which * kMaxN + n) * kChunk + j * 64 + (ln ^ j);
+      const int off = (which * N + n) * kChunk + j * 64 + (ln ^ j);
+      float v = 0.f;
+      for (int cp = 0; cp < n_copy; ++cp) {
+        v += acc[cp * 2 * N * kChunk + off];
+        acc[cp * 2 * N * kChunk + off] = 0.f;
+      }
       const int t = t0 + toff;
-      if (t < L) part[which * nl + static_cast<size_t>(n) * L + t] = *src;
-      *src = 0.f;
+      if (t < L) part[which * nl + static_cast<size_t>(n) * L + t] = v;
     }
     __syncthreads();
   }
@@ -362,14 +375,16 @@ int bwd_chan_per_block(int batch, int dim) {
   return static_cast<int>(k) * kBwdW;
 }
 
-hipError_t launch_bwd(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, void* dA, void* dB,
-                      void* dC, float* dD, float* dbias, hipStream_t stream) {
-  hipError_t e;
-  if (io_bf16) e = bc_bf16 ? launch_bwd_io<bf16_t, bf16_t>(p, zoh, stream)
-                           : launch_bwd_io<bf16_t, float>(p, zoh, stream);
-  else e = bc_bf16 ? launch_bwd_io<float, bf16_t>(p, zoh, stream)
-                   : launch_bwd_io<float, float>(p, zoh, stream);
-  if (e != hipSuccess) return e;
+hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16,
+                           hipStream_t stream) {
+  if (io_bf16) return bc_bf16 ? launch_bwd_io<bf16_t, bf16_t>(p, zoh, stream)
+                              : launch_bwd_io<bf16_t, float>(p, zoh, stream);
+  return bc_bf16 ? launch_bwd_io<float, bf16_t>(p, zoh, stream)
+                 : launch_bwd_io<float, float>(p, zoh, stream);
+}
+
+hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB, void* dC,
+                             float* dD, float* dbias, hipStream_t stream) {
   const size_t nl = static_cast<size_t>(p.dstate) * p.seqlen;
   const size_t total = static_cast<size_t>(p.batch) * 2 * nl;
   int grid = static_cast<int>((total + 255) / 256);
@@ -381,7 +396,7 @@ hipError_t launch_bwd(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, voi
     hipLaunchKernelGGL(reduce_bc_kernel<float>, dim3(grid), dim3(256), 0, stream, p.part_dBC,
                        p.n_blocks_d, p.batch, nl, static_cast<float*>(dB), static_cast<float*>(dC));
   }
-  e = hipGetLastError();
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int small = p.dim * p.dstate + 2 * p.dim;
   hipLaunchKernelGGL(reduce_small_kernel, dim3((small + 255) / 256), dim3(256), 0, stream, p.part_dA,

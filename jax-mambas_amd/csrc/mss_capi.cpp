@@ -18,8 +18,10 @@
 
 namespace mss {
 hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
-hipError_t launch_bwd(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, void* dA, void* dB,
-                      void* dC, float* dD, float* dbias, hipStream_t stream);
+hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16,
+                           hipStream_t stream);
+hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB, void* dC,
+                             float* dD, float* dbias, hipStream_t stream);
 int bwd_chan_per_block(int batch, int dim);
 }  // namespace mss
 
@@ -129,17 +131,9 @@ int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching selective scan forward");
 }
 
-int run_bwd(const mss_bwd_args* a, hipStream_t stream) {
-  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate);
-  char* ws = static_cast<char*>(a->workspace);
-  bool owned = false;
-  if (ws == nullptr) {
-    const hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), l.total, stream);
-    if (e != hipSuccess) return hip_fail(e, "allocating backward workspace");
-    owned = true;
-  } else if (a->workspace_bytes < l.total) {
-    return MSS_ERR_WORKSPACE;
-  }
+enum BwdPhase { kPhaseScan = 1, kPhaseReduce = 2, kPhaseBoth = 3 };
+
+mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   mss::BwdParams p{};
   p.batch = a->batch;
   p.dim = a->dim;
@@ -175,9 +169,30 @@ int run_bwd(const mss_bwd_args* a, hipStream_t stream) {
   p.part_dA = reinterpret_cast<float*>(ws + l.off_dA);
   p.part_dD = reinterpret_cast<float*>(ws + l.off_dD);
   p.part_dbias = reinterpret_cast<float*>(ws + l.off_db);
-  hipError_t e = mss::launch_bwd(p, a->discretization == MSS_ZOH, a->io_dtype == MSS_BF16,
-                                 a->bc_dtype == MSS_BF16, a->dA, a->dB, a->dC, a->dD,
-                                 a->ddelta_bias, stream);
+  return p;
+}
+
+int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream) {
+  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate);
+  char* ws = static_cast<char*>(a->workspace);
+  bool owned = false;
+  if (ws == nullptr) {
+    // Split phases hand partial sums from one call to the next through the workspace.
+    if (phases != kPhaseBoth) return MSS_ERR_WORKSPACE;
+    const hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), l.total, stream);
+    if (e != hipSuccess) return hip_fail(e, "allocating backward workspace");
+    owned = true;
+  } else if (a->workspace_bytes < l.total) {
+    return MSS_ERR_WORKSPACE;
+  }
+  const mss::BwdParams p = pack_bwd(a, l, ws);
+  const int zoh = a->discretization == MSS_ZOH;
+  const int io_bf16 = a->io_dtype == MSS_BF16;
+  const int bc_bf16 = a->bc_dtype == MSS_BF16;
+  hipError_t e = hipSuccess;
+  if (phases & kPhaseScan) e = mss::launch_bwd_scan(p, zoh, io_bf16, bc_bf16, stream);
+  if (e == hipSuccess && (phases & kPhaseReduce))
+    e = mss::launch_bwd_reduce(p, bc_bf16, a->dA, a->dB, a->dC, a->dD, a->ddelta_bias, stream);
   if (owned) {
     const hipError_t f = hipFreeAsync(ws, stream);
     if (e == hipSuccess) e = f;
@@ -218,7 +233,19 @@ int mss_fwd(const mss_fwd_args* args, void* stream) {
 int mss_bwd(const mss_bwd_args* args, void* stream) {
   const int s = validate_bwd(args);
   if (s != MSS_OK) return s;
-  return run_bwd(args, static_cast<hipStream_t>(stream));
+  return run_bwd(args, kPhaseBoth, static_cast<hipStream_t>(stream));
+}
+
+int mss_bwd_scan(const mss_bwd_args* args, void* stream) {
+  const int s = validate_bwd(args);
+  if (s != MSS_OK) return s;
+  return run_bwd(args, kPhaseScan, static_cast<hipStream_t>(stream));
+}
+
+int mss_bwd_reduce(const mss_bwd_args* args, void* stream) {
+  const int s = validate_bwd(args);
+  if (s != MSS_OK) return s;
+  return run_bwd(args, kPhaseReduce, static_cast<hipStream_t>(stream));
 }
 
 int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,
@@ -325,7 +352,7 @@ int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32
   a.dB = dB;
   a.dC = dC;
   a.dinitial_state = dinitial_x;
-  s = run_bwd(&a, st);
+  s = run_bwd(&a, kPhaseBoth, st);
   e = hipFreeAsync(carries, st);
   if (s != MSS_OK) return s;
   return e == hipSuccess ? MSS_OK : hip_fail(e, "freeing carry states");

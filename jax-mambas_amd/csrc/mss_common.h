@@ -133,7 +133,15 @@ __device__ __forceinline__ float log1p_pos(float w) {
   const float u = 1.f + w;
   const float d = u - 1.f;
   const float l = fast_log2(u) * kLn2;
-  return d == 0.f ? w : l * (w / d);
+  return d == 0.f ? w : l * (w * fast_rcp(d));
+}
+
+// 1 - exp(-x) for x >= 0 (= sigmoid(y) when x = softplus(y)); series below 1/64 keeps
+// the relative error near one ulp where 1 - exp(-x) would cancel.
+__device__ __forceinline__ float one_minus_exp_neg(float x) {
+  const float e = fast_exp2(-x * kLog2e);
+  const float series = x * __builtin_fmaf(x, __builtin_fmaf(x, __builtin_fmaf(x, -1.f / 24.f, 1.f / 6.f), -0.5f), 1.f);
+  return x < 0.015625f ? series : 1.f - e;
 }
 
 // softplus(x) = log(1 + e^x), identity above 20 (threshold of the reference kernel,
@@ -178,6 +186,47 @@ __device__ __forceinline__ void load_seg(const bf16_t* __restrict__ row, int t, 
 #pragma unroll
     for (int q = 0; q < N / 8; ++q) {
       const u32x4 x = __builtin_nontemporal_load(p + q);
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[8 * q + 2 * k + 0] = __uint_as_float(w[k] << 16);
+        v[8 * q + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = (t + j < L) ? to_f32(row[t + j]) : 0.f;
+  }
+}
+
+// Cached (non-streaming) variant for rows many waves re-read (B, C).
+template <int N>
+__device__ __forceinline__ void load_seg_cached(const float* __restrict__ row, int t, int L, bool vec,
+                                                float (&v)[N]) {
+  if (vec && t + N <= L) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(row + t);
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+      const f32x4 x = p[q];
+      v[4 * q + 0] = x.x;
+      v[4 * q + 1] = x.y;
+      v[4 * q + 2] = x.z;
+      v[4 * q + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = (t + j < L) ? row[t + j] : 0.f;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void load_seg_cached(const bf16_t* __restrict__ row, int t, int L, bool vec,
+                                                float (&v)[N]) {
+  if (vec && t + N <= L) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(row + t);
+#pragma unroll
+    for (int q = 0; q < N / 8; ++q) {
+      const u32x4 x = p[q];
       const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {

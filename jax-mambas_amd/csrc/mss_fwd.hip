@@ -13,19 +13,110 @@
 //   scan     64-lane inclusive affine scan of (P, H) on DPP; the lane's carry-in is the
 //            previous lane's end state (the chunk's running state for lane 0)
 //   phase C  lane-local re-run from the true carry; y_t += C_t * h_t
-// B and C rows of the chunk are staged in LDS once per workgroup and shared by its waves.
+// B and C rows of the chunk are staged in LDS once per workgroup and shared by its waves:
+// rounds of kNB states are copied global->LDS with gfx950's direct-to-LDS loads into one
+// of two buffers while the previous round is computed (one barrier per round).
 #include "mss_common.h"
 
 namespace mss {
 
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef __attribute__((address_space(1))) void* gbl_void_t;
+
+// Staging layout of one chunk row: 16-byte slots; segment i (lane i) owns slots
+// [kQ*i, kQ*i + kQ) with its q-th slot stored at kQ*i + (q ^ swz(i)) so that 16
+// consecutive lanes reading their q-th slot hit 16 distinct 4-bank groups.
+template <int kQ>
+__device__ __forceinline__ int slot_swz(int i) {
+  static_assert(kQ >= 1 && kQ <= 16 && (kQ & (kQ - 1)) == 0, "kQ must be a power of two <= 16");
+  constexpr int kShift = kQ == 16 ? 0 : (kQ == 8 ? 1 : (kQ == 4 ? 2 : (kQ == 2 ? 3 : 4)));
+  return (i >> kShift) & (kQ - 1);
+}
+
+template <typename bc_t>
+struct BcStage {
+  static constexpr int kElemsPerSlot = 16 / static_cast<int>(sizeof(bc_t));
+};
+
+// Read lane `lane`'s kT staged values of one row (fp32 or bf16 in LDS) as floats.
+template <int kT, typename bc_t>
+__device__ __forceinline__ void read_staged(const uint4* __restrict__ row, int lane, float (&v)[kT]) {
+  constexpr int kE = BcStage<bc_t>::kElemsPerSlot;
+  constexpr int kQ = kT / kE;
+  const int sw = slot_swz<kQ>(lane);
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const uint4 x = row[kQ * lane + (q ^ sw)];
+    if constexpr (sizeof(bc_t) == 4) {
+      v[4 * q + 0] = __uint_as_float(x.x);
+      v[4 * q + 1] = __uint_as_float(x.y);
+      v[4 * q + 2] = __uint_as_float(x.z);
+      v[4 * q + 3] = __uint_as_float(x.w);
+    } else {
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[8 * q + 2 * k + 0] = __uint_as_float(w[k] << 16);
+        v[8 * q + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      }
+    }
+  }
+}
+
+// Stage elements [t0, t0 + 64*kT) of one row into `dst` (64*kT elements of bc_t).
+// dma: rows are 16-byte aligned and L is a multiple of the slot width, so each slot is
+// either fully inside [0, L) or fully past it; past-the-end slots re-read the last valid
+// slot (finite values; they only meet zero coefficients).
+template <int kT, int kW, typename bc_t>
+__device__ __forceinline__ void stage_row_async(const bc_t* __restrict__ row, int t0, int L, bool dma,
+                                                uint4* __restrict__ dst, int tid) {
+  constexpr int kE = BcStage<bc_t>::kElemsPerSlot;
+  constexpr int kQ = kT / kE;
+  constexpr int kSlots = 64 * kQ;
+  if (dma) {
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    for (int s0 = w * 64; s0 < kSlots; s0 += kW * 64) {
+      const int s = s0 + lane;
+      const int i = s / kQ;
+      const int q = (s % kQ) ^ slot_swz<kQ>(i);
+      int e = t0 + i * kT + q * kE;
+      e = e < L ? e : L - kE;
+      __builtin_amdgcn_global_load_lds((gbl_void_t)(row + e), (lds_void_t)(dst + s0), 16, 0, 0);
+    }
+  } else {
+    bc_t* d = reinterpret_cast<bc_t*>(dst);
+    for (int e = tid; e < 64 * kT; e += kW * 64) {
+      const int i = e / kT;
+      const int r = e % kT;
+      const int q = r / kE;
+      const int s = kQ * i + (q ^ slot_swz<kQ>(i));
+      const int t = t0 + e;
+      bc_t v;
+      if (t < L) {
+        v = row[t];
+      } else {
+        store_as(&v, 0.f);
+      }
+      d[s * kE + (r % kE)] = v;
+    }
+  }
+}
+
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 template <int kT, int kW, bool kZOH, typename io_t, typename bc_t>
 __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
   constexpr int kChunk = 64 * kT;
-  constexpr int kStride = kT + 4;
-  constexpr int kNB = 4;  // states staged per LDS round
-  __shared__ __attribute__((aligned(16))) float sB[kNB][64 * kStride];
-  __shared__ __attribute__((aligned(16))) float sC[kNB][64 * kStride];
+  constexpr int kNB = 2;  // states staged per round
+  constexpr int kRowSlots = kChunk * static_cast<int>(sizeof(bc_t)) / 16;
+  // Two stage buffers as distinct objects, selected statically (rounds run in pairs), so
+  // the compiler can tell the in-flight copy into one from the reads of the other.
+  __shared__ uint4 stage0[kNB][2][kRowSlots];  // [state][B|C][slot]
+  __shared__ uint4 stage1[kNB][2][kRowSlots];
   __shared__ float s_run[kW][kMaxN];
+  __shared__ float s_a2[kW][kMaxN];
+  __shared__ float s_a[kW][kMaxN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -46,19 +137,39 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
   const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + static_cast<size_t>(b) * N * L;
   const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + static_cast<size_t>(b) * N * L;
 
-  if (lane < N) s_run[w][lane] = p.x0 ? p.x0[chan * N + lane] : 0.f;
+  if (lane < N) {
+    s_run[w][lane] = p.x0 ? p.x0[chan * N + lane] : 0.f;
+    const float an = p.A[static_cast<size_t>(d) * N + lane];
+    s_a[w][lane] = an;
+    s_a2[w][lane] = an * kLog2e;
+  }
   const float Dv = p.D ? p.D[d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
   const bool vec_io = p.vec_io != 0;
-  const bool vec_bc = p.vec_bc != 0;
+  const bool dma = p.vec_bc != 0;
   float dsum_total = 0.f;  // sum of delta over all finished steps (reference residual)
 
   const int n_chunks = (L + kChunk - 1) / kChunk;
+  const int n_active_chunks = (len + kChunk - 1) / kChunk;
+  // Rounds of kNB states per chunk, padded to an even count so round g of every chunk
+  // uses buffer g & 1.
+  const int rounds = ((N + kNB - 1) / kNB + 1) & ~1;
+  auto issue_round = [&](int r, uint4 (*buf)[2][kRowSlots]) {
+    const int c = r / rounds;
+    const int n0 = (r - c * rounds) * kNB;
+    const int nb = min(kNB, N - n0);
+    for (int k = 0; k < nb; ++k) {
+      stage_row_async<kT, kW, bc_t>(Bb + static_cast<size_t>(n0 + k) * L, c * kChunk, L, dma, buf[k][0], tid);
+      stage_row_async<kT, kW, bc_t>(Cb + static_cast<size_t>(n0 + k) * L, c * kChunk, L, dma, buf[k][1], tid);
+    }
+  };
+  if (n_active_chunks > 0) issue_round(0, stage0);
+
   for (int c = 0; c < n_chunks; ++c) {
     const int t0 = c * kChunk;
     const int tl = t0 + lane * kT;
 
-    if (t0 >= len) {
+    if (c >= n_active_chunks) {
       // Entire chunk is past this row's length: state frozen, output zero.
       if (active) {
         float zero[kT];
@@ -72,9 +183,8 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
         }
         if (p.ref_states && lane == 63 && c < p.n_ref) {
           for (int n = 0; n < N; ++n) {
-            const float a2 = p.A[d * N + n] * kLog2e;
             float* rs = p.ref_states + ((chan * p.n_ref + c) * N + n) * 2;
-            rs[0] = fast_exp2(a2 * dsum_total);
+            rs[0] = fast_exp2(s_a2[w][n] * dsum_total);
             rs[1] = s_run[w][n];
           }
         }
@@ -106,29 +216,23 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
     }
     if (p.ref_states) dsum_total += wave_sum(ssum);
 
-    for (int n0 = 0; n0 < N; n0 += kNB) {
+    auto compute_round = [&](int g, uint4 (*buf)[2][kRowSlots]) {
+      const int n0 = g * kNB;
       const int nb = min(kNB, N - n0);
-      __syncthreads();  // previous round's LDS readers are done
-      for (int k = 0; k < nb; ++k) {
-        stage_row<kT>(Bb + static_cast<size_t>(n0 + k) * L, t0, L, vec_bc, sB[k], tid, kW * 64);
-        stage_row<kT>(Cb + static_cast<size_t>(n0 + k) * L, t0, L, vec_bc, sC[k], tid, kW * 64);
-      }
-      __syncthreads();
-      if (!active) continue;
       for (int k = 0; k < nb; ++k) {
         const int n = n0 + k;
-        const float An = p.A[d * N + n];
-        const float a2 = An * kLog2e;
+        const float a2 = s_a2[w][n];
         float a[kT], bu[kT];
         float H = 0.f;
         {
           float bv[kT];
-          lds_read_seg<kT>(sB[k], lane, bv);
+          read_staged<kT, bc_t>(buf[k][0], lane, bv);
 #pragma unroll
           for (int j = 0; j < kT; ++j) {
             a[j] = fast_exp2(dlt[j] * a2);
             if constexpr (kZOH) {
-              bu[j] = (expm1f(dlt[j] * An) / An) * bv[j] * dlu[j];
+              const float An = s_a[w][n];
+              bu[j] = (expm1f(dlt[j] * An) * fast_rcp(An)) * bv[j] * dlu[j];
             } else {
               bu[j] = dlu[j] * bv[j];
             }
@@ -142,7 +246,7 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
         float h = dpp_mov<kWaveShr1, 0xF>(run, hend);   // carry-in (lane 0: running state)
         {
           float cv[kT];
-          lds_read_seg<kT>(sC[k], lane, cv);
+          read_staged<kT, bc_t>(buf[k][1], lane, cv);
 #pragma unroll
           for (int j = 0; j < kT; ++j) {
             h = __builtin_fmaf(a[j], h, bu[j]);
@@ -163,6 +267,18 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
         }
         if (p.last && c == n_chunks - 1 && lane == 63) p.last[chan * N + n] = hend;
       }
+    };
+    const int last_round = n_active_chunks * rounds;
+    for (int g = 0; g < rounds; g += 2) {
+      const int r = c * rounds + g;
+      wait_vmem_all();   // this thread's copies for round r have landed in LDS
+      __syncthreads();   // ... and everyone's; round r-1's readers are done
+      if (r + 1 < last_round) issue_round(r + 1, stage1);
+      if (active) compute_round(g, stage0);
+      wait_vmem_all();
+      __syncthreads();
+      if (r + 2 < last_round) issue_round(r + 2, stage0);
+      if (active) compute_round(g + 1, stage1);
     }
 
     if (active && p.out) {

@@ -31,6 +31,8 @@ EXPORTED_SYMBOLS = (
     "mss_bwd_workspace_bytes",
     "mss_fwd",
     "mss_bwd",
+    "mss_bwd_scan",
+    "mss_bwd_reduce",
     "mss_scan_fwd",
     "mss_scan_fwd_repeat",
     "mss_scan_bwd",
@@ -94,6 +96,9 @@ def register_hip_kernel(library_path=None):
     lib.mss_fwd.restype = ctypes.c_int
     lib.mss_bwd.argtypes = [ctypes.POINTER(BwdArgs), _p]
     lib.mss_bwd.restype = ctypes.c_int
+    for name in ("mss_bwd_scan", "mss_bwd_reduce"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(BwdArgs), _p]
+        getattr(lib, name).restype = ctypes.c_int
     lib.mss_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
     lib.mss_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.mss_scan_fwd.argtypes = [_p, _i32, _i32, _i32, _i32, _i32] + [_p] * 9
