@@ -66,6 +66,7 @@ def gpu_step_setup(torch, cfg):
     t["out"] = torch.empty_like(t["u"])
     t["last"] = torch.empty(b, d, n, device=dev)
     t["carries"] = torch.empty(b, d, n_carry, n, device=dev)
+    t["y_pre"] = torch.empty_like(t["u"])
     t["dlast"] = torch.zeros(b, d, n, device=dev)
     for k in ("u", "delta", "z"):
         t["d" + k] = torch.empty_like(t[k])
@@ -75,11 +76,11 @@ def gpu_step_setup(torch, cfg):
     fa = _lib.FwdArgs(batch=b, dim=d, seqlen=l, dstate=n, discretization=_lib.MSS_EULER, delta_softplus=1,
                       io_dtype=_lib.MSS_F32, bc_dtype=_lib.MSS_F32, u=P("u"), delta=P("delta"), A=P("A"),
                       B=P("B"), C=P("C"), D=P("D"), z=P("z"), delta_bias=P("delta_bias"),
-                      out=P("out"), last_state=P("last"), carries=P("carries"))
+                      out=P("out"), last_state=P("last"), carries=P("carries"), y_pre=P("y_pre"))
     ba = _lib.BwdArgs(batch=b, dim=d, seqlen=l, dstate=n, discretization=_lib.MSS_EULER, delta_softplus=1,
                       io_dtype=_lib.MSS_F32, bc_dtype=_lib.MSS_F32, u=P("u"), delta=P("delta"), A=P("A"),
                       B=P("B"), C=P("C"), D=P("D"), z=P("z"), delta_bias=P("delta_bias"),
-                      carries=P("carries"), dout=P("dout"), dlast_state=P("dlast"), du=P("du"),
+                      carries=P("carries"), y_pre=P("y_pre"), dout=P("dout"), dlast_state=P("dlast"), du=P("du"),
                       ddelta=P("ddelta"), dA=P("dA"), dB=P("dB"), dC=P("dC"), dD=P("dD"), dz=P("dz"),
                       ddelta_bias=P("ddelta_bias"))
     ws_bytes = int(lib.mss_bwd_workspace_bytes(ba))

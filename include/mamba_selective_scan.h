@@ -16,6 +16,7 @@
  *   seq_lens                              : [batch] int32 (optional variable lengths)
  *   carries                               : [batch][dim][ceil(seqlen/1024)][dstate] float32
  *                                           state h at the end of every 1024-step chunk
+ *   y_pre                                 : [batch][dim][seqlen] y before the z gate
  *
  * All entry points are asynchronous on the given stream (a hipStream_t passed as
  * void*; NULL = the default stream), re-entrant, and validate every argument before
@@ -78,6 +79,8 @@ typedef struct mss_fwd_args {
   void* out;
   float* last_state; /* optional */
   float* carries;    /* optional; required by mss_bwd */
+  void* y_pre;       /* optional [B][D][L] (io dtype): y before the silu(z) gate, the
+                        residual mss_bwd needs when z is given */
 } mss_fwd_args;
 
 /* Backward of the fused scan. Outputs are fully overwritten (no accumulation).
@@ -100,6 +103,7 @@ typedef struct mss_bwd_args {
   const float* initial_state;
   const int32_t* seq_lens;
   const float* carries;     /* from mss_fwd with the same inputs; required */
+  const void* y_pre;        /* from mss_fwd; required iff z given */
   const void* dout;
   const float* dlast_state; /* optional cotangent of last_state */
   void* du;

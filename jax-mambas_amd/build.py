@@ -37,20 +37,23 @@ def flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build(verbose: bool = False, out_dir: Path | None = None, defines: dict | None = None) -> Path:
+    """Compile the library; `defines` (name -> value) are passed as -D options."""
+    out_dir = Path(out_dir) if out_dir is not None else BUILD
+    out_dir.mkdir(parents=True, exist_ok=True)
+    extra = [f"-D{k}={v}" for k, v in (defines or {}).items()]
     objs = []
     for src in SOURCES:
-        obj = BUILD / (src + ".o")
-        cmd = [hipcc(), *flags(), "-c", str(CSRC / src), "-o", str(obj)]
+        obj = out_dir / (src + ".o")
+        cmd = [hipcc(), *flags(), *extra, "-c", str(CSRC / src), "-o", str(obj)]
         if src.endswith(".cpp"):
             cmd[1:1] = ["-x", "hip"]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
         objs.append(str(obj))
-    out = BUILD / LIB_NAME
-    tmp = BUILD / (LIB_NAME + ".tmp")
+    out = out_dir / LIB_NAME
+    tmp = out_dir / (LIB_NAME + ".tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)

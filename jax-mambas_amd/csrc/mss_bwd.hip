@@ -32,8 +32,10 @@ template <int kT, int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
 __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   constexpr int kChunk = 64 * kT;
   static_assert(kChunk == kCarryChunk, "backward chunk must match the carry residual");
-  // dB/dC partial sums of the workgroup's channels for one chunk: [copy][which][n][slot],
-  // slot = j*64 + (lane ^ j). At state iteration i wave w owns row n = (i + w) mod N of
+  // dB/dC partial sums of the workgroup's channels for one chunk: [copy][n][j][which][lane]
+  // (step j of lane `lane`'s segment): conflict-free for the 64 lanes of a wave, and every
+  // access of a state is a constant offset from one per-lane base, so the read-add-writes
+  // batch freely. At state iteration i wave w owns row n = (i + w) mod N of
   // copy w / N, so rows are updated with plain read-add-write in a fixed order
   // (LDS float atomics run ~40x slower than stores on gfx950 and are avoided).
   __shared__ float acc[2 * kMaxN * kChunk];
@@ -59,6 +61,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + static_cast<size_t>(b) * N * L;
 
   const int n_copy = (kW + N - 1) / N;  // n_copy * N <= 2 * kMaxN for N <= kMaxN
+  const int w_mod_n = w % N;
   float* const acc_w = acc + (w / N) * 2 * N * kChunk;
   for (int i = tid; i < 2 * kMaxN * kChunk; i += kW * 64) acc[i] = 0.f;
   for (int k = 0; k < K; ++k) {
@@ -81,6 +84,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   for (int c = n_chunks - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
     const int tl = t0 + lane * kT;
+    const bool fast = vec_io && (t0 + kChunk <= L);     // wave-uniform
+    const bool fast_bc = vec_bc && (t0 + kChunk <= L);  // wave-uniform
     for (int k = 0; k < K; ++k) {
       const int cl = k * kW + w;
       const int d_raw = blk * p.chan_per_block + cl;
@@ -96,9 +101,9 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         float zero[kT];
 #pragma unroll
         for (int j = 0; j < kT; ++j) zero[j] = 0.f;
-        store_seg<kT>(du_row, tl, L, vec_io, zero);
-        store_seg<kT>(dd_row, tl, L, vec_io, zero);
-        if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, vec_io, zero);
+        store_seg<kT>(du_row, tl, L, fast, zero);
+        store_seg<kT>(dd_row, tl, L, fast, zero);
+        if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, zero);
         if (c == 0 && p.dinit && lane < N) {
           // len == 0: x0 flows through identity steps to the last state.
           p.dinit[chan * N + lane] = s_mu[cl][lane];
@@ -114,49 +119,63 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       const float Dv = p.D ? p.D[d] : 0.f;
       const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
       float dlt[kT], dlu[kT], uu[kT], g[kT], s1[kT], s2[kT];
-      float wz[kT], y[kT];
       float ssum = 0.f;
-      {
-        float zr[kT];
-        load_seg<kT>(static_cast<const io_t*>(p.delta) + row, tl, L, vec_io, dlt);
-        load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, vec_io, uu);
-        load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, vec_io, g);
-        if constexpr (kHasZ) load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, vec_io, zr);
+      load_seg<kT>(static_cast<const io_t*>(p.delta) + row, tl, L, fast, dlt);
+      load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
+      load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, fast, g);
+      if constexpr (kHasZ) {
+        // Gate: g = dout * silu(z); dz = dout * y * sigmoid(z) * (1 + z * (1 - sigmoid(z)))
+        // with y the pre-gate output kept by the forward.
+        float zr[kT], yp[kT];
+        load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zr);
+        load_seg<kT>(static_cast<const io_t*>(p.y_pre) + row, tl, L, fast, yp);
 #pragma unroll
         for (int j = 0; j < kT; ++j) {
           const bool valid = tl + j < len;
-          const float x = dlt[j] + bias;
-          float dv = p.delta_softplus ? softplus(x) : x;
-          dv = valid ? dv : 0.f;
-          const float uv = valid ? uu[j] : 0.f;
-          float go = valid ? g[j] : 0.f;
-          if constexpr (kHasZ) {
-            const float sz = sigmoid(zr[j]);
-            wz[j] = go * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);  // dz = wz * y
-            go = go * zr[j] * sz;
-            y[j] = Dv * uv;
-          }
-          dlt[j] = dv;
-          uu[j] = uv;
-          dlu[j] = dv * uv;
-          g[j] = go;
-          s1[j] = 0.f;
-          s2[j] = 0.f;
-          ssum += dv;
+          const float go = valid ? g[j] : 0.f;
+          const float sz = sigmoid(zr[j]);
+          yp[j] = go * yp[j] * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
+          g[j] = go * zr[j] * sz;
         }
+        store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);
+      }
+#pragma unroll
+      for (int j = 0; j < kT; ++j) {
+        const bool valid = tl + j < len;
+        const float x = dlt[j] + bias;
+        float dv = p.delta_softplus ? softplus(x) : x;
+        dv = valid ? dv : 0.f;
+        const float uv = valid ? uu[j] : 0.f;
+        dlt[j] = dv;
+        uu[j] = uv;
+        dlu[j] = dv * uv;
+        if constexpr (!kHasZ) g[j] = valid ? g[j] : 0.f;
+        s1[j] = 0.f;
+        s2[j] = 0.f;
+        ssum += dv;
       }
 
       // States in a per-wave rotated order (see the accumulator above); the barrier per
       // iteration keeps every wave inside the same iteration.
       for (int i = 0; i < N; ++i) {
-        const int n = (i + w) % N;
+        int n = i + w_mod_n;
+        n = n >= N ? n - N : n;
         __syncthreads();
         if (!active) continue;
+        // This wave owns accumulator row n until the next barrier: fetch it now so the LDS
+        // latency overlaps the state's arithmetic; it is written back at the end.
+        float* accn = acc_w + n * 2 * kChunk + lane;
+        float accv[2 * kT];
+#pragma unroll
+        for (int j = 0; j < kT; ++j) {
+          accv[2 * j] = accn[j * 128];
+          accv[2 * j + 1] = accn[j * 128 + 64];
+        }
         const float An = s_a[w][n];
         const float a2 = An * kLog2e;
         float bv[kT], cv[kT], a[kT];
-        load_seg_cached<kT>(Bb + static_cast<size_t>(n) * L, tl, L, vec_bc, bv);
-        load_seg_cached<kT>(Cb + static_cast<size_t>(n) * L, tl, L, vec_bc, cv);
+        load_seg<kT>(Bb + static_cast<size_t>(n) * L, tl, L, fast_bc, bv);
+        load_seg<kT>(Cb + static_cast<size_t>(n) * L, tl, L, fast_bc, cv);
         // ---- forward: local aggregate, scan, re-run from the true carry-in
         float H = 0.f;
 #pragma unroll
@@ -179,7 +198,6 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
             const float bu = kZOH ? (expm1f(dlt[j] * An) * fast_rcp(An)) * bv[j] * uu[j] : dlu[j] * bv[j];
             h = __builtin_fmaf(a[j], h, bu);
             hh[j] = h;
-            if constexpr (kHasZ) y[j] = __builtin_fmaf(cv[j], h, y[j]);
           }
         }
         // ---- reverse: local aggregate of lambda, reverse scan, re-run with true lambda
@@ -194,8 +212,6 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         const float rb_s = dpp_mov<kWaveShl1, 0xF>(0.f, rb);
         lam = __builtin_fmaf(ra_s, mu_in, rb_s) + cv[kT - 1] * g[kT - 1];
         float dA_acc = 0.f;
-        float* accB = acc_w + n * kChunk;
-        float* accC = acc_w + (N + n) * kChunk;
 #pragma unroll
         for (int j = kT - 1; j >= 0; --j) {
           if (j < kT - 1) lam = __builtin_fmaf(a[j + 1], lam, cv[j] * g[j]);
@@ -216,9 +232,13 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
             dA_acc = __builtin_fmaf(dlt[j], q, dA_acc);
             dBv = lam * dlu[j];
           }
-          const int slot = j * 64 + (lane ^ j);
-          accB[slot] += dBv;
-          accC[slot] += g[j] * hh[j];
+          accv[2 * j] += dBv;
+          accv[2 * j + 1] = __builtin_fmaf(g[j], hh[j], accv[2 * j + 1]);
+        }
+#pragma unroll
+        for (int j = 0; j < kT; ++j) {
+          accn[j * 128] = accv[2 * j];
+          accn[j * 128 + 64] = accv[2 * j + 1];
         }
         const float dA_sum = wave_sum(dA_acc);
         if (lane == 0) {
@@ -253,11 +273,9 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         db_acc += dd_j;
         duv[j] = du_j;
         ddv[j] = dd_j;
-        if constexpr (kHasZ) y[j] = valid ? wz[j] * y[j] : 0.f;
       }
-      store_seg<kT>(du_row, tl, L, vec_io, duv);
-      store_seg<kT>(dd_row, tl, L, vec_io, ddv);
-      if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, vec_io, y);
+      store_seg<kT>(du_row, tl, L, fast, duv);
+      store_seg<kT>(dd_row, tl, L, fast, ddv);
       const float dD_sum = wave_sum(dD_acc);
       const float db_sum = wave_sum(db_acc);
       if (lane == 0) {
@@ -269,21 +287,30 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
     // ---- flush this chunk's dB/dC sums over the block's channels
     __syncthreads();
     const size_t nl = static_cast<size_t>(N) * L;
-    float* part = p.part_dBC + (static_cast<size_t>(blk) * p.batch + b) * 2 * nl;
-    for (int e = tid; e < 2 * N * kChunk; e += kW * 64) {
-      const int which = e / (N * kChunk);
-      const int rem = e - which * N * kChunk;
-      const int n = rem / kChunk;
-      const int toff = rem - n * kChunk;
-      const int ln = toff / kT, j = toff - ln * kT;
-      const int off = (which * N + n) * kChunk + j * 64 + (ln ^ j);
-      float v = 0.f;
-      for (int cp = 0; cp < n_copy; ++cp) {
-        v += acc[cp * 2 * N * kChunk + off];
-        acc[cp * 2 * N * kChunk + off] = 0.f;
+    float* part = p.part_dBC + static_cast<size_t>(blk) * p.part_stride + static_cast<size_t>(b) * 2 * nl;
+    for (int row_i = 0; row_i < 2 * N; ++row_i) {  // (which, n) rows of the accumulator
+      const int which = row_i >= N;
+      const int n = row_i - which * N;
+      float* dst = part + which * nl + static_cast<size_t>(n) * L + t0;
+      // Thread -> (segment ln, quarter q): steps 4q..4q+3 of segment ln, summed over copies.
+      for (int pos = tid; pos < 64 * (kT / 4); pos += kW * 64) {
+        const int ln = pos & 63, q = pos >> 6;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int off = n * 2 * kChunk + (4 * q + e) * 128 + which * 64 + ln;
+          float sum = 0.f;
+          for (int cp = 0; cp < n_copy; ++cp) {
+            sum += acc[cp * 2 * N * kChunk + off];
+            acc[cp * 2 * N * kChunk + off] = 0.f;
+          }
+          v[e] = sum;
+        }
+        const int toff = ln * kT + 4 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (t0 + toff + e < L) dst[toff + e] = v[e];
       }
-      const int t = t0 + toff;
-      if (t < L) part[which * nl + static_cast<size_t>(n) * L + t] = v;
     }
     __syncthreads();
   }
@@ -302,21 +329,42 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   }
 }
 
-// dB/dC[b][n][t] = sum over channel blocks of the partials, fixed order.
+// dB/dC[b][n][t] = sum over channel blocks of the partials, fixed order. Each thread
+// owns 4 consecutive elements (16-byte loads) and keeps 4 blocks' loads in flight.
 template <typename bc_t>
 __global__ __launch_bounds__(256) void reduce_bc_kernel(const float* __restrict__ part, int n_blk,
-                                                        int batch, size_t nl, bc_t* __restrict__ dB,
-                                                        bc_t* __restrict__ dC) {
+                                                        size_t stride, int batch, size_t nl,
+                                                        bc_t* __restrict__ dB, bc_t* __restrict__ dC) {
   const size_t total = static_cast<size_t>(batch) * 2 * nl;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
-    float s = 0.f;
-    for (int k = 0; k < n_blk; ++k) s += part[static_cast<size_t>(k) * total + i];
-    const size_t bb = i / (2 * nl);
-    const size_t rem = i - bb * 2 * nl;
-    const int which = rem >= nl;
-    const size_t off = bb * nl + (rem - which * nl);
-    store_as(which ? dC + off : dB + off, s);
+  const size_t nvec = (total + 3) / 4;    // the block stride is padded to a multiple of 4
+  const size_t svec = stride / 4;
+  for (size_t v = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; v < nvec;
+       v += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(part) + v;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    int k = 0;
+    for (; k + 4 <= n_blk; k += 4) {
+      const f32x4 a0 = src[static_cast<size_t>(k + 0) * svec];
+      const f32x4 a1 = src[static_cast<size_t>(k + 1) * svec];
+      const f32x4 a2 = src[static_cast<size_t>(k + 2) * svec];
+      const f32x4 a3 = src[static_cast<size_t>(k + 3) * svec];
+      s += a0;
+      s += a1;
+      s += a2;
+      s += a3;
+    }
+    for (; k < n_blk; ++k) s += src[static_cast<size_t>(k) * svec];
+    const float out[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const size_t i = 4 * v + e;
+      if (i >= total) break;  // padding of the last vector
+      const size_t bb = i / (2 * nl);
+      const size_t rem = i - bb * 2 * nl;
+      const int which = rem >= nl;
+      const size_t off = bb * nl + (rem - which * nl);
+      store_as(which ? dC + off : dB + off, out[e]);
+    }
   }
 }
 
@@ -387,14 +435,14 @@ hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB
                              float* dD, float* dbias, hipStream_t stream) {
   const size_t nl = static_cast<size_t>(p.dstate) * p.seqlen;
   const size_t total = static_cast<size_t>(p.batch) * 2 * nl;
-  int grid = static_cast<int>((total + 255) / 256);
+  int grid = static_cast<int>(((total + 3) / 4 + 255) / 256);
   if (grid > 4096) grid = 4096;
   if (bc_bf16) {
     hipLaunchKernelGGL(reduce_bc_kernel<bf16_t>, dim3(grid), dim3(256), 0, stream, p.part_dBC,
-                       p.n_blocks_d, p.batch, nl, static_cast<bf16_t*>(dB), static_cast<bf16_t*>(dC));
+                       p.n_blocks_d, p.part_stride, p.batch, nl, static_cast<bf16_t*>(dB), static_cast<bf16_t*>(dC));
   } else {
     hipLaunchKernelGGL(reduce_bc_kernel<float>, dim3(grid), dim3(256), 0, stream, p.part_dBC,
-                       p.n_blocks_d, p.batch, nl, static_cast<float*>(dB), static_cast<float*>(dC));
+                       p.n_blocks_d, p.part_stride, p.batch, nl, static_cast<float*>(dB), static_cast<float*>(dC));
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -58,6 +58,7 @@ int n_carry_of(int32_t seqlen) { return (seqlen + MSS_CARRY_CHUNK - 1) / MSS_CAR
 
 struct BwdLayout {
   int chan_per_block = 0, n_blocks_d = 0;
+  size_t part_stride = 0;  // floats per channel block of dB/dC partials (multiple of 64)
   size_t off_dA = 0, off_dD = 0, off_db = 0, total = 0;
 };
 
@@ -66,7 +67,8 @@ BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate)
   l.chan_per_block = mss::bwd_chan_per_block(batch, dim);
   l.n_blocks_d = (dim + l.chan_per_block - 1) / l.chan_per_block;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
-  const size_t bc = static_cast<size_t>(l.n_blocks_d) * batch * 2 * dstate * seqlen * sizeof(float);
+  l.part_stride = (static_cast<size_t>(batch) * 2 * dstate * seqlen + 63) / 64 * 64;
+  const size_t bc = static_cast<size_t>(l.n_blocks_d) * l.part_stride * sizeof(float);
   l.off_dA = up(bc);
   l.off_dD = l.off_dA + up(static_cast<size_t>(batch) * dim * dstate * sizeof(float));
   l.off_db = l.off_dD + up(static_cast<size_t>(batch) * dim * sizeof(float));
@@ -93,7 +95,7 @@ int validate_bwd(const mss_bwd_args* a) {
   if (!a->u || !a->delta || !a->A || !a->B || !a->C || !a->carries || !a->dout) return MSS_ERR_INVALID_ARGUMENT;
   if (!a->du || !a->ddelta || !a->dA || !a->dB || !a->dC) return MSS_ERR_INVALID_ARGUMENT;
   if (a->D && !a->dD) return MSS_ERR_INVALID_ARGUMENT;
-  if (a->z && !a->dz) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->z && (!a->dz || !a->y_pre)) return MSS_ERR_INVALID_ARGUMENT;
   if (a->delta_bias && !a->ddelta_bias) return MSS_ERR_INVALID_ARGUMENT;
   return MSS_OK;
 }
@@ -108,7 +110,7 @@ int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
   const size_t io_row = static_cast<size_t>(a->seqlen) * dtype_size(a->io_dtype);
   const size_t bc_row = static_cast<size_t>(a->seqlen) * dtype_size(a->bc_dtype);
   p.vec_io = (io_row % 16 == 0) && aligned16(a->u) && aligned16(a->delta) && aligned16(a->z) &&
-             aligned16(a->out);
+             aligned16(a->out) && aligned16(a->y_pre);
   p.vec_bc = (bc_row % 16 == 0) && aligned16(a->B) && aligned16(a->C);
   p.n_carry = n_carry_of(a->seqlen);
   p.n_ref = (a->seqlen + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK;
@@ -126,6 +128,7 @@ int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
   p.last = a->last_state;
   p.carries = a->carries;
   p.ref_states = ref_states;
+  p.y_pre = a->z ? a->y_pre : nullptr;
   const hipError_t e = mss::launch_fwd(p, a->discretization == MSS_ZOH, a->io_dtype == MSS_BF16,
                                        a->bc_dtype == MSS_BF16, stream);
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching selective scan forward");
@@ -143,7 +146,8 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   const size_t io_row = static_cast<size_t>(a->seqlen) * dtype_size(a->io_dtype);
   const size_t bc_row = static_cast<size_t>(a->seqlen) * dtype_size(a->bc_dtype);
   p.vec_io = (io_row % 16 == 0) && aligned16(a->u) && aligned16(a->delta) && aligned16(a->z) &&
-             aligned16(a->dout) && aligned16(a->du) && aligned16(a->ddelta) && aligned16(a->dz);
+             aligned16(a->dout) && aligned16(a->du) && aligned16(a->ddelta) && aligned16(a->dz) &&
+             aligned16(a->y_pre);
   p.vec_bc = (bc_row % 16 == 0) && aligned16(a->B) && aligned16(a->C);
   p.n_carry = n_carry_of(a->seqlen);
   p.chan_per_block = l.chan_per_block;
@@ -159,6 +163,7 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   p.x0 = a->initial_state;
   p.seq_lens = a->seq_lens;
   p.carries = a->carries;
+  p.y_pre = a->y_pre;
   p.dout = a->dout;
   p.dlast = a->dlast_state;
   p.du = a->du;
@@ -166,6 +171,7 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   p.dz = a->dz;
   p.dinit = a->dinitial_state;
   p.part_dBC = reinterpret_cast<float*>(ws);
+  p.part_stride = l.part_stride;
   p.part_dA = reinterpret_cast<float*>(ws + l.off_dA);
   p.part_dD = reinterpret_cast<float*>(ws + l.off_dD);
   p.part_dbias = reinterpret_cast<float*>(ws + l.off_db);

@@ -61,41 +61,37 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// One Hillis-Steele step of an affine scan with the lane shift fused into the ALU ops:
+//   H = P * H[src] + H ;  P = P[src] * P      (lanes without a source keep their values)
+// `s_nop 1` supplies the two wait states a DPP read needs after a VALU write of its
+// source register (also covering writes just before/after the asm block).
+#define MSS_DPP_AFFINE_STEP(CTRL, RM, H, P)                                            \
+  asm volatile("s_nop 1\n\t"                                                          \
+               "v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
+               "s_nop 1\n\t"                                                          \
+               "v_mul_f32_dpp %1, %1, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
+               "s_nop 1"                                                              \
+               : "+v"(H), "+v"(P))
+
 // Inclusive scan over the 64 lanes (lane order = time order) of affine maps
 // h -> P*h + H. Combining an earlier element (Pl, Hl) with a later one (Pr, Hr) gives
 // (Pl*Pr, Pr*Hl + Hr): the operator of reference native/selective_scan_cuda.cu:58-63.
 __device__ __forceinline__ void wave_scan_affine_fwd(float& P, float& H) {
-#define MSS_FWD_STEP(CTRL, RM)                   \
-  {                                              \
-    const float ps = dpp_mov<CTRL, RM>(1.f, P);  \
-    const float hs = dpp_mov<CTRL, RM>(0.f, H);  \
-    H = __builtin_fmaf(P, hs, H);                \
-    P = P * ps;                                  \
-  }
-  MSS_FWD_STEP(kRowShr1, 0xF)
-  MSS_FWD_STEP(kRowShr2, 0xF)
-  MSS_FWD_STEP(kRowShr4, 0xF)
-  MSS_FWD_STEP(kRowShr8, 0xF)
-  MSS_FWD_STEP(kRowBcast15, 0xA)
-  MSS_FWD_STEP(kRowBcast31, 0xC)
-#undef MSS_FWD_STEP
+  MSS_DPP_AFFINE_STEP("row_shr:1", "0xf", H, P);
+  MSS_DPP_AFFINE_STEP("row_shr:2", "0xf", H, P);
+  MSS_DPP_AFFINE_STEP("row_shr:4", "0xf", H, P);
+  MSS_DPP_AFFINE_STEP("row_shr:8", "0xf", H, P);
+  MSS_DPP_AFFINE_STEP("row_bcast:15", "0xa", H, P);
+  MSS_DPP_AFFINE_STEP("row_bcast:31", "0xc", H, P);
 }
 
 // Inclusive reverse scan (lane 63 is applied first) of affine maps m -> a*m + b:
 // lane i ends with R_i = f_i o f_{i+1} o ... o f_63.
 __device__ __forceinline__ void wave_scan_affine_rev(float& a, float& b, int lane) {
-#define MSS_REV_STEP(CTRL)                        \
-  {                                               \
-    const float as = dpp_mov<CTRL, 0xF>(1.f, a);  \
-    const float bs = dpp_mov<CTRL, 0xF>(0.f, b);  \
-    b = __builtin_fmaf(a, bs, b);                 \
-    a = a * as;                                   \
-  }
-  MSS_REV_STEP(kRowShl1)
-  MSS_REV_STEP(kRowShl2)
-  MSS_REV_STEP(kRowShl4)
-  MSS_REV_STEP(kRowShl8)
-#undef MSS_REV_STEP
+  MSS_DPP_AFFINE_STEP("row_shl:1", "0xf", b, a);
+  MSS_DPP_AFFINE_STEP("row_shl:2", "0xf", b, a);
+  MSS_DPP_AFFINE_STEP("row_shl:4", "0xf", b, a);
+  MSS_DPP_AFFINE_STEP("row_shl:8", "0xf", b, a);
   // Row r (lanes 16r..16r+15) now holds suffixes within the row; lane 16r holds the
   // whole row's map. Compose with the rows to the right.
   const float a1 = readlane(a, 16), b1 = readlane(b, 16);
@@ -157,53 +153,14 @@ __device__ __forceinline__ float sigmoid(float x) {
 }
 
 // ---------------------------------------------------------------------------------
-// Segment loads/stores. `row` points at element 0 of a [.. ][L] row; the segment is
-// elements [t, t+N). Elements at or beyond `L` read as 0 and are not written.
+// Segment loads/stores. `row` points at element 0 of a [..][L] row; the segment is
+// elements [t, t+N). `fast` must be wave-uniform: true when 16-byte vector access is
+// legal for the row and the whole wave's chunk lies inside [0, L); otherwise elements at
+// or beyond `L` read as 0 and are not written.
 template <int N>
-__device__ __forceinline__ void load_seg(const float* __restrict__ row, int t, int L, bool vec,
+__device__ __forceinline__ void load_seg(const float* __restrict__ row, int t, int L, bool fast,
                                          float (&v)[N]) {
-  if (vec && t + N <= L) {
-    const f32x4* p = reinterpret_cast<const f32x4*>(row + t);
-#pragma unroll
-    for (int q = 0; q < N / 4; ++q) {
-      const f32x4 x = __builtin_nontemporal_load(p + q);
-      v[4 * q + 0] = x.x;
-      v[4 * q + 1] = x.y;
-      v[4 * q + 2] = x.z;
-      v[4 * q + 3] = x.w;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < N; ++j) v[j] = (t + j < L) ? row[t + j] : 0.f;
-  }
-}
-
-template <int N>
-__device__ __forceinline__ void load_seg(const bf16_t* __restrict__ row, int t, int L, bool vec,
-                                         float (&v)[N]) {
-  if (vec && t + N <= L) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(row + t);
-#pragma unroll
-    for (int q = 0; q < N / 8; ++q) {
-      const u32x4 x = __builtin_nontemporal_load(p + q);
-      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[8 * q + 2 * k + 0] = __uint_as_float(w[k] << 16);
-        v[8 * q + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < N; ++j) v[j] = (t + j < L) ? to_f32(row[t + j]) : 0.f;
-  }
-}
-
-// Cached (non-streaming) variant for rows many waves re-read (B, C).
-template <int N>
-__device__ __forceinline__ void load_seg_cached(const float* __restrict__ row, int t, int L, bool vec,
-                                                float (&v)[N]) {
-  if (vec && t + N <= L) {
+  if (fast) {
     const f32x4* p = reinterpret_cast<const f32x4*>(row + t);
 #pragma unroll
     for (int q = 0; q < N / 4; ++q) {
@@ -220,9 +177,9 @@ __device__ __forceinline__ void load_seg_cached(const float* __restrict__ row, i
 }
 
 template <int N>
-__device__ __forceinline__ void load_seg_cached(const bf16_t* __restrict__ row, int t, int L, bool vec,
-                                                float (&v)[N]) {
-  if (vec && t + N <= L) {
+__device__ __forceinline__ void load_seg(const bf16_t* __restrict__ row, int t, int L, bool fast,
+                                         float (&v)[N]) {
+  if (fast) {
     const u32x4* p = reinterpret_cast<const u32x4*>(row + t);
 #pragma unroll
     for (int q = 0; q < N / 8; ++q) {
@@ -241,14 +198,14 @@ __device__ __forceinline__ void load_seg_cached(const bf16_t* __restrict__ row, 
 }
 
 template <int N>
-__device__ __forceinline__ void store_seg(float* __restrict__ row, int t, int L, bool vec,
+__device__ __forceinline__ void store_seg(float* __restrict__ row, int t, int L, bool fast,
                                           const float (&v)[N]) {
-  if (vec && t + N <= L) {
+  if (fast) {
     f32x4* p = reinterpret_cast<f32x4*>(row + t);
 #pragma unroll
     for (int q = 0; q < N / 4; ++q) {
       const f32x4 x = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-      __builtin_nontemporal_store(x, p + q);
+      p[q] = x;
     }
   } else {
 #pragma unroll
@@ -258,9 +215,9 @@ __device__ __forceinline__ void store_seg(float* __restrict__ row, int t, int L,
 }
 
 template <int N>
-__device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L, bool vec,
+__device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L, bool fast,
                                           const float (&v)[N]) {
-  if (vec && t + N <= L) {
+  if (fast) {
     u32x4* p = reinterpret_cast<u32x4*>(row + t);
 #pragma unroll
     for (int q = 0; q < N / 8; ++q) {
@@ -271,76 +228,12 @@ __device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L
                (static_cast<uint32_t>(f32_to_bf16(v[8 * q + 2 * k + 1]).bits) << 16);
       }
       const u32x4 x = {w[0], w[1], w[2], w[3]};
-      __builtin_nontemporal_store(x, p + q);
+      p[q] = x;
     }
   } else {
 #pragma unroll
     for (int j = 0; j < N; ++j)
       if (t + j < L) store_as(row + t + j, v[j]);
-  }
-}
-
-// Stage elements [t0, t0 + 64*kT) of a [..][L] row into LDS with a padded segment
-// stride of (kT + 4) floats (lane-strided reads then hit distinct banks). Cooperative
-// over `nthreads` threads starting at `tid`.
-template <int kT>
-__device__ __forceinline__ void stage_row(const float* __restrict__ row, int t0, int L, bool vec,
-                                          float* __restrict__ lds, int tid, int nthreads) {
-  constexpr int kChunk = 64 * kT;
-  constexpr int kStride = kT + 4;
-  if (vec && t0 + kChunk <= L) {
-    const float4* p = reinterpret_cast<const float4*>(row + t0);
-    for (int q = tid; q < kChunk / 4; q += nthreads) {
-      const float4 x = p[q];
-      const int e = 4 * q;
-      *reinterpret_cast<float4*>(lds + (e / kT) * kStride + (e % kT)) = x;
-    }
-  } else {
-    for (int e = tid; e < kChunk; e += nthreads) {
-      const int t = t0 + e;
-      lds[(e / kT) * kStride + (e % kT)] = t < L ? row[t] : 0.f;
-    }
-  }
-}
-
-template <int kT>
-__device__ __forceinline__ void stage_row(const bf16_t* __restrict__ row, int t0, int L, bool vec,
-                                          float* __restrict__ lds, int tid, int nthreads) {
-  constexpr int kChunk = 64 * kT;
-  constexpr int kStride = kT + 4;
-  if (vec && t0 + kChunk <= L) {
-    const uint4* p = reinterpret_cast<const uint4*>(row + t0);
-    for (int q = tid; q < kChunk / 8; q += nthreads) {
-      const uint4 x = p[q];
-      const int e = 8 * q;
-      float* dst = lds + (e / kT) * kStride + (e % kT);
-      *reinterpret_cast<float4*>(dst) =
-          make_float4(__uint_as_float(x.x << 16), __uint_as_float(x.x & 0xffff0000u),
-                      __uint_as_float(x.y << 16), __uint_as_float(x.y & 0xffff0000u));
-      *reinterpret_cast<float4*>(dst + 4) =
-          make_float4(__uint_as_float(x.z << 16), __uint_as_float(x.z & 0xffff0000u),
-                      __uint_as_float(x.w << 16), __uint_as_float(x.w & 0xffff0000u));
-    }
-  } else {
-    for (int e = tid; e < kChunk; e += nthreads) {
-      const int t = t0 + e;
-      lds[(e / kT) * kStride + (e % kT)] = t < L ? to_f32(row[t]) : 0.f;
-    }
-  }
-}
-
-// Read a lane's kT staged values (16-byte LDS reads).
-template <int kT>
-__device__ __forceinline__ void lds_read_seg(const float* __restrict__ lds, int lane,
-                                             float (&v)[kT]) {
-  const float4* p = reinterpret_cast<const float4*>(lds + lane * (kT + 4));
-#pragma unroll
-  for (int q = 0; q < kT / 4; ++q) {
-    const float4 x = p[q];
-    v[4 * q + 0] = x.x;
-    v[4 * q + 1] = x.y;
-    v[4 * q + 2] = x.z;
-    v[4 * q + 3] = x.w;
   }
 }
 
@@ -367,6 +260,7 @@ struct FwdParams {
   float* last;
   float* carries;
   float* ref_states;
+  void* y_pre;
 };
 
 struct BwdParams {
@@ -387,6 +281,7 @@ struct BwdParams {
   const float* x0;
   const int* seq_lens;
   const float* carries;
+  const void* y_pre;
   const void* dout;
   const float* dlast;
   void* du;
@@ -394,7 +289,8 @@ struct BwdParams {
   void* dz;
   float* dinit;
   // workspace partials
-  float* part_dBC;   // [n_blocks_d][batch][2][dstate][L]
+  float* part_dBC;   // [n_blocks_d][part_stride]; block = [batch][2][dstate][L] (+ padding)
+  size_t part_stride;  // floats per channel block, a multiple of 64
   float* part_dA;    // [batch][dim][dstate]
   float* part_dD;    // [batch][dim]
   float* part_dbias; // [batch][dim]

@@ -18,6 +18,21 @@
 // of two buffers while the previous round is computed (one barrier per round).
 #include "mss_common.h"
 
+// Launch shape (steps per lane, waves per workgroup, states per staging round, waves per
+// SIMD the register allocation targets); overridable at build time for tuning sweeps.
+#ifndef MSS_FWD_T
+#define MSS_FWD_T 16
+#endif
+#ifndef MSS_FWD_W
+#define MSS_FWD_W 8
+#endif
+#ifndef MSS_FWD_NB
+#define MSS_FWD_NB 4
+#endif
+#ifndef MSS_FWD_OCC
+#define MSS_FWD_OCC 4
+#endif
+
 namespace mss {
 
 typedef __attribute__((address_space(3))) void* lds_void_t;
@@ -63,52 +78,65 @@ __device__ __forceinline__ void read_staged(const uint4* __restrict__ row, int l
   }
 }
 
-// Stage elements [t0, t0 + 64*kT) of one row into `dst` (64*kT elements of bc_t).
+// Stage elements [t0, t0 + 64*kT) of `nrows` rows (B rows of states n0.., then C rows)
+// into dst[row][slot] (64*kT elements of bc_t per row), spread over all threads.
 // dma: rows are 16-byte aligned and L is a multiple of the slot width, so each slot is
 // either fully inside [0, L) or fully past it; past-the-end slots re-read the last valid
 // slot (finite values; they only meet zero coefficients).
-template <int kT, int kW, typename bc_t>
-__device__ __forceinline__ void stage_row_async(const bc_t* __restrict__ row, int t0, int L, bool dma,
-                                                uint4* __restrict__ dst, int tid) {
+template <int kT, int kW, int kNB, typename bc_t>
+__device__ __forceinline__ void stage_round(const bc_t* __restrict__ Bb, const bc_t* __restrict__ Cb,
+                                            int n0, int nb, int t0, int L, bool dma,
+                                            uint4 (*dst)[2][64 * kT * sizeof(bc_t) / 16], int tid) {
   constexpr int kE = BcStage<bc_t>::kElemsPerSlot;
   constexpr int kQ = kT / kE;
-  constexpr int kSlots = 64 * kQ;
+  constexpr int kSlots = 64 * kQ;  // per row
+  const int total = nb * 2 * kSlots;
   if (dma) {
     const int lane = tid & 63;
     const int w = tid >> 6;
-    for (int s0 = w * 64; s0 < kSlots; s0 += kW * 64) {
+    // Lane's source offset inside a row for slot s0 + lane: the same for every row.
+    for (int f0 = w * 64; f0 < total; f0 += kW * 64) {
+      const int rowi = f0 / kSlots;  // uniform: kSlots is a multiple of 64
+      const int k = rowi >> 1;
+      const int which = rowi & 1;
+      const int s0 = f0 - rowi * kSlots;
       const int s = s0 + lane;
-      const int i = s / kQ;
+      const int i = s / kQ;  // kQ is a power of two
       const int q = (s % kQ) ^ slot_swz<kQ>(i);
       int e = t0 + i * kT + q * kE;
       e = e < L ? e : L - kE;
-      __builtin_amdgcn_global_load_lds((gbl_void_t)(row + e), (lds_void_t)(dst + s0), 16, 0, 0);
+      const bc_t* src = (which ? Cb : Bb) + static_cast<size_t>(n0 + k) * L + e;
+      __builtin_amdgcn_global_load_lds((gbl_void_t)src, (lds_void_t)(&dst[k][which][s0]), 16, 0, 0);
     }
   } else {
-    bc_t* d = reinterpret_cast<bc_t*>(dst);
-    for (int e = tid; e < 64 * kT; e += kW * 64) {
+    for (int f = tid; f < nb * 2 * 64 * kT; f += kW * 64) {
+      const int rowi = f / (64 * kT);
+      const int k = rowi >> 1;
+      const int which = rowi & 1;
+      const int e = f - rowi * 64 * kT;
       const int i = e / kT;
       const int r = e % kT;
       const int q = r / kE;
-      const int s = kQ * i + (q ^ slot_swz<kQ>(i));
+      const int sl = kQ * i + (q ^ slot_swz<kQ>(i));
       const int t = t0 + e;
+      const bc_t* src = (which ? Cb : Bb) + static_cast<size_t>(n0 + k) * L;
       bc_t v;
       if (t < L) {
-        v = row[t];
+        v = src[t];
       } else {
         store_as(&v, 0.f);
       }
-      d[s * kE + (r % kE)] = v;
+      reinterpret_cast<bc_t*>(&dst[k][which][0])[sl * kE + (r % kE)] = v;
     }
   }
 }
 
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int kT, int kW, bool kZOH, typename io_t, typename bc_t>
-__global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
+template <int kT, int kW, int kNB, bool kZOH, typename io_t, typename bc_t>
+__global__ __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(MSS_FWD_OCC, MSS_FWD_OCC)))
+void fwd_kernel(FwdParams p) {
   constexpr int kChunk = 64 * kT;
-  constexpr int kNB = 2;  // states staged per round
   constexpr int kRowSlots = kChunk * static_cast<int>(sizeof(bc_t)) / 16;
   // Two stage buffers as distinct objects, selected statically (rounds run in pairs), so
   // the compiler can tell the in-flight copy into one from the reads of the other.
@@ -158,16 +186,20 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
     const int c = r / rounds;
     const int n0 = (r - c * rounds) * kNB;
     const int nb = min(kNB, N - n0);
-    for (int k = 0; k < nb; ++k) {
-      stage_row_async<kT, kW, bc_t>(Bb + static_cast<size_t>(n0 + k) * L, c * kChunk, L, dma, buf[k][0], tid);
-      stage_row_async<kT, kW, bc_t>(Cb + static_cast<size_t>(n0 + k) * L, c * kChunk, L, dma, buf[k][1], tid);
-    }
+    if (nb > 0) stage_round<kT, kW, kNB, bc_t>(Bb, Cb, n0, nb, c * kChunk, L, dma, buf, tid);
   };
   if (n_active_chunks > 0) issue_round(0, stage0);
 
   for (int c = 0; c < n_chunks; ++c) {
     const int t0 = c * kChunk;
     const int tl = t0 + lane * kT;
+    const bool fast = vec_io && (t0 + kChunk <= L);  // wave-uniform
+    // Reference residual slot written at this chunk's end (2048-step boundary or end of
+    // the sequence), -1 if none.
+    const int chunk_end = t0 + kChunk;
+    const int ref_idx = (chunk_end % kRefChunk == 0 || c == n_chunks - 1)
+                            ? min((chunk_end + kRefChunk - 1) / kRefChunk, p.n_ref) - 1
+                            : -1;
 
     if (c >= n_active_chunks) {
       // Entire chunk is past this row's length: state frozen, output zero.
@@ -175,15 +207,16 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
         float zero[kT];
 #pragma unroll
         for (int j = 0; j < kT; ++j) zero[j] = 0.f;
-        if (p.out) store_seg<kT>(out_row, tl, L, vec_io, zero);
+        if (p.out) store_seg<kT>(out_row, tl, L, fast, zero);
+        if (p.out && p.z && p.y_pre) store_seg<kT>(static_cast<io_t*>(p.y_pre) + row, tl, L, fast, zero);
         const int cidx = (tl + kT) / kCarryChunk - 1;
         if (p.carries && ((tl + kT) % kCarryChunk == 0) && cidx < p.n_carry) {
           for (int n = 0; n < N; ++n)
             p.carries[(chan * p.n_carry + cidx) * N + n] = s_run[w][n];
         }
-        if (p.ref_states && lane == 63 && c < p.n_ref) {
+        if (p.ref_states && lane == 63 && ref_idx >= 0) {
           for (int n = 0; n < N; ++n) {
-            float* rs = p.ref_states + ((chan * p.n_ref + c) * N + n) * 2;
+            float* rs = p.ref_states + ((chan * p.n_ref + ref_idx) * N + n) * 2;
             rs[0] = fast_exp2(s_a2[w][n] * dsum_total);
             rs[1] = s_run[w][n];
           }
@@ -196,8 +229,8 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
     float dlt[kT], dlu[kT], y[kT];
     float ssum = 0.f;
     if (active) {
-      load_seg<kT>(dl_row, tl, L, vec_io, dlt);
-      load_seg<kT>(u_row, tl, L, vec_io, y);
+      load_seg<kT>(dl_row, tl, L, fast, dlt);
+      load_seg<kT>(u_row, tl, L, fast, y);
 #pragma unroll
       for (int j = 0; j < kT; ++j) {
         const bool valid = tl + j < len;
@@ -260,8 +293,8 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
           const int cidx = (tl + kT) / kCarryChunk - 1;
           if (cidx < p.n_carry) p.carries[(chan * p.n_carry + cidx) * N + n] = hend;
         }
-        if (p.ref_states && lane == 63 && (tl + kT) % kRefChunk == 0) {
-          float* rs = p.ref_states + ((chan * p.n_ref + (tl + kT) / kRefChunk - 1) * N + n) * 2;
+        if (p.ref_states && lane == 63 && ref_idx >= 0) {
+          float* rs = p.ref_states + ((chan * p.n_ref + ref_idx) * N + n) * 2;
           rs[0] = fast_exp2(a2 * dsum_total);
           rs[1] = hend;
         }
@@ -283,28 +316,34 @@ __global__ __launch_bounds__(kW * 64) void fwd_kernel(FwdParams p) {
 
     if (active && p.out) {
       if (p.z) {
+        if (p.y_pre) {
+          float yp[kT];
+#pragma unroll
+          for (int j = 0; j < kT; ++j) yp[j] = (tl + j < len) ? y[j] : 0.f;
+          store_seg<kT>(static_cast<io_t*>(p.y_pre) + row, tl, L, fast, yp);
+        }
         float zv[kT];
-        load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, vec_io, zv);
+        load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zv);
 #pragma unroll
         for (int j = 0; j < kT; ++j) y[j] *= zv[j] * sigmoid(zv[j]);
       }
 #pragma unroll
       for (int j = 0; j < kT; ++j) y[j] = (tl + j < len) ? y[j] : 0.f;
-      store_seg<kT>(out_row, tl, L, vec_io, y);
+      store_seg<kT>(out_row, tl, L, fast, y);
     }
   }
 }
 
-template <int kT, int kW, bool kZOH, typename io_t, typename bc_t>
+template <int kT, int kW, int kNB, bool kZOH, typename io_t, typename bc_t>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   dim3 grid((p.dim + kW - 1) / kW, p.batch);
-  hipLaunchKernelGGL((fwd_kernel<kT, kW, kZOH, io_t, bc_t>), grid, dim3(kW * 64), 0, stream, p);
+  hipLaunchKernelGGL((fwd_kernel<kT, kW, kNB, kZOH, io_t, bc_t>), grid, dim3(kW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
 template <bool kZOH, typename io_t, typename bc_t>
 static hipError_t launch_fwd_z(const FwdParams& p, hipStream_t stream) {
-  return launch_fwd_t<32, 4, kZOH, io_t, bc_t>(p, stream);
+  return launch_fwd_t<MSS_FWD_T, MSS_FWD_W, MSS_FWD_NB, kZOH, io_t, bc_t>(p, stream);
 }
 
 hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream) {

@@ -51,7 +51,7 @@ class FwdArgs(ctypes.Structure):
         ("discretization", _i32), ("delta_softplus", _i32), ("io_dtype", _i32), ("bc_dtype", _i32),
         ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
         ("D", _p), ("z", _p), ("delta_bias", _p), ("initial_state", _p), ("seq_lens", _p),
-        ("out", _p), ("last_state", _p), ("carries", _p),
+        ("out", _p), ("last_state", _p), ("carries", _p), ("y_pre", _p),
     ]
 
 
@@ -61,7 +61,7 @@ class BwdArgs(ctypes.Structure):
         ("discretization", _i32), ("delta_softplus", _i32), ("io_dtype", _i32), ("bc_dtype", _i32),
         ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
         ("D", _p), ("z", _p), ("delta_bias", _p), ("initial_state", _p), ("seq_lens", _p),
-        ("carries", _p), ("dout", _p), ("dlast_state", _p),
+        ("carries", _p), ("y_pre", _p), ("dout", _p), ("dlast_state", _p),
         ("du", _p), ("ddelta", _p), ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("dz", _p),
         ("ddelta_bias", _p), ("dinitial_state", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),

@@ -117,6 +117,8 @@ class _SelectiveScan(torch.autograd.Function):
         out = torch.empty_like(u)
         last = torch.empty(batch, dim, n, device=u.device, dtype=torch.float32)
         carries = torch.empty(batch, dim, n_carry, n, device=u.device, dtype=torch.float32)
+        # Pre-gate output: the backward's dz needs it (kept only when z is given).
+        y_pre = torch.empty_like(u) if z is not None else None
         args = _lib.FwdArgs(
             batch=batch, dim=dim, seqlen=length, dstate=n,
             discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER,
@@ -124,19 +126,18 @@ class _SelectiveScan(torch.autograd.Function):
             io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
             u=_ptr(u), delta=_ptr(delta), A=_ptr(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
             delta_bias=_ptr(delta_bias), initial_state=_ptr(initial_state), seq_lens=_ptr(seq_lens),
-            out=_ptr(out), last_state=_ptr(last), carries=_ptr(carries),
+            out=_ptr(out), last_state=_ptr(last), carries=_ptr(carries), y_pre=_ptr(y_pre),
         )
         _lib.check(lib.mss_fwd(args, _stream(u)), "mss_fwd")
-        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries)
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre)
         ctx.delta_softplus = bool(delta_softplus)
         ctx.zoh = bool(zoh)
-        ctx.mark_non_differentiable(carries)
         return out, last
 
     @staticmethod
     def backward(ctx, dout, dlast):
         lib = register_hip_kernel()
-        u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries = ctx.saved_tensors
+        u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre = ctx.saved_tensors
         batch, dim, length = u.shape
         n = A.shape[1]
         dout = dout.to(u.dtype).contiguous()
@@ -157,7 +158,7 @@ class _SelectiveScan(torch.autograd.Function):
             io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
             u=_ptr(u), delta=_ptr(delta), A=_ptr(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
             delta_bias=_ptr(delta_bias), initial_state=_ptr(initial_state), seq_lens=_ptr(seq_lens),
-            carries=_ptr(carries), dout=_ptr(dout), dlast_state=_ptr(dlast),
+            carries=_ptr(carries), y_pre=_ptr(y_pre), dout=_ptr(dout), dlast_state=_ptr(dlast),
             du=_ptr(du), ddelta=_ptr(ddelta), dA=_ptr(dA), dB=_ptr(dB), dC=_ptr(dC), dD=_ptr(dD),
             dz=_ptr(dz), ddelta_bias=_ptr(dbias), dinitial_state=_ptr(dinit),
         )
