@@ -156,7 +156,13 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       }
 
       // States in a per-wave rotated order (see the accumulator above); the barrier per
-      // iteration keeps every wave inside the same iteration.
+      // iteration keeps every wave inside the same iteration. B/C rows of the next state are
+      // requested at the end of each iteration, into the registers of the current ones.
+      float bv[kT], cv[kT];
+      if (active) {
+        load_seg<kT>(Bb + static_cast<size_t>(w_mod_n) * L, tl, L, fast_bc, bv);
+        load_seg<kT>(Cb + static_cast<size_t>(w_mod_n) * L, tl, L, fast_bc, cv);
+      }
       for (int i = 0; i < N; ++i) {
         int n = i + w_mod_n;
         n = n >= N ? n - N : n;
@@ -173,9 +179,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         }
         const float An = s_a[w][n];
         const float a2 = An * kLog2e;
-        float bv[kT], cv[kT], a[kT];
-        load_seg<kT>(Bb + static_cast<size_t>(n) * L, tl, L, fast_bc, bv);
-        load_seg<kT>(Cb + static_cast<size_t>(n) * L, tl, L, fast_bc, cv);
+        float a[kT];
         // ---- forward: local aggregate, scan, re-run from the true carry-in
         float H = 0.f;
 #pragma unroll
@@ -239,6 +243,11 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         for (int j = 0; j < kT; ++j) {
           accn[j * 128] = accv[2 * j];
           accn[j * 128 + 64] = accv[2 * j + 1];
+        }
+        if (i + 1 < N) {
+          const int nn = n + 1 == N ? 0 : n + 1;
+          load_seg<kT>(Bb + static_cast<size_t>(nn) * L, tl, L, fast_bc, bv);
+          load_seg<kT>(Cb + static_cast<size_t>(nn) * L, tl, L, fast_bc, cv);
         }
         const float dA_sum = wave_sum(dA_acc);
         if (lane == 0) {
