@@ -193,6 +193,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="approximate CPU work for the CPU baseline (0 disables it)")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after the timed region, copy a device buffer of this many MiB twice "
+                         "(a kernel of known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -220,6 +223,14 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(tag),
                 "kernel": tag, "algorithmic_bytes": bytes_, "avg_launch_ms": round(dur, 5)}
+    if args.calibration_copy_mib > 0:
+        src = torch.ones(args.calibration_copy_mib * (1 << 20) // 4, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy of {args.calibration_copy_mib} MiB done")
+        del src, dst
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, cfg, args.cpu_seconds)

@@ -13,6 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
+MSS_ABI_VERSION = 1
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -113,6 +114,9 @@ def register_hip_kernel(library_path=None):
     lib.mss_last_hip_error.restype = ctypes.c_char_p
     lib.mss_abi_version.argtypes = []
     lib.mss_abi_version.restype = ctypes.c_int
+    if lib.mss_abi_version() != MSS_ABI_VERSION:
+        raise ImportError(f"{path} has ABI version {lib.mss_abi_version()}, this front-end "
+                          f"expects {MSS_ABI_VERSION}; rebuild the library")
     _LIBRARY = lib
     _LIBRARY_PATH = path
     return lib
