@@ -4,9 +4,12 @@
  * Library: libmamba_selective_scan_hip.so (built from jax-mambas_amd/csrc/).
  *
  * Everything here is plain C: pointers, sizes and int32 flags. Tensors are device
- * pointers, contiguous, in the physical layout the reference's kernel boundary uses
- * (reference mamba/selective_scan_cuda.py:135-147 declares XLA layouts (0,2,1), i.e.
- * channel-major [B][D][L] for u/delta/z/out and [B][N][L] for B/C):
+ * pointers in the physical layout the reference's kernel boundary uses (reference
+ * mamba/selective_scan_cuda.py:135-147 declares XLA layouts (0,2,1), i.e. channel-major
+ * [B][D][L] for u/delta/z/out and [B][N][L] for B/C). The fused entry points also take
+ * row strides (mss_strides): steps are always contiguous, but rows may be laid out as
+ * e.g. [D][B][L] — the layout of a (D, B*L) activation matrix, which lets a model keep
+ * every projection a plain 2-D GEMM with no transposes around the scan:
  *
  *   u, delta, z, out, du, ddelta, dz, dout : [batch][dim][seqlen]
  *   B, C, dB, dC                          : [batch][dstate][seqlen]
@@ -41,7 +44,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 1
+#define MSS_ABI_VERSION 2
 #define MSS_MAX_DSTATE 16
 #define MSS_CARRY_CHUNK 1024 /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
@@ -56,6 +59,15 @@ typedef enum mss_status {
 
 typedef enum mss_dtype { MSS_F32 = 0, MSS_BF16 = 1 } mss_dtype;
 typedef enum mss_discretization { MSS_EULER = 0, MSS_ZOH = 1 } mss_discretization;
+
+/* Row strides, in elements, of the fused entry points' tensors. The step axis is always
+ * contiguous. 0 selects the contiguous default. Rows must not overlap. */
+typedef struct mss_strides {
+  int64_t io_batch; /* u, delta, z, out, y_pre, dout, du, ddelta, dz: (b,d)->(b+1,d); default dim*seqlen */
+  int64_t io_dim;   /* (b,d) -> (b,d+1); default seqlen */
+  int64_t bc_batch; /* B, C, dB, dC: (b,n) -> (b+1,n); default dstate*seqlen */
+  int64_t bc_state; /* (b,n) -> (b,n+1); default seqlen */
+} mss_strides;
 
 /* Forward of the fused scan (no counterpart symbol in the reference: it generalises
  * MambaSelectiveScan, native/selective_scan_cuda.cu:554-573, with the fusions the
@@ -79,8 +91,9 @@ typedef struct mss_fwd_args {
   void* out;
   float* last_state; /* optional */
   float* carries;    /* optional; required by mss_bwd */
-  void* y_pre;       /* optional [B][D][L] (io dtype): y before the silu(z) gate, the
-                        residual mss_bwd needs when z is given */
+  void* y_pre;       /* optional [B][D][L] (io dtype, io strides): y before the silu(z)
+                        gate, the residual mss_bwd needs when z is given */
+  mss_strides strides;
 } mss_fwd_args;
 
 /* Backward of the fused scan. Outputs are fully overwritten (no accumulation).
@@ -117,6 +130,7 @@ typedef struct mss_bwd_args {
   float* dinitial_state; /* optional */
   void* workspace;       /* device scratch; NULL = library allocates stream-ordered */
   size_t workspace_bytes;
+  mss_strides strides;   /* the forward's strides; also those of dout/du/ddelta/dz, dB/dC */
 } mss_bwd_args;
 
 /* Size of the scratch mss_bwd needs for these shapes (0 on invalid arguments). */

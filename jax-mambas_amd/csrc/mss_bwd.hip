@@ -57,8 +57,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   const int len = p.seq_lens ? min(max(p.seq_lens[b], 0), L) : L;
   const bool vec_io = p.vec_io != 0;
   const bool vec_bc = p.vec_bc != 0;
-  const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + static_cast<size_t>(b) * N * L;
-  const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + static_cast<size_t>(b) * N * L;
+  const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + b * p.bc_sb;
+  const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + b * p.bc_sb;
 
   const int n_copy = (kW + N - 1) / N;  // n_copy * N <= 2 * kMaxN for N <= kMaxN
   const int w_mod_n = w % N;
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       const bool active = d_raw < p.dim;
       const int d = active ? d_raw : p.dim - 1;
       const size_t chan = static_cast<size_t>(b) * p.dim + d;
-      const size_t row = chan * L;
+      const long long row = b * p.io_sb + d * p.io_sd;
       io_t* __restrict__ du_row = static_cast<io_t*>(p.du) + row;
       io_t* __restrict__ dd_row = static_cast<io_t*>(p.ddelta) + row;
 
@@ -160,8 +160,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       // requested at the end of each iteration, into the registers of the current ones.
       float bv[kT], cv[kT];
       if (active) {
-        load_seg<kT>(Bb + static_cast<size_t>(w_mod_n) * L, tl, L, fast_bc, bv);
-        load_seg<kT>(Cb + static_cast<size_t>(w_mod_n) * L, tl, L, fast_bc, cv);
+        load_seg<kT>(Bb + w_mod_n * p.bc_sn, tl, L, fast_bc, bv);
+        load_seg<kT>(Cb + w_mod_n * p.bc_sn, tl, L, fast_bc, cv);
       }
       for (int i = 0; i < N; ++i) {
         int n = i + w_mod_n;
@@ -246,8 +246,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         }
         if (i + 1 < N) {
           const int nn = n + 1 == N ? 0 : n + 1;
-          load_seg<kT>(Bb + static_cast<size_t>(nn) * L, tl, L, fast_bc, bv);
-          load_seg<kT>(Cb + static_cast<size_t>(nn) * L, tl, L, fast_bc, cv);
+          load_seg<kT>(Bb + nn * p.bc_sn, tl, L, fast_bc, bv);
+          load_seg<kT>(Cb + nn * p.bc_sn, tl, L, fast_bc, cv);
         }
         const float dA_sum = wave_sum(dA_acc);
         if (lane == 0) {
@@ -338,41 +338,49 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   }
 }
 
-// dB/dC[b][n][t] = sum over channel blocks of the partials, fixed order. Each thread
-// owns 4 consecutive elements (16-byte loads) and keeps 4 blocks' loads in flight.
-template <typename bc_t>
+// dB/dC[b][n][t] = sum over channel blocks of the partials, fixed order. Partials are
+// [block][b][B|C][n][t] (block stride `stride` floats). grid.y = partial row
+// (b, which, n); threads walk the row's steps, 4 at a time (16-byte loads) when kVec
+// (L a multiple of 4), keeping 4 blocks' loads in flight.
+template <bool kVec, typename bc_t>
 __global__ __launch_bounds__(256) void reduce_bc_kernel(const float* __restrict__ part, int n_blk,
-                                                        size_t stride, int batch, size_t nl,
+                                                        size_t stride, int L, int N,
+                                                        long long sb, long long sn,
                                                         bc_t* __restrict__ dB, bc_t* __restrict__ dC) {
-  const size_t total = static_cast<size_t>(batch) * 2 * nl;
-  const size_t nvec = (total + 3) / 4;    // the block stride is padded to a multiple of 4
-  const size_t svec = stride / 4;
-  for (size_t v = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; v < nvec;
-       v += static_cast<size_t>(gridDim.x) * blockDim.x) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(part) + v;
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    int k = 0;
-    for (; k + 4 <= n_blk; k += 4) {
-      const f32x4 a0 = src[static_cast<size_t>(k + 0) * svec];
-      const f32x4 a1 = src[static_cast<size_t>(k + 1) * svec];
-      const f32x4 a2 = src[static_cast<size_t>(k + 2) * svec];
-      const f32x4 a3 = src[static_cast<size_t>(k + 3) * svec];
-      s += a0;
-      s += a1;
-      s += a2;
-      s += a3;
-    }
-    for (; k < n_blk; ++k) s += src[static_cast<size_t>(k) * svec];
-    const float out[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const size_t i = 4 * v + e;
-      if (i >= total) break;  // padding of the last vector
-      const size_t bb = i / (2 * nl);
-      const size_t rem = i - bb * 2 * nl;
-      const int which = rem >= nl;
-      const size_t off = bb * nl + (rem - which * nl);
-      store_as(which ? dC + off : dB + off, out[e]);
+  const int r = blockIdx.y;
+  const int bb = r / (2 * N);
+  const int rem = r - bb * 2 * N;
+  const int which = rem >= N;
+  const int n = rem - which * N;
+  const float* src_row = part + static_cast<size_t>(r) * L;
+  bc_t* dst = (which ? dC : dB) + bb * sb + n * sn;
+  constexpr int kE = kVec ? 4 : 1;
+  const int nvec = (L + kE - 1) / kE;
+  for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += gridDim.x * blockDim.x) {
+    if constexpr (kVec) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(src_row) + v;
+      const size_t svec = stride / 4;
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+      int k = 0;
+      for (; k + 4 <= n_blk; k += 4) {
+        const f32x4 a0 = src[static_cast<size_t>(k + 0) * svec];
+        const f32x4 a1 = src[static_cast<size_t>(k + 1) * svec];
+        const f32x4 a2 = src[static_cast<size_t>(k + 2) * svec];
+        const f32x4 a3 = src[static_cast<size_t>(k + 3) * svec];
+        s += a0;
+        s += a1;
+        s += a2;
+        s += a3;
+      }
+      for (; k < n_blk; ++k) s += src[static_cast<size_t>(k) * svec];
+      store_as(dst + 4 * v + 0, s.x);
+      store_as(dst + 4 * v + 1, s.y);
+      store_as(dst + 4 * v + 2, s.z);
+      store_as(dst + 4 * v + 3, s.w);
+    } else {
+      float s = 0.f;
+      for (int k = 0; k < n_blk; ++k) s += src_row[static_cast<size_t>(k) * stride + v];
+      store_as(dst + v, s);
     }
   }
 }
@@ -442,17 +450,20 @@ hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16
 
 hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB, void* dC,
                              float* dD, float* dbias, hipStream_t stream) {
-  const size_t nl = static_cast<size_t>(p.dstate) * p.seqlen;
-  const size_t total = static_cast<size_t>(p.batch) * 2 * nl;
-  int grid = static_cast<int>(((total + 3) / 4 + 255) / 256);
-  if (grid > 4096) grid = 4096;
+  const int L = p.seqlen;
+  const bool vec = (L % 4) == 0;  // partial rows are 16-byte aligned (block stride: 64 floats)
+  const int nvec = vec ? L / 4 : L;
+  const dim3 grid((nvec + 255) / 256, p.batch * 2 * p.dstate);
+#define MSS_REDUCE_BC(VEC, T)                                                                 \
+  hipLaunchKernelGGL((reduce_bc_kernel<VEC, T>), grid, dim3(256), 0, stream, p.part_dBC,       \
+                     p.n_blocks_d, p.part_stride, L, p.dstate, p.bc_sb, p.bc_sn,              \
+                     static_cast<T*>(dB), static_cast<T*>(dC))
   if (bc_bf16) {
-    hipLaunchKernelGGL(reduce_bc_kernel<bf16_t>, dim3(grid), dim3(256), 0, stream, p.part_dBC,
-                       p.n_blocks_d, p.part_stride, p.batch, nl, static_cast<bf16_t*>(dB), static_cast<bf16_t*>(dC));
+    if (vec) MSS_REDUCE_BC(true, bf16_t); else MSS_REDUCE_BC(false, bf16_t);
   } else {
-    hipLaunchKernelGGL(reduce_bc_kernel<float>, dim3(grid), dim3(256), 0, stream, p.part_dBC,
-                       p.n_blocks_d, p.part_stride, p.batch, nl, static_cast<float*>(dB), static_cast<float*>(dC));
+    if (vec) MSS_REDUCE_BC(true, float); else MSS_REDUCE_BC(false, float);
   }
+#undef MSS_REDUCE_BC
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int small = p.dim * p.dstate + 2 * p.dim;

@@ -42,6 +42,8 @@ int check_dims(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate) {
   if (batch <= 0 || dim <= 0 || seqlen <= 0) return MSS_ERR_INVALID_ARGUMENT;
   if (dstate <= 0 || dstate > 256) return MSS_ERR_INVALID_ARGUMENT;
   if (dstate > MSS_MAX_DSTATE) return MSS_ERR_UNSUPPORTED;
+  // Grid limits: batch rows (and the dB/dC reduction's batch*2*dstate rows) on grid.y.
+  if (static_cast<long long>(batch) * 2 * dstate > 65535) return MSS_ERR_UNSUPPORTED;
   // Index arithmetic inside the kernels uses 64-bit offsets; per-row steps are int.
   return MSS_OK;
 }
@@ -52,6 +54,43 @@ int check_common(int32_t discretization, int32_t softplus, int32_t io_dtype, int
   if ((io_dtype != MSS_F32 && io_dtype != MSS_BF16) || (bc_dtype != MSS_F32 && bc_dtype != MSS_BF16))
     return MSS_ERR_INVALID_ARGUMENT;
   return MSS_OK;
+}
+
+// Row strides with the contiguous defaults filled in.
+struct Strides {
+  long long io_sb = 0, io_sd = 0, bc_sb = 0, bc_sn = 0;
+};
+
+// Rows (i, j) start at i*s_i + j*s_j and are `len` long (i < n_i, j < n_j): true when no
+// two of them overlap.
+bool rows_disjoint(long long n_i, long long s_i, long long n_j, long long s_j, long long len) {
+  if (n_i == 1 && n_j == 1) return true;
+  if (n_i == 1) return s_j >= len;
+  if (n_j == 1) return s_i >= len;
+  const bool i_inner = s_i <= s_j;
+  const long long lo = i_inner ? s_i : s_j, hi = i_inner ? s_j : s_i;
+  const long long n_lo = i_inner ? n_i : n_j;
+  return lo >= len && hi >= (n_lo - 1) * lo + len;
+}
+
+int resolve_strides(const mss_strides& in, int32_t batch, int32_t dim, int32_t seqlen,
+                    int32_t dstate, Strides* out) {
+  constexpr long long kMaxStride = 1LL << 40;
+  const long long L = seqlen;
+  out->io_sb = in.io_batch ? in.io_batch : static_cast<long long>(dim) * L;
+  out->io_sd = in.io_dim ? in.io_dim : L;
+  out->bc_sb = in.bc_batch ? in.bc_batch : static_cast<long long>(dstate) * L;
+  out->bc_sn = in.bc_state ? in.bc_state : L;
+  for (long long v : {out->io_sb, out->io_sd, out->bc_sb, out->bc_sn})
+    if (v < 0 || v > kMaxStride) return MSS_ERR_INVALID_ARGUMENT;
+  if (!rows_disjoint(batch, out->io_sb, dim, out->io_sd, L)) return MSS_ERR_INVALID_ARGUMENT;
+  if (!rows_disjoint(batch, out->bc_sb, dstate, out->bc_sn, L)) return MSS_ERR_INVALID_ARGUMENT;
+  return MSS_OK;
+}
+
+// 16-byte vector access of every row: aligned bases and strides.
+bool strides_aligned(long long s0, long long s1, size_t esz) {
+  return (static_cast<size_t>(s0) * esz) % 16 == 0 && (static_cast<size_t>(s1) * esz) % 16 == 0;
 }
 
 int n_carry_of(int32_t seqlen) { return (seqlen + MSS_CARRY_CHUNK - 1) / MSS_CARRY_CHUNK; }
@@ -83,7 +122,8 @@ int validate_fwd(const mss_fwd_args* a) {
   s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
   if (s != MSS_OK) return s;
   if (!a->u || !a->delta || !a->A || !a->B || !a->C || !a->out) return MSS_ERR_INVALID_ARGUMENT;
-  return MSS_OK;
+  Strides st;
+  return resolve_strides(a->strides, a->batch, a->dim, a->seqlen, a->dstate, &st);
 }
 
 int validate_bwd(const mss_bwd_args* a) {
@@ -97,7 +137,8 @@ int validate_bwd(const mss_bwd_args* a) {
   if (a->D && !a->dD) return MSS_ERR_INVALID_ARGUMENT;
   if (a->z && (!a->dz || !a->y_pre)) return MSS_ERR_INVALID_ARGUMENT;
   if (a->delta_bias && !a->ddelta_bias) return MSS_ERR_INVALID_ARGUMENT;
-  return MSS_OK;
+  Strides st;
+  return resolve_strides(a->strides, a->batch, a->dim, a->seqlen, a->dstate, &st);
 }
 
 int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
@@ -107,11 +148,19 @@ int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
   p.seqlen = a->seqlen;
   p.dstate = a->dstate;
   p.delta_softplus = a->delta_softplus;
-  const size_t io_row = static_cast<size_t>(a->seqlen) * dtype_size(a->io_dtype);
-  const size_t bc_row = static_cast<size_t>(a->seqlen) * dtype_size(a->bc_dtype);
-  p.vec_io = (io_row % 16 == 0) && aligned16(a->u) && aligned16(a->delta) && aligned16(a->z) &&
-             aligned16(a->out) && aligned16(a->y_pre);
-  p.vec_bc = (bc_row % 16 == 0) && aligned16(a->B) && aligned16(a->C);
+  Strides st;
+  resolve_strides(a->strides, a->batch, a->dim, a->seqlen, a->dstate, &st);  // validated
+  p.io_sb = st.io_sb;
+  p.io_sd = st.io_sd;
+  p.bc_sb = st.bc_sb;
+  p.bc_sn = st.bc_sn;
+  const size_t io_e = dtype_size(a->io_dtype), bc_e = dtype_size(a->bc_dtype);
+  const size_t bc_row = static_cast<size_t>(a->seqlen) * bc_e;
+  p.vec_io = strides_aligned(st.io_sb, st.io_sd, io_e) && aligned16(a->u) && aligned16(a->delta) &&
+             aligned16(a->z) && aligned16(a->out) && aligned16(a->y_pre);
+  // B/C staging also needs L to be a multiple of the 16-byte slot width.
+  p.vec_bc = (bc_row % 16 == 0) && strides_aligned(st.bc_sb, st.bc_sn, bc_e) && aligned16(a->B) &&
+             aligned16(a->C);
   p.n_carry = n_carry_of(a->seqlen);
   p.n_ref = (a->seqlen + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK;
   p.u = a->u;
@@ -143,12 +192,19 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   p.seqlen = a->seqlen;
   p.dstate = a->dstate;
   p.delta_softplus = a->delta_softplus;
-  const size_t io_row = static_cast<size_t>(a->seqlen) * dtype_size(a->io_dtype);
-  const size_t bc_row = static_cast<size_t>(a->seqlen) * dtype_size(a->bc_dtype);
-  p.vec_io = (io_row % 16 == 0) && aligned16(a->u) && aligned16(a->delta) && aligned16(a->z) &&
-             aligned16(a->dout) && aligned16(a->du) && aligned16(a->ddelta) && aligned16(a->dz) &&
-             aligned16(a->y_pre);
-  p.vec_bc = (bc_row % 16 == 0) && aligned16(a->B) && aligned16(a->C);
+  Strides st;
+  resolve_strides(a->strides, a->batch, a->dim, a->seqlen, a->dstate, &st);  // validated
+  p.io_sb = st.io_sb;
+  p.io_sd = st.io_sd;
+  p.bc_sb = st.bc_sb;
+  p.bc_sn = st.bc_sn;
+  const size_t io_e = dtype_size(a->io_dtype), bc_e = dtype_size(a->bc_dtype);
+  const size_t bc_row = static_cast<size_t>(a->seqlen) * bc_e;
+  p.vec_io = strides_aligned(st.io_sb, st.io_sd, io_e) && aligned16(a->u) && aligned16(a->delta) &&
+             aligned16(a->z) && aligned16(a->dout) && aligned16(a->du) && aligned16(a->ddelta) &&
+             aligned16(a->dz) && aligned16(a->y_pre);
+  p.vec_bc = (bc_row % 16 == 0) && strides_aligned(st.bc_sb, st.bc_sn, bc_e) && aligned16(a->B) &&
+             aligned16(a->C);
   p.n_carry = n_carry_of(a->seqlen);
   p.chan_per_block = l.chan_per_block;
   p.n_blocks_d = l.n_blocks_d;
@@ -188,7 +244,7 @@ int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream) {
     const hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), l.total, stream);
     if (e != hipSuccess) return hip_fail(e, "allocating backward workspace");
     owned = true;
-  } else if (a->workspace_bytes < l.total) {
+  } else if (a->workspace_bytes < l.total || !aligned16(ws)) {
     return MSS_ERR_WORKSPACE;
   }
   const mss::BwdParams p = pack_bwd(a, l, ws);
@@ -216,7 +272,7 @@ const char* mss_strerror(int status) {
   switch (status) {
     case MSS_OK: return "ok";
     case MSS_ERR_INVALID_ARGUMENT: return "invalid argument";
-    case MSS_ERR_UNSUPPORTED: return "unsupported configuration (dstate must be <= 16)";
+    case MSS_ERR_UNSUPPORTED: return "unsupported configuration (dstate <= 16, batch * 2 * dstate <= 65535)";
     case MSS_ERR_HIP: return "HIP runtime error";
     case MSS_ERR_WORKSPACE: return "workspace too small";
     default: return "unknown status";
@@ -318,6 +374,10 @@ int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32
   p.dim = dim;
   p.seqlen = length;
   p.dstate = dstate;
+  p.io_sb = static_cast<long long>(dim) * length;
+  p.io_sd = length;
+  p.bc_sb = static_cast<long long>(dstate) * length;
+  p.bc_sn = length;
   const size_t row = static_cast<size_t>(length) * sizeof(float);
   p.vec_io = (row % 16 == 0) && aligned16(u) && aligned16(deltas);
   p.vec_bc = (row % 16 == 0) && aligned16(B) && aligned16(C);

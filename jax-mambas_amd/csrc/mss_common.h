@@ -246,6 +246,8 @@ struct FwdParams {
   int vec_bc;  // ... for B/C rows
   int n_carry;  // ceil(L / 1024)
   int n_ref;    // ceil(L / 2048)
+  long long io_sb, io_sd;  // row strides (elements) of u/delta/z/out/y_pre: batch, channel
+  long long bc_sb, bc_sn;  // row strides of B/C: batch, state
   const void* u;
   const void* delta;
   const float* A;
@@ -270,6 +272,8 @@ struct BwdParams {
   int n_carry;
   int chan_per_block;  // channels one workgroup walks (multiple of the wave count)
   int n_blocks_d;      // ceil(dim / chan_per_block)
+  long long io_sb, io_sd;  // row strides of u/delta/z/y_pre/dout/du/ddelta/dz
+  long long bc_sb, bc_sn;  // row strides of B/C and dB/dC
   const void* u;
   const void* delta;
   const float* A;

@@ -80,12 +80,13 @@ __device__ __forceinline__ void read_staged(const uint4* __restrict__ row, int l
 
 // Stage elements [t0, t0 + 64*kT) of `nrows` rows (B rows of states n0.., then C rows)
 // into dst[row][slot] (64*kT elements of bc_t per row), spread over all threads.
+// Row k of B (C) starts at Bb (Cb) + (n0 + k) * sn.
 // dma: rows are 16-byte aligned and L is a multiple of the slot width, so each slot is
 // either fully inside [0, L) or fully past it; past-the-end slots re-read the last valid
 // slot (finite values; they only meet zero coefficients).
 template <int kT, int kW, int kNB, typename bc_t>
 __device__ __forceinline__ void stage_round(const bc_t* __restrict__ Bb, const bc_t* __restrict__ Cb,
-                                            int n0, int nb, int t0, int L, bool dma,
+                                            int n0, int nb, int t0, int L, long long sn, bool dma,
                                             uint4 (*dst)[2][64 * kT * sizeof(bc_t) / 16], int tid) {
   constexpr int kE = BcStage<bc_t>::kElemsPerSlot;
   constexpr int kQ = kT / kE;
@@ -105,7 +106,7 @@ __device__ __forceinline__ void stage_round(const bc_t* __restrict__ Bb, const b
       const int q = (s % kQ) ^ slot_swz<kQ>(i);
       int e = t0 + i * kT + q * kE;
       e = e < L ? e : L - kE;
-      const bc_t* src = (which ? Cb : Bb) + static_cast<size_t>(n0 + k) * L + e;
+      const bc_t* src = (which ? Cb : Bb) + (n0 + k) * sn + e;
       __builtin_amdgcn_global_load_lds((gbl_void_t)src, (lds_void_t)(&dst[k][which][s0]), 16, 0, 0);
     }
   } else {
@@ -119,7 +120,7 @@ __device__ __forceinline__ void stage_round(const bc_t* __restrict__ Bb, const b
       const int q = r / kE;
       const int sl = kQ * i + (q ^ slot_swz<kQ>(i));
       const int t = t0 + e;
-      const bc_t* src = (which ? Cb : Bb) + static_cast<size_t>(n0 + k) * L;
+      const bc_t* src = (which ? Cb : Bb) + (n0 + k) * sn;
       bc_t v;
       if (t < L) {
         v = src[t];
@@ -157,13 +158,13 @@ void fwd_kernel(FwdParams p) {
   const int N = p.dstate;
   const int len = p.seq_lens ? min(max(p.seq_lens[b], 0), L) : L;
   const size_t chan = static_cast<size_t>(b) * p.dim + d;
-  const size_t row = chan * L;
+  const long long row = b * p.io_sb + d * p.io_sd;
 
   const io_t* __restrict__ u_row = static_cast<const io_t*>(p.u) + row;
   const io_t* __restrict__ dl_row = static_cast<const io_t*>(p.delta) + row;
   io_t* __restrict__ out_row = static_cast<io_t*>(p.out) + row;
-  const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + static_cast<size_t>(b) * N * L;
-  const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + static_cast<size_t>(b) * N * L;
+  const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + b * p.bc_sb;
+  const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + b * p.bc_sb;
 
   if (lane < N) {
     s_run[w][lane] = p.x0 ? p.x0[chan * N + lane] : 0.f;
@@ -186,7 +187,7 @@ void fwd_kernel(FwdParams p) {
     const int c = r / rounds;
     const int n0 = (r - c * rounds) * kNB;
     const int nb = min(kNB, N - n0);
-    if (nb > 0) stage_round<kT, kW, kNB, bc_t>(Bb, Cb, n0, nb, c * kChunk, L, dma, buf, tid);
+    if (nb > 0) stage_round<kT, kW, kNB, bc_t>(Bb, Cb, n0, nb, c * kChunk, L, p.bc_sn, dma, buf, tid);
   };
   if (n_active_chunks > 0) issue_round(0, stage0);
 

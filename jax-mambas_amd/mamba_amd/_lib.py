@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 1
+MSS_ABI_VERSION = 2
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -46,6 +46,12 @@ _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 
 
+class Strides(ctypes.Structure):
+    """mss_strides: row strides in elements (0 = contiguous default)."""
+    _fields_ = [("io_batch", ctypes.c_int64), ("io_dim", ctypes.c_int64),
+                ("bc_batch", ctypes.c_int64), ("bc_state", ctypes.c_int64)]
+
+
 class FwdArgs(ctypes.Structure):
     _fields_ = [
         ("batch", _i32), ("dim", _i32), ("seqlen", _i32), ("dstate", _i32),
@@ -53,6 +59,7 @@ class FwdArgs(ctypes.Structure):
         ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
         ("D", _p), ("z", _p), ("delta_bias", _p), ("initial_state", _p), ("seq_lens", _p),
         ("out", _p), ("last_state", _p), ("carries", _p), ("y_pre", _p),
+        ("strides", Strides),
     ]
 
 
@@ -66,6 +73,7 @@ class BwdArgs(ctypes.Structure):
         ("du", _p), ("ddelta", _p), ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("dz", _p),
         ("ddelta_bias", _p), ("dinitial_state", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+        ("strides", Strides),
     ]
 
 

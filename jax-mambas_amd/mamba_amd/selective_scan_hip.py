@@ -48,6 +48,12 @@ def _require_gpu(*tensors):
             raise RuntimeError("the HIP selective scan requires tensors on a ROCm GPU device")
 
 
+def _strides(u, io_layout, B, bc_layout):
+    io_b, io_r = _row_strides(u, io_layout)
+    bc_b, bc_r = _row_strides(B, bc_layout)
+    return _lib.Strides(io_batch=io_b, io_dim=io_r, bc_batch=bc_b, bc_state=bc_r)
+
+
 def _stream(t):
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -107,18 +113,63 @@ def _contig(t):
     return None if t is None else t.contiguous()
 
 
+# Row layouts of a (batch, rows, steps) tensor the kernels read without a copy: steps
+# contiguous and rows dense either batch-outer ("brl": [B][R][L]) or row-outer ("rbl":
+# [R][B][L], the layout of an (R, B*L) activation matrix).
+def _dense_strides(shape, layout):
+    b, r, l = shape
+    return (r * l, l, 1) if layout == "brl" else (l, b * l, 1)
+
+
+def _strides_match(t, layout):
+    b, r, l = t.shape
+    want = _dense_strides(t.shape, layout)
+    got = t.stride()
+    return got[2] == 1 and (b == 1 or got[0] == want[0]) and (r == 1 or got[1] == want[1])
+
+
+def _layout_of(t):
+    for layout in ("brl", "rbl"):
+        if _strides_match(t, layout):
+            return layout
+    return None
+
+
+def _empty_rows(shape, layout, dtype, device):
+    b, r, l = shape
+    if layout == "rbl":
+        return torch.empty(r, b, l, dtype=dtype, device=device).permute(1, 0, 2)
+    return torch.empty(b, r, l, dtype=dtype, device=device)
+
+
+def _conform(t, layout):
+    """t in the given dense row layout (a copy only when its strides differ)."""
+    if t is None or _strides_match(t, layout):
+        return t
+    out = _empty_rows(t.shape, layout, t.dtype, t.device)
+    out.copy_(t)
+    return out
+
+
+def _row_strides(t, layout):
+    """(batch stride, row stride) the kernels use for tensors in this layout."""
+    s = _dense_strides(t.shape, layout)
+    return s[0], s[1]
+
+
 class _SelectiveScan(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh):
+    def forward(ctx, u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh,
+                io_layout, bc_layout):
         lib = register_hip_kernel()
         batch, dim, length = u.shape
         n = A.shape[1]
         n_carry = (length + _lib.MSS_CARRY_CHUNK - 1) // _lib.MSS_CARRY_CHUNK
-        out = torch.empty_like(u)
+        out = _empty_rows(u.shape, io_layout, u.dtype, u.device)
         last = torch.empty(batch, dim, n, device=u.device, dtype=torch.float32)
         carries = torch.empty(batch, dim, n_carry, n, device=u.device, dtype=torch.float32)
         # Pre-gate output: the backward's dz needs it (kept only when z is given).
-        y_pre = torch.empty_like(u) if z is not None else None
+        y_pre = _empty_rows(u.shape, io_layout, u.dtype, u.device) if z is not None else None
         args = _lib.FwdArgs(
             batch=batch, dim=dim, seqlen=length, dstate=n,
             discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER,
@@ -127,11 +178,13 @@ class _SelectiveScan(torch.autograd.Function):
             u=_ptr(u), delta=_ptr(delta), A=_ptr(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
             delta_bias=_ptr(delta_bias), initial_state=_ptr(initial_state), seq_lens=_ptr(seq_lens),
             out=_ptr(out), last_state=_ptr(last), carries=_ptr(carries), y_pre=_ptr(y_pre),
+            strides=_strides(u, io_layout, B, bc_layout),
         )
         _lib.check(lib.mss_fwd(args, _stream(u)), "mss_fwd")
         ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre)
         ctx.delta_softplus = bool(delta_softplus)
         ctx.zoh = bool(zoh)
+        ctx.layouts = (io_layout, bc_layout)
         return out, last
 
     @staticmethod
@@ -140,15 +193,18 @@ class _SelectiveScan(torch.autograd.Function):
         u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre = ctx.saved_tensors
         batch, dim, length = u.shape
         n = A.shape[1]
-        dout = dout.to(u.dtype).contiguous()
+        io_layout, bc_layout = ctx.layouts
+        if dout is None:
+            dout = torch.zeros_like(u)
+        dout = _conform(dout.to(u.dtype), io_layout)
         dlast = None if dlast is None else dlast.float().contiguous()
-        du = torch.empty_like(u)
-        ddelta = torch.empty_like(delta)
+        du = _empty_rows(u.shape, io_layout, u.dtype, u.device)
+        ddelta = _empty_rows(u.shape, io_layout, u.dtype, u.device)
         dA = torch.empty_like(A)
-        dB = torch.empty_like(B)
-        dC = torch.empty_like(C)
+        dB = _empty_rows(B.shape, bc_layout, B.dtype, B.device)
+        dC = _empty_rows(C.shape, bc_layout, C.dtype, C.device)
         dD = None if D is None else torch.empty_like(D)
-        dz = None if z is None else torch.empty_like(z)
+        dz = None if z is None else _empty_rows(u.shape, io_layout, u.dtype, u.device)
         dbias = None if delta_bias is None else torch.empty_like(delta_bias)
         dinit = None if initial_state is None else torch.empty_like(initial_state)
         args = _lib.BwdArgs(
@@ -161,13 +217,14 @@ class _SelectiveScan(torch.autograd.Function):
             carries=_ptr(carries), y_pre=_ptr(y_pre), dout=_ptr(dout), dlast_state=_ptr(dlast),
             du=_ptr(du), ddelta=_ptr(ddelta), dA=_ptr(dA), dB=_ptr(dB), dC=_ptr(dC), dD=_ptr(dD),
             dz=_ptr(dz), ddelta_bias=_ptr(dbias), dinitial_state=_ptr(dinit),
+            strides=_strides(u, io_layout, B, bc_layout),
         )
         ws_bytes = int(lib.mss_bwd_workspace_bytes(args))
         ws = torch.empty(ws_bytes, device=u.device, dtype=torch.uint8)
         args.workspace = ws.data_ptr()
         args.workspace_bytes = ws_bytes
         _lib.check(lib.mss_bwd(args, _stream(u)), "mss_bwd")
-        return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit, None, None, None
+        return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit, None, None, None, None, None
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
@@ -176,10 +233,15 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
     """Fused selective scan in channel-major layout; see the module docstring."""
     _validate_fused(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, discretization)
     register_hip_kernel()
+    # Rows of u/delta/z (and B/C) may be batch-outer or channel-outer; the others follow
+    # u's (B's) layout, copied only when they differ.
+    io_layout = _layout_of(u) or "brl"
+    bc_layout = _layout_of(B) or "brl"
     out, last = _SelectiveScan.apply(
-        u.contiguous(), delta.contiguous(), A.contiguous(), B.contiguous(), C.contiguous(),
-        _contig(D), _contig(z), _contig(delta_bias), _contig(initial_state), _contig(seq_lens),
-        bool(delta_softplus), discretization == "zoh")
+        _conform(u, io_layout), _conform(delta, io_layout), A.contiguous(),
+        _conform(B, bc_layout), _conform(C, bc_layout),
+        _contig(D), _conform(z, io_layout), _contig(delta_bias), _contig(initial_state),
+        _contig(seq_lens), bool(delta_softplus), discretization == "zoh", io_layout, bc_layout)
     return (out, last) if return_last_state else out
 
 
@@ -224,5 +286,5 @@ def selective_scan(A, deltas, Bs, Cs, u, initial_x=None, *, use_euler_barB_appro
     t = lambda x: x.transpose(1, 2).contiguous()
     out, last = _SelectiveScan.apply(t(u), t(deltas), A.contiguous(), t(Bs), t(Cs), None, None,
                                      None, initial_x.contiguous(), None, False,
-                                     not use_euler_barB_approx)
+                                     not use_euler_barB_approx, "brl", "brl")
     return out.transpose(1, 2), last

@@ -9,6 +9,7 @@
 """
 import ctypes
 import re
+import subprocess
 from pathlib import Path
 
 import numpy as np
@@ -82,6 +83,66 @@ def fwd_args(**kw):
 ])
 def test_fwd_validation(lib, kw, status):
     assert lib.mss_fwd(fwd_args(**kw), None) == status
+
+
+@pytest.mark.parametrize("strides,status", [
+    (dict(io_dim=-10), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(io_dim=5), _lib.MSS_ERR_INVALID_ARGUMENT),                # rows of 10 steps overlap
+    (dict(io_batch=10, io_dim=10), _lib.MSS_ERR_INVALID_ARGUMENT),  # (1,0) and (0,1) collide
+    (dict(io_batch=10, io_dim=15), _lib.MSS_ERR_INVALID_ARGUMENT),  # [D][B][L] needs io_dim >= 20
+    (dict(bc_state=3), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(bc_batch=10, bc_state=10), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(bc_batch=1 << 41), _lib.MSS_ERR_INVALID_ARGUMENT),
+])
+def test_fwd_stride_validation(lib, strides, status):
+    assert lib.mss_fwd(fwd_args(strides=_lib.Strides(**strides)), None) == status
+    assert lib.mss_bwd(bwd_args(strides=_lib.Strides(**strides)), None) == status
+
+
+def test_grid_limit_is_unsupported(lib):
+    assert lib.mss_fwd(fwd_args(batch=2048, dstate=16), None) == _lib.MSS_ERR_UNSUPPORTED
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """The ctypes mirrors have the C structs' size and field offsets (compiled with gcc)."""
+    structs = {"mss_fwd_args": _lib.FwdArgs, "mss_bwd_args": _lib.BwdArgs, "mss_strides": _lib.Strides}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "mamba_selective_scan.h"',
+             "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    seen = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        cname, field, value = line.split()
+        seen[(cname, field)] = int(value)
+    for cname, cls in structs.items():
+        assert seen[(cname, "sizeof")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert seen[(cname, field)] == getattr(cls, field).offset, (cname, field)
+
+
+def test_row_layout_helpers():
+    from mamba_amd import selective_scan_hip as ss
+    x = torch.empty(3, 5, 7)
+    assert ss._layout_of(x) == "brl"
+    xt = torch.empty(5, 3, 7).permute(1, 0, 2)
+    assert ss._layout_of(xt) == "rbl"
+    assert ss._row_strides(xt, "rbl") == (7, 21)
+    # a row slice of a bigger (R, B*L) matrix: dense rbl strides, no copy
+    big = torch.empty(12, 3 * 7)
+    view = big[4:9].view(5, 3, 7).permute(1, 0, 2)
+    assert ss._layout_of(view) == "rbl" and ss._conform(view, "rbl") is view
+    # a strided view that is neither layout is copied into the requested one
+    odd = torch.randn(3, 10, 7)[:, ::2]
+    assert ss._layout_of(odd) is None
+    c = ss._conform(odd, "rbl")
+    assert ss._strides_match(c, "rbl") and torch.equal(c, odd)
 
 
 def test_null_args(lib):
