@@ -15,6 +15,8 @@ Fields beyond the driver contract:
   cpu_baseline  torch-CPU restatement of the reference's pure-JAX scan path
                 (oracle/assoc_torch.py) timed on this host on a channel slice
   fwd_bwd_hbm_frac  (fwd + bwd algorithmic bytes) / step time / 8 TB/s
+  train_c5      the metric's second half: tokens/s of one training step of the Mamba-1
+                130M-shape LM (config 5) through the HIP scan
 """
 from __future__ import annotations
 
@@ -132,6 +134,69 @@ def run_gpu(torch, cfg, steps, warmup):
     return total_ms / steps, float(np.mean(fwd)), float(np.mean(bws)), float(np.mean(red))
 
 
+C5_MODEL = dict(vocab=50280, d_model=768, n_layers=24, expand=2, d_state=16, dt_rank=48, d_conv=4)
+C5_BATCH, C5_LENGTH = 8, 2048
+
+
+def run_train_c5(torch, steps, warmup):
+    """Config 5: one training step of the Mamba-1 130M-shape LM (random init, uniform random
+    tokens): bf16 activations with fp32 master weights and residual stream, forward, fp32
+    cross-entropy over all next-token positions, backward (HIP scan backward inside),
+    fused AdamW step. Timed with events on the current stream around exactly `steps` steps."""
+    import torch.nn.functional as F
+    from mamba_amd.mamba1 import MambaLM
+
+    torch.manual_seed(0)
+    m = C5_MODEL
+    model = MambaLM(m["vocab"], m["d_model"], m["n_layers"], m["expand"], m["d_state"], m["dt_rank"],
+                    m["d_conv"], device="cuda")
+    n_params = sum(p.numel() for p in model.parameters())
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    tokens = torch.randint(0, m["vocab"], (C5_BATCH, C5_LENGTH + 1), device="cuda", generator=gen)
+    inp = tokens[:, :-1].contiguous()
+    tgt = tokens[:, 1:].reshape(-1)
+
+    def step():
+        logits = model(inp, act_dtype=torch.bfloat16)
+        loss = F.cross_entropy(logits.float(), tgt)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(warmup):
+        loss = step()
+    torch.cuda.synchronize()
+    log(f"[bench] c5 warmup done ({warmup} steps, loss {loss.item():.4f}, {n_params / 1e6:.1f} M params)")
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        loss = step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    log(f"[bench] c5 timed {steps} steps: {ms:.2f} ms/step, loss {loss.item():.4f}")
+    del model, opt
+    torch.cuda.empty_cache()
+    return {
+        "metric": "Mamba-1 130M train tokens/s",
+        "value": round(C5_BATCH * C5_LENGTH / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "ms_per_step": round(ms, 3),
+        "steps": steps,
+        "warmup": warmup,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"model": "Mamba-1 130M shape", "params_m": round(n_params / 1e6, 2), **m,
+                   "global_batch": C5_BATCH, "seq_len": C5_LENGTH, "optimizer": "AdamW (fused)",
+                   "parallelism": "none (1 GPU)"},
+    }
+
+
 def cpu_baseline(torch, cfg, target_s):
     """Reference composition on the CPU: softplus(delta + bias) -> pure-JAX-style scan
     (oracle/assoc_torch.py, mamba/selective_scan_cuda.py:56-90) -> + D*u -> * silu(z);
@@ -193,6 +258,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="approximate CPU work for the CPU baseline (0 disables it)")
+    ap.add_argument("--train-steps", type=int, default=10,
+                    help="timed config-5 training steps (0 skips the training measurement)")
+    ap.add_argument("--train-warmup", type=int, default=3)
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the timed region, copy a device buffer of this many MiB twice "
                          "(a kernel of known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -231,6 +299,9 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] calibration copy of {args.calibration_copy_mib} MiB done")
         del src, dst
+    train = None
+    if args.train_steps > 0:
+        train = run_train_c5(torch, args.train_steps, args.train_warmup)
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, cfg, args.cpu_seconds)
@@ -255,6 +326,7 @@ def main():
         "cpu_baseline": cpu,
         "fwd_bwd_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "kernels_ms": {"fwd": round(fwd_ms, 5), "bwd_scan": round(bwd_ms, 5), "bwd_reduce": round(red_ms, 5)},
+        "train_c5": train,
     }
     print(json.dumps(result), flush=True)
 

@@ -148,6 +148,37 @@ int mss_bwd(const mss_bwd_args* args, void* stream);
 int mss_bwd_scan(const mss_bwd_args* args, void* stream);
 int mss_bwd_reduce(const mss_bwd_args* args, void* stream);
 
+/* --- Causal depthwise conv1d + activation (the Mamba-1 block's short convolution). ---
+ * No counterpart symbol in the reference: it runs there as an XLA convolution
+ * (mamba/mamba1.py:250-255, 313-329: nnx.Conv(feature_group_count=channels,
+ * padding="CAUSAL"), then silu, with the padding mask applied before and after).
+ * Rows of x/y/dy/dx use the io strides of `strides` (bc strides unused):
+ *   pre[t] = bias[d] + sum_{k<width} weight[d][k] * x[t - (width-1) + k]   (x[t<0] = 0)
+ *   y[t]   = silu(pre[t]) (activation 1) or pre[t] (activation 0);  y[t] = 0 for t >= seq_lens[b]
+ * The backward recomputes pre from x and overwrites dx, dweight and dbias. */
+typedef struct mss_conv_args {
+  int32_t batch, dim, seqlen;
+  int32_t width;      /* taps, 1..4 */
+  int32_t io_dtype;   /* x, y, dy, dx */
+  int32_t activation; /* 0 none, 1 silu */
+  const void* x;
+  const float* weight;     /* [dim][width] */
+  const float* bias;       /* [dim], optional */
+  const int32_t* seq_lens; /* optional */
+  void* y;                 /* forward output */
+  const void* dy;          /* backward inputs / outputs */
+  void* dx;
+  float* dweight;          /* [dim][width] */
+  float* dbias;            /* optional (required iff bias given) */
+  void* workspace;         /* backward scratch; NULL = library allocates stream-ordered */
+  size_t workspace_bytes;
+  mss_strides strides;
+} mss_conv_args;
+
+size_t mss_conv_bwd_workspace_bytes(const mss_conv_args* args);
+int mss_conv_fwd(const mss_conv_args* args, void* stream);
+int mss_conv_bwd(const mss_conv_args* args, void* stream);
+
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------
  * Same argument order, attribute meaning and buffer shapes as the reference's XLA-FFI
  * handlers; physical layouts as listed at the top of this file. */

@@ -23,6 +23,11 @@ hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16
 hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB, void* dC,
                              float* dD, float* dbias, hipStream_t stream);
 int bwd_chan_per_block(int batch, int dim);
+hipError_t launch_conv(const ConvParams& p, bool bwd, bool vec, bool silu, bool io_bf16,
+                       hipStream_t stream);
+hipError_t launch_conv_reduce(const ConvParams& p, int n_tiles, float* dw, float* dbias,
+                              hipStream_t stream);
+int conv_tile_steps(int vec, int io_bf16);
 }  // namespace mss
 
 namespace {
@@ -264,6 +269,55 @@ int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream) {
 
 }  // namespace
 
+// ---- causal conv1d
+int validate_conv(const mss_conv_args* a, bool bwd) {
+  if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->batch <= 0 || a->dim <= 0 || a->seqlen <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->width < 1 || a->width > 4) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->batch > 65535 || a->dim > 65535) return MSS_ERR_UNSUPPORTED;
+  if (a->io_dtype != MSS_F32 && a->io_dtype != MSS_BF16) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->activation != 0 && a->activation != 1) return MSS_ERR_INVALID_ARGUMENT;
+  if (!a->x || !a->weight) return MSS_ERR_INVALID_ARGUMENT;
+  if (!bwd && !a->y) return MSS_ERR_INVALID_ARGUMENT;
+  if (bwd && (!a->dy || !a->dx || !a->dweight)) return MSS_ERR_INVALID_ARGUMENT;
+  if (bwd && a->bias && !a->dbias) return MSS_ERR_INVALID_ARGUMENT;
+  Strides st;
+  return resolve_strides(a->strides, a->batch, a->dim, a->seqlen, 1, &st);
+}
+
+struct ConvSetup {
+  mss::ConvParams p{};
+  bool vec = false;
+  int n_tiles = 0;
+  size_t ws_bytes = 0;
+};
+
+ConvSetup conv_setup(const mss_conv_args* a) {
+  ConvSetup c;
+  Strides st;
+  resolve_strides(a->strides, a->batch, a->dim, a->seqlen, 1, &st);  // validated
+  c.p.batch = a->batch;
+  c.p.dim = a->dim;
+  c.p.seqlen = a->seqlen;
+  c.p.width = a->width;
+  c.p.sb = st.io_sb;
+  c.p.sd = st.io_sd;
+  c.p.x = a->x;
+  c.p.w = a->weight;
+  c.p.bias = a->bias;
+  c.p.seq_lens = a->seq_lens;
+  c.p.y = a->y;
+  c.p.dy = a->dy;
+  c.p.dx = a->dx;
+  const size_t esz = dtype_size(a->io_dtype);
+  c.vec = strides_aligned(st.io_sb, st.io_sd, esz) && aligned16(a->x) && aligned16(a->y) &&
+          aligned16(a->dy) && aligned16(a->dx);
+  const int tile = mss::conv_tile_steps(c.vec, a->io_dtype == MSS_BF16);
+  c.n_tiles = (a->seqlen + tile - 1) / tile;
+  c.ws_bytes = static_cast<size_t>(a->dim) * a->batch * c.n_tiles * (a->width + 1) * sizeof(float);
+  return c;
+}
+
 extern "C" {
 
 int mss_abi_version(void) { return MSS_ABI_VERSION; }
@@ -308,6 +362,48 @@ int mss_bwd_reduce(const mss_bwd_args* args, void* stream) {
   const int s = validate_bwd(args);
   if (s != MSS_OK) return s;
   return run_bwd(args, kPhaseReduce, static_cast<hipStream_t>(stream));
+}
+
+size_t mss_conv_bwd_workspace_bytes(const mss_conv_args* a) {
+  // Shapes only: sized for the scalar path, which has the most step tiles.
+  if (a == nullptr || a->batch <= 0 || a->dim <= 0 || a->seqlen <= 0 || a->width < 1 || a->width > 4)
+    return 0;
+  const int tile = mss::conv_tile_steps(0, 0);
+  const size_t tiles = (static_cast<size_t>(a->seqlen) + tile - 1) / tile;
+  return static_cast<size_t>(a->dim) * a->batch * tiles * (a->width + 1) * sizeof(float);
+}
+
+int mss_conv_fwd(const mss_conv_args* args, void* stream) {
+  const int s = validate_conv(args, false);
+  if (s != MSS_OK) return s;
+  ConvSetup c = conv_setup(args);
+  const hipError_t e = mss::launch_conv(c.p, false, c.vec, args->activation == 1,
+                                        args->io_dtype == MSS_BF16, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching conv1d forward");
+}
+
+int mss_conv_bwd(const mss_conv_args* args, void* stream) {
+  const int s = validate_conv(args, true);
+  if (s != MSS_OK) return s;
+  ConvSetup c = conv_setup(args);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(args->workspace);
+  bool owned = false;
+  if (ws == nullptr) {
+    const hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), c.ws_bytes, st);
+    if (e != hipSuccess) return hip_fail(e, "allocating conv1d workspace");
+    owned = true;
+  } else if (args->workspace_bytes < c.ws_bytes || !aligned16(ws)) {
+    return MSS_ERR_WORKSPACE;
+  }
+  c.p.part = reinterpret_cast<float*>(ws);
+  hipError_t e = mss::launch_conv(c.p, true, c.vec, args->activation == 1, args->io_dtype == MSS_BF16, st);
+  if (e == hipSuccess) e = mss::launch_conv_reduce(c.p, c.n_tiles, args->dweight, args->dbias, st);
+  if (owned) {
+    const hipError_t f = hipFreeAsync(ws, st);
+    if (e == hipSuccess) e = f;
+  }
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching conv1d backward");
 }
 
 int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,

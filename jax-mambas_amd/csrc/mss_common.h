@@ -239,6 +239,19 @@ __device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L
 
 // ---------------------------------------------------------------------------------
 // Kernel parameter blocks (host fills them after validation).
+struct ConvParams {
+  int batch, dim, seqlen, width;
+  long long sb, sd;  // row strides (elements) of x, y, dy, dx: batch, channel
+  const void* x;
+  const float* w;     // [dim][width]
+  const float* bias;  // [dim] or null
+  const int* seq_lens;
+  void* y;
+  const void* dy;
+  void* dx;
+  float* part;  // backward: per-(d, b, tile) partials of dw / dbias, (width + 1) floats each
+};
+
 struct FwdParams {
   int batch, dim, seqlen, dstate;
   int delta_softplus;

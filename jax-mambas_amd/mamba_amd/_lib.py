@@ -37,6 +37,9 @@ EXPORTED_SYMBOLS = (
     "mss_scan_fwd",
     "mss_scan_fwd_repeat",
     "mss_scan_bwd",
+    "mss_conv_bwd_workspace_bytes",
+    "mss_conv_fwd",
+    "mss_conv_bwd",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -73,6 +76,16 @@ class BwdArgs(ctypes.Structure):
         ("du", _p), ("ddelta", _p), ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("dz", _p),
         ("ddelta_bias", _p), ("dinitial_state", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+        ("strides", Strides),
+    ]
+
+
+class ConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i32), ("dim", _i32), ("seqlen", _i32), ("width", _i32), ("io_dtype", _i32),
+        ("activation", _i32),
+        ("x", _p), ("weight", _p), ("bias", _p), ("seq_lens", _p), ("y", _p), ("dy", _p), ("dx", _p),
+        ("dweight", _p), ("dbias", _p), ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
         ("strides", Strides),
     ]
 
@@ -116,6 +129,11 @@ def register_hip_kernel(library_path=None):
     lib.mss_scan_fwd_repeat.restype = ctypes.c_int
     lib.mss_scan_bwd.argtypes = [_p, _i32, _i32, _i32, _i32] + [_p] * 15
     lib.mss_scan_bwd.restype = ctypes.c_int
+    for name in ("mss_conv_fwd", "mss_conv_bwd"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(ConvArgs), _p]
+        getattr(lib, name).restype = ctypes.c_int
+    lib.mss_conv_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ConvArgs)]
+    lib.mss_conv_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

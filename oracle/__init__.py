@@ -14,4 +14,7 @@ Modules:
                    ``selective_scan_reference`` (odd/even associative scan over a
                    materialised (B, L, D, N) tensor); used as the CPU baseline and as an
                    independent formulation the sequential oracle is checked against.
+  * ``mamba1_torch`` — torch restatement of the reference's Mamba-1 S6 / block / stacked
+                   model in its (B, L, features) layout, for checking the channel-major
+                   model of the product end to end.
 """

@@ -1,0 +1,70 @@
+"""Torch restatement of the reference's Mamba-1 model — TEST INFRASTRUCTURE ONLY.
+
+The callers of the scan in the reference's own logical layout (B, L, features), any float
+dtype (tests use float64 on the CPU), differentiable through torch autograd:
+
+* ``S6.__call__`` — ``mamba/mamba1.py:160-198``: ``A = -exp(A_log)``; B, C and the
+  low-rank delta from linear maps of the input; ``delta = softplus(dt_proj(.) + bias)``;
+  scan (``oracle/assoc_torch.py``, the reference's ``selective_scan_reference``);
+  ``y += D * u``.
+* ``Mamba.__call__`` — ``mamba/mamba1.py:300-337``: norm, two up-projections, causal
+  depthwise conv (``nnx.Conv(..., feature_group_count=D, padding="CAUSAL")``,
+  ``:250-255``: out[t] = bias + sum_k w[k] x[t - (K-1) + k]) + silu, S6, times
+  ``silu(z)``, down-projection, residual.
+* Stack — ``experiments/mamba_inductionheads.py:85-120``: embedding, blocks, final
+  RMSNorm (``nnx.RMSNorm(epsilon=1e-5)``), head; the head is tied to the embedding here.
+
+Parameters come in a dict named like the product's ``MambaLM.state_dict()`` so a test can
+copy one model into the other; the x_proj rows are [dt | B | C] (the reference's
+``Linear_R``, ``s_B``, ``s_C``).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .assoc_torch import selective_scan_reference
+
+
+def rmsnorm(x, weight, eps=1e-5):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * weight
+
+
+def causal_depthwise_conv(x, weight, bias):
+    """x (B, L, D), weight (D, K), bias (D): out[t] = bias + sum_k w[k] x[t - (K-1) + k]."""
+    k = weight.shape[1]
+    xp = F.pad(x, (0, 0, k - 1, 0))
+    length = x.shape[1]
+    out = bias.expand_as(x).clone()
+    for j in range(k):
+        out = out + weight[:, j] * xp[:, j:j + length, :]
+    return out
+
+
+def s6(p, prefix, u, dt_rank, d_state, euler=True):
+    x_dbl = u @ p[prefix + "x_proj"].t()
+    r, n = dt_rank, d_state
+    delta = F.softplus(x_dbl[..., :r] @ p[prefix + "dt_proj"].t() + p[prefix + "dt_bias"])
+    A = -torch.exp(p[prefix + "A_log"])
+    y, _ = selective_scan_reference(A, delta, x_dbl[..., r:r + n], x_dbl[..., r + n:], u,
+                                    use_euler_barB_approx=euler)
+    return y + p[prefix + "D"] * u
+
+
+def mamba_block(p, prefix, h, dt_rank, d_state, euler=True):
+    x = rmsnorm(h, p[prefix + "norm.weight"])
+    projed = x @ p[prefix + "in_proj"].t()
+    skip = F.silu(x @ p[prefix + "z_proj"].t())
+    u = F.silu(causal_depthwise_conv(projed, p[prefix + "conv_weight"], p[prefix + "conv_bias"]))
+    y = s6(p, prefix + "s6.", u, dt_rank, d_state, euler)
+    return (y * skip) @ p[prefix + "out_proj"].t() + h
+
+
+def mamba_lm(p, tokens, n_layers, dt_rank, d_state, euler=True):
+    """tokens (B, L) -> logits (B*L, vocab) in (b, t) row order."""
+    h = p["embedding"][tokens]
+    for i in range(n_layers):
+        h = mamba_block(p, f"blocks.{i}.", h, dt_rank, d_state, euler)
+    hn = rmsnorm(h, p["final_norm.weight"])
+    logits = hn @ p["embedding"].t()
+    return logits.reshape(-1, logits.shape[-1])

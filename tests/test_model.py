@@ -1,0 +1,133 @@
+"""Mamba-1 model plumbing around the scan (callers: mamba/mamba1.py:160-198, 300-337).
+
+CPU: the model oracle's pieces against independent routines (torch conv1d, torch
+rms_norm, the float64 scan oracle with its fused extras), and the product's channel-major
+norm against the oracle's (B, L, D) form.
+GPU: the channel-major ``MambaLM`` (HIP scan) against the oracle model in float64 on the
+CPU with the same weights, at the reference's CPU-plumbing shape (config 1: 2 layers,
+d_model 64, expand 2, N 16, d_conv 4, RMSNorm, tied embeddings, vocab 16, B 8, L 256).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mamba_amd.mamba1 import MambaLM, RMSNormCM
+from oracle import mamba1_torch as ref
+from oracle import scan64
+
+C1 = dict(vocab=16, d_model=64, n_layers=2, expand=2, d_state=16, d_conv=4, batch=8, length=256)
+
+
+def test_oracle_conv_matches_torch_conv1d():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 50, 6, generator=g, dtype=torch.float64)
+    w = torch.randn(6, 4, generator=g, dtype=torch.float64)
+    b = torch.randn(6, generator=g, dtype=torch.float64)
+    got = ref.causal_depthwise_conv(x, w, b)
+    want = F.conv1d(F.pad(x.transpose(1, 2), (3, 0)), w[:, None, :], b, groups=6).transpose(1, 2)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    # causality: changing x at step t leaves outputs before t unchanged
+    x2 = x.clone()
+    x2[:, 20] += 1.0
+    assert torch.equal(ref.causal_depthwise_conv(x2, w, b)[:, :20], got[:, :20])
+
+
+def test_oracle_rmsnorm_matches_torch():
+    x = torch.randn(4, 9, 32, dtype=torch.float64)
+    w = torch.randn(32, dtype=torch.float64)
+    torch.testing.assert_close(ref.rmsnorm(x, w), F.rms_norm(x, (32,), w, eps=1e-5))
+
+
+def small_params(d_model=8, expand=2, d_state=4, dt_rank=2, vocab=11, n_layers=2, seed=0):
+    torch.manual_seed(seed)
+    m = MambaLM(vocab, d_model, n_layers, expand, d_state, dt_rank, 4)
+    return {k: v.detach().double() for k, v in m.state_dict().items()}, m
+
+
+@pytest.mark.parametrize("euler", [True, False])
+def test_oracle_s6_matches_scan64(euler):
+    p, _ = small_params()
+    pre = "blocks.0.s6."
+    rng = np.random.default_rng(1)
+    u = torch.from_numpy(rng.standard_normal((2, 30, 16)))
+    got = ref.s6(p, pre, u, 2, 4, euler)
+    x_dbl = (u @ p[pre + "x_proj"].t()).numpy()
+    dt_raw = x_dbl[..., :2] @ p[pre + "dt_proj"].t().numpy()
+    sw = lambda a: np.ascontiguousarray(np.swapaxes(a, 1, 2))
+    fw = scan64.forward(sw(u.numpy()), sw(dt_raw), -np.exp(p[pre + "A_log"].numpy()), sw(x_dbl[..., 2:6]),
+                        sw(x_dbl[..., 6:]), D=p[pre + "D"].numpy(), delta_bias=p[pre + "dt_bias"].numpy(),
+                        delta_softplus=True, discretization="euler" if euler else "zoh")
+    np.testing.assert_allclose(got.numpy(), np.swapaxes(fw["out"], 1, 2), rtol=1e-9, atol=1e-12)
+
+
+def test_oracle_block_gate_matches_scan64_gate():
+    p, _ = small_params()
+    pre = "blocks.1."
+    rng = np.random.default_rng(2)
+    h = torch.from_numpy(rng.standard_normal((2, 25, 8)))
+    got = ref.mamba_block(p, pre, h, 2, 4)
+    x = ref.rmsnorm(h, p[pre + "norm.weight"])
+    u = F.silu(ref.causal_depthwise_conv(x @ p[pre + "in_proj"].t(), p[pre + "conv_weight"], p[pre + "conv_bias"]))
+    z = x @ p[pre + "z_proj"].t()
+    s = pre + "s6."
+    x_dbl = (u @ p[s + "x_proj"].t()).numpy()
+    sw = lambda a: np.ascontiguousarray(np.swapaxes(np.asarray(a), 1, 2))
+    fw = scan64.forward(sw(u.numpy()), sw(x_dbl[..., :2] @ p[s + "dt_proj"].t().numpy()),
+                        -np.exp(p[s + "A_log"].numpy()), sw(x_dbl[..., 2:6]), sw(x_dbl[..., 6:]),
+                        D=p[s + "D"].numpy(), z=sw(z.numpy()), delta_bias=p[s + "dt_bias"].numpy(),
+                        delta_softplus=True)
+    want = np.swapaxes(fw["out"], 1, 2) @ p[pre + "out_proj"].t().numpy() + h.numpy()
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-9, atol=1e-12)
+
+
+def test_channel_major_rmsnorm_matches_oracle():
+    x = torch.randn(3, 7, 12)
+    norm = RMSNormCM(12)
+    with torch.no_grad():
+        norm.weight.uniform_(0.5, 1.5)
+    got = norm(x.permute(2, 0, 1).reshape(12, 21)).view(12, 3, 7).permute(1, 2, 0)
+    torch.testing.assert_close(got, ref.rmsnorm(x, norm.weight.detach()), rtol=1e-5, atol=1e-6)
+
+
+def test_parameter_initialisation_follows_reference():
+    _, m = small_params(d_model=64, d_state=16, dt_rank=None)
+    s6 = m.blocks[0].s6
+    assert s6.dt_rank == 4  # from d_model: ceil(64 / 16) (mamba/mamba1.py:228-231)
+    torch.testing.assert_close(-torch.exp(s6.A_log[3]), -torch.arange(1, 17, dtype=torch.float32))
+    dt = F.softplus(s6.dt_bias.detach())
+    assert float(dt.min()) >= 1e-4 * 0.999 and float(dt.max()) <= 0.1 * 1.001
+    assert torch.equal(s6.D.detach(), torch.ones(128))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("euler", [True, False])
+def test_model_matches_oracle_on_gpu(euler):
+    print(f"case model c1 euler={euler}", flush=True)
+    torch.manual_seed(0)
+    cfg = C1
+    dev = "cuda"
+    model = MambaLM(cfg["vocab"], cfg["d_model"], cfg["n_layers"], cfg["expand"], cfg["d_state"], None,
+                    cfg["d_conv"], use_euler_barB_approx=euler, device=dev)
+    g = torch.Generator().manual_seed(0)
+    tokens = torch.randint(0, cfg["vocab"], (cfg["batch"], cfg["length"]), generator=g)
+    targets = torch.roll(tokens, -1, dims=1).reshape(-1)
+    logits = model(tokens.to(dev), act_dtype=torch.float32)
+    loss = F.cross_entropy(logits.float(), targets.to(dev))
+    loss.backward()
+    torch.cuda.synchronize()
+
+    p = {k: v.detach().cpu().double().requires_grad_(True) for k, v in model.state_dict().items()}
+    dt_rank = model.blocks[0].s6.dt_rank
+    ref_logits = ref.mamba_lm(p, tokens, cfg["n_layers"], dt_rank, cfg["d_state"], euler)
+    ref_loss = F.cross_entropy(ref_logits, targets)
+    ref_loss.backward()
+    torch.testing.assert_close(logits.detach().cpu().double(), ref_logits.detach(), rtol=1e-4, atol=1e-4)
+    assert abs(loss.item() - ref_loss.item()) < 1e-5
+    named = dict(model.named_parameters())
+    for k, v in p.items():
+        got = named[k].grad.detach().cpu().double()
+        scale = float(v.grad.abs().max())
+        err = float((got - v.grad).abs().max())
+        print(f"  grad {k:28s} max|g|={scale:.3e} max_err={err:.3e}", flush=True)
+        assert err <= 1e-3 * scale + 1e-7, k
