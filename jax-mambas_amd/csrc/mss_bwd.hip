@@ -6,7 +6,7 @@
 // cotangent, du/ddelta/dA/dB/dC formulas) and its dormant fused branches :151-203,
 // :442-485 (softplus, z gate, D, delta bias, initial-state gradient).
 //
-// Mapping: one wave per channel, lane = segment of kT steps, chunk = 64*kT = 1024 steps
+// Mapping: one wave per channel, lane = segment of kT steps, chunk = 64*kT = 512 steps
 // (the granularity of the forward's `carries` residual, so no forward recompute across
 // chunks is needed). A workgroup of kW waves walks K rounds of kW channels of one batch
 // row ("channel block") and every chunk from last to first. Per chunk, per state n:
@@ -16,16 +16,17 @@
 //            the chunk to the right (or dlast), then a re-run producing lambda_t and all
 //            per-step gradient terms
 // dB/dC are sums over channels: each wave adds its per-(n, t) terms into an LDS
-// accumulator shared by the workgroup (ds_add_f32), flushed once per chunk to a
-// per-channel-block partial; a second kernel sums the partials in a fixed order.
+// accumulator shared by the workgroup (rows owned in rotation, plain read-add-write),
+// flushed once per chunk to a per-channel-block partial; a second kernel sums the
+// partials in a fixed order.
 // This replaces the reference's one-global-atomic-per-(b,d,n,t) scheme
 // (selective_scan_bwd_kernel.cuh:295-318).
 #include "mss_common.h"
 
 namespace mss {
 
-constexpr int kBwdT = 16;
-constexpr int kBwdW = 8;
+constexpr int kBwdT = 8;
+constexpr int kBwdW = 12;
 constexpr int kMaxChanPerBlock = 64;
 
 template <int kT, int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
@@ -431,8 +432,8 @@ static hipError_t launch_bwd_io(const BwdParams& p, int zoh, hipStream_t stream)
 int bwd_chan_per_block(int batch, int dim) {
   // Enough channel rounds per workgroup that ~one workgroup per CU (256 CUs) covers the
   // problem, bounded by the LDS bookkeeping size. Depends on shapes only.
-  const long long octets = (static_cast<long long>(batch) * dim + kBwdW - 1) / kBwdW;
-  long long k = octets / 256;
+  const long long groups = (static_cast<long long>(batch) * dim + kBwdW - 1) / kBwdW;
+  long long k = groups / 256;
   if (k < 1) k = 1;
   if (k > kMaxChanPerBlock / kBwdW) k = kMaxChanPerBlock / kBwdW;
   const long long per_row = (dim + kBwdW - 1) / kBwdW;

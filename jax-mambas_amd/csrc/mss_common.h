@@ -16,7 +16,7 @@ namespace mss {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxN = 16;
-constexpr int kCarryChunk = 1024;
+constexpr int kCarryChunk = 512;
 constexpr int kRefChunk = 2048;
 
 struct bf16_t {
@@ -257,7 +257,7 @@ struct FwdParams {
   int delta_softplus;
   int vec_io;  // 16-byte vector access legal for u/delta/z/out rows
   int vec_bc;  // ... for B/C rows
-  int n_carry;  // ceil(L / 1024)
+  int n_carry;  // ceil(L / kCarryChunk)
   int n_ref;    // ceil(L / 2048)
   long long io_sb, io_sd;  // row strides (elements) of u/delta/z/out/y_pre: batch, channel
   long long bc_sb, bc_sn;  // row strides of B/C: batch, state

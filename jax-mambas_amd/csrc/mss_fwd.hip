@@ -289,7 +289,7 @@ void fwd_kernel(FwdParams p) {
         }
         const float run_new = readlane(hend, 63);
         if (lane == 0) s_run[w][n] = run_new;
-        // Residuals: state at each 1024-step boundary; reference (prod, h) at 2048 ends.
+        // Residuals: state at each 512-step boundary; reference (prod, h) at 2048 ends.
         if (p.carries && ((tl + kT) % kCarryChunk == 0)) {
           const int cidx = (tl + kT) / kCarryChunk - 1;
           if (cidx < p.n_carry) p.carries[(chan * p.n_carry + cidx) * N + n] = hend;

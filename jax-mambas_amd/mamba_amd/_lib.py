@@ -24,7 +24,7 @@ MSS_BF16 = 1
 MSS_EULER = 0
 MSS_ZOH = 1
 MSS_MAX_DSTATE = 16
-MSS_CARRY_CHUNK = 1024
+MSS_CARRY_CHUNK = 512
 MSS_REF_CHUNK = 2048
 
 # Every symbol include/mamba_selective_scan.h declares.
