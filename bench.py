@@ -15,8 +15,11 @@ Fields beyond the driver contract:
   cpu_baseline  torch-CPU restatement of the reference's pure-JAX scan path
                 (oracle/assoc_torch.py) timed on this host on a channel slice
   fwd_bwd_hbm_frac  (fwd + bwd algorithmic bytes) / step time / 8 TB/s
+  configs       per config (c2 and, by default, c3 bf16 and c4 variable-length): ms fwd/bwd,
+                tokens/s, algorithmic MB and HBM fractions, and a CPU baseline of its own
   train_c5      the metric's second half: tokens/s of one training step of the Mamba-1
                 130M-shape LM (config 5) through the HIP scan
+Inputs are drawn on the GPU from each config's recipe (seeded torch generator).
 """
 from __future__ import annotations
 
@@ -55,47 +58,66 @@ def read_traffic(kernel_tag):
     return None
 
 
+def gpu_inputs(torch, cfg, seed=0):
+    """The config's input recipe (configs.py) drawn on the GPU with a seeded torch
+    generator: u, delta_raw, z, dout, B, C ~ N(0, 1) in the config's activation dtype;
+    delta_bias = inverse softplus of U[1e-3, 1e-1]; A = -(n + 1); D = 1. Variable-length
+    configs take lengths from np.random.default_rng(seed).integers(lo, hi + 1, B)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    b, d, l, n = cfg.batch, cfg.dim, cfg.length, cfg.dstate
+    act = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
+    t = {}
+    for k, shape in (("u", (b, d, l)), ("delta", (b, d, l)), ("z", (b, d, l)), ("dout", (b, d, l)),
+                     ("B", (b, n, l)), ("C", (b, n, l))):
+        t[k] = torch.randn(shape, generator=g, device="cuda").to(act)
+    dt = torch.rand(d, generator=g, device="cuda") * (1e-1 - 1e-3) + 1e-3
+    t["delta_bias"] = dt + torch.log(-torch.expm1(-dt))
+    t["A"] = -(torch.arange(n, device="cuda", dtype=torch.float32) + 1).repeat(d, 1)
+    t["D"] = torch.ones(d, device="cuda")
+    lens = None
+    if cfg.varlen is not None:
+        lo, hi = cfg.varlen
+        lens = np.random.default_rng(seed).integers(lo, hi + 1, size=b).astype(np.int32)
+        t["seq_lens"] = torch.from_numpy(lens).cuda()
+    return t, lens
+
+
 def gpu_step_setup(torch, cfg):
     from mamba_amd import _lib
-    from mamba_amd.configs import make_scan_inputs
 
     lib = _lib.register_hip_kernel()
-    x = make_scan_inputs(cfg, seed=0, with_z=True, with_dout=True)
+    t, lens = gpu_inputs(torch, cfg)
     dev = "cuda"
-    t = {k: torch.from_numpy(v).to(dev) for k, v in x.items()}
     b, d, l, n = cfg.batch, cfg.dim, cfg.length, cfg.dstate
+    io = _lib.MSS_BF16 if cfg.dtype == "bf16" else _lib.MSS_F32
     n_carry = (l + _lib.MSS_CARRY_CHUNK - 1) // _lib.MSS_CARRY_CHUNK
     t["out"] = torch.empty_like(t["u"])
     t["last"] = torch.empty(b, d, n, device=dev)
     t["carries"] = torch.empty(b, d, n_carry, n, device=dev)
     t["y_pre"] = torch.empty_like(t["u"])
     t["dlast"] = torch.zeros(b, d, n, device=dev)
-    for k in ("u", "delta", "z"):
+    for k in ("u", "delta", "z", "A", "B", "C", "D", "delta_bias"):
         t["d" + k] = torch.empty_like(t[k])
-    for k in ("A", "B", "C", "D", "delta_bias"):
-        t["d" + k] = torch.empty_like(t[k])
-    P = lambda k: t[k].data_ptr()
-    fa = _lib.FwdArgs(batch=b, dim=d, seqlen=l, dstate=n, discretization=_lib.MSS_EULER, delta_softplus=1,
-                      io_dtype=_lib.MSS_F32, bc_dtype=_lib.MSS_F32, u=P("u"), delta=P("delta"), A=P("A"),
-                      B=P("B"), C=P("C"), D=P("D"), z=P("z"), delta_bias=P("delta_bias"),
-                      out=P("out"), last_state=P("last"), carries=P("carries"), y_pre=P("y_pre"))
-    ba = _lib.BwdArgs(batch=b, dim=d, seqlen=l, dstate=n, discretization=_lib.MSS_EULER, delta_softplus=1,
-                      io_dtype=_lib.MSS_F32, bc_dtype=_lib.MSS_F32, u=P("u"), delta=P("delta"), A=P("A"),
-                      B=P("B"), C=P("C"), D=P("D"), z=P("z"), delta_bias=P("delta_bias"),
-                      carries=P("carries"), y_pre=P("y_pre"), dout=P("dout"), dlast_state=P("dlast"), du=P("du"),
-                      ddelta=P("ddelta"), dA=P("dA"), dB=P("dB"), dC=P("dC"), dD=P("dD"), dz=P("dz"),
+    P = lambda k: t[k].data_ptr() if k in t else None
+    common = dict(batch=b, dim=d, seqlen=l, dstate=n, discretization=_lib.MSS_EULER, delta_softplus=1,
+                  io_dtype=io, bc_dtype=io, u=P("u"), delta=P("delta"), A=P("A"), B=P("B"), C=P("C"),
+                  D=P("D"), z=P("z"), delta_bias=P("delta_bias"), seq_lens=P("seq_lens"))
+    fa = _lib.FwdArgs(**common, out=P("out"), last_state=P("last"), carries=P("carries"), y_pre=P("y_pre"))
+    ba = _lib.BwdArgs(**common, carries=P("carries"), y_pre=P("y_pre"), dout=P("dout"), dlast_state=P("dlast"),
+                      du=P("du"), ddelta=P("ddelta"), dA=P("dA"), dB=P("dB"), dC=P("dC"), dD=P("dD"), dz=P("dz"),
                       ddelta_bias=P("ddelta_bias"))
     ws_bytes = int(lib.mss_bwd_workspace_bytes(ba))
     t["ws"] = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     ba.workspace = t["ws"].data_ptr()
     ba.workspace_bytes = ws_bytes
-    return lib, t, fa, ba
+    return lib, t, fa, ba, lens
 
 
 def run_gpu(torch, cfg, steps, warmup):
+    """Times `steps` fwd+bwd steps of the scan at `cfg`; returns per-kernel means (ms)."""
     from mamba_amd import _lib
 
-    lib, t, fa, ba = gpu_step_setup(torch, cfg)
+    lib, t, fa, ba, lens = gpu_step_setup(torch, cfg)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
@@ -115,7 +137,7 @@ def run_gpu(torch, cfg, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    log(f"[bench] warmup done ({warmup} steps)")
+    log(f"[bench] {cfg.name}: warmup done ({warmup} steps)")
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -126,12 +148,36 @@ def run_gpu(torch, cfg, steps, warmup):
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    fwd = [e[0].elapsed_time(e[1]) for e in evs]
-    bws = [e[1].elapsed_time(e[2]) for e in evs]
-    red = [e[2].elapsed_time(e[3]) for e in evs]
-    log(f"[bench] timed {steps} steps: {total_ms / steps:.4f} ms/step "
-        f"(fwd {np.mean(fwd):.4f}, bwd_scan {np.mean(bws):.4f}, bwd_reduce {np.mean(red):.4f} ms)")
-    return total_ms / steps, float(np.mean(fwd)), float(np.mean(bws)), float(np.mean(red))
+    fwd = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    bws = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    red = float(np.mean([e[2].elapsed_time(e[3]) for e in evs]))
+    log(f"[bench] {cfg.name}: timed {steps} steps: {total_ms / steps:.4f} ms/step "
+        f"(fwd {fwd:.4f}, bwd_scan {bws:.4f}, bwd_reduce {red:.4f} ms)")
+    del t
+    torch.cuda.empty_cache()
+    return dict(ms=total_ms / steps, fwd=fwd, bwd_scan=bws, bwd_reduce=red, lens=lens)
+
+
+def scan_report(cfg, r):
+    """ms, tokens/s and fractions of the 8 TB/s HBM roofline for one config's timings."""
+    from mamba_amd.configs import algorithmic_bytes
+
+    lens = r["lens"]
+    fwd_b, bwd_b = algorithmic_bytes(cfg, lens)
+    tokens = int(np.sum(lens)) if lens is not None else cfg.batch * cfg.length
+    frac = lambda nbytes, ms: round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    rep = {
+        "workload": cfg.description, "dtype": cfg.dtype,
+        "ms_fwd": round(r["fwd"], 5), "ms_bwd": round(r["bwd_scan"] + r["bwd_reduce"], 5),
+        "ms_fwd_bwd": round(r["ms"], 5), "tokens_per_s": round(tokens / (r["ms"] * 1e-3), 1),
+        "algorithmic_mb": {"fwd": round(fwd_b / 1e6, 1), "bwd": round(bwd_b / 1e6, 1)},
+        "hbm_frac": {"fwd": frac(fwd_b, r["fwd"]), "bwd": frac(bwd_b, r["bwd_scan"] + r["bwd_reduce"]),
+                     "fwd_bwd": frac(fwd_b + bwd_b, r["ms"])},
+    }
+    if lens is not None:
+        rep["seq_lens"] = [int(x) for x in lens]
+        rep["valid_fraction"] = round(float(np.sum(lens)) / (cfg.batch * cfg.length), 4)
+    return rep
 
 
 C5_MODEL = dict(vocab=50280, d_model=768, n_layers=24, expand=2, d_state=16, dt_rank=48, d_conv=4)
@@ -197,19 +243,23 @@ def run_train_c5(torch, steps, warmup):
     }
 
 
-def cpu_baseline(torch, cfg, target_s):
-    """Reference composition on the CPU: softplus(delta + bias) -> pure-JAX-style scan
-    (oracle/assoc_torch.py, mamba/selective_scan_cuda.py:56-90) -> + D*u -> * silu(z);
-    loss-weighted backward through autograd. Timed on a slice of channels (channels are
-    independent) and scaled to the full channel count."""
+def cpu_baseline(torch, cfg, target_s, lens=None, d0=32):
+    """Reference composition on the CPU: softplus(delta + bias) (x validity mask for
+    variable lengths, mamba/mamba1.py:165-168) -> pure-JAX-style scan (oracle/assoc_torch.py,
+    mamba/selective_scan_cuda.py:56-90) -> + D*u -> * silu(z); loss-weighted backward
+    through autograd, in fp32 (bf16 configs use bf16-rounded inputs). Timed on a slice of
+    channels (channels are independent) and scaled to the full channel count."""
     from mamba_amd.configs import make_scan_inputs, ScanConfig
     from oracle.assoc_torch import selective_scan_reference
 
     threads = max(1, min(len(os.sched_getaffinity(0)), 16))
     torch.set_num_threads(threads)
+    mask = None
+    if lens is not None:
+        mask = (torch.arange(cfg.length)[None, :, None] < torch.as_tensor(lens)[:, None, None]).float()
 
     def run(dslice):
-        sub = ScanConfig("slice", cfg.batch, dslice, cfg.length, cfg.dstate, "f32")
+        sub = ScanConfig("slice", cfg.batch, dslice, cfg.length, cfg.dstate, cfg.dtype)
         x = make_scan_inputs(sub, seed=0, with_z=True, with_dout=True)
         tr = lambda a: torch.from_numpy(np.ascontiguousarray(np.swapaxes(a, 1, 2)))
         u, dr, z, dout = (tr(x[k]) for k in ("u", "delta", "z", "dout"))
@@ -221,33 +271,36 @@ def cpu_baseline(torch, cfg, target_s):
             v.requires_grad_(True)
         t0 = time.perf_counter()
         deltas = torch.nn.functional.softplus(dr + bias)
+        if mask is not None:
+            deltas = deltas * mask
         y, last = selective_scan_reference(A, deltas, Bs, Cs, u)
         out = (y + D * u) * torch.nn.functional.silu(z)
         loss = (out * dout).sum() + last.sum() * 0.0
         loss.backward()
         return time.perf_counter() - t0
 
-    d0 = 32
     run(d0)
     t_probe = run(d0)
-    dslice = int(np.clip(d0 * (target_s / 4.0) / max(t_probe, 1e-3), d0, cfg.dim)) // 8 * 8
-    log(f"[bench] cpu baseline probe D={d0}: {t_probe:.2f} s; timing slice D={dslice} x3 on {threads} threads")
-    run(dslice)
+    dslice = max(8, int(np.clip(d0 * (target_s / 4.0) / max(t_probe, 1e-3), d0, cfg.dim)) // 8 * 8)
+    log(f"[bench] {cfg.name} cpu baseline probe D={d0}: {t_probe:.2f} s; timing slice D={dslice} x3 "
+        f"on {threads} threads")
+    if dslice != d0:
+        run(dslice)
     times = []
     for i in range(3):
         times.append(run(dslice))
-        log(f"[bench] cpu baseline rep {i}: {times[-1]:.2f} s")
+        log(f"[bench] {cfg.name} cpu baseline rep {i}: {times[-1]:.2f} s")
     t_med = float(np.median(times))
     t_full = t_med * cfg.dim / dslice
-    tokens = cfg.batch * cfg.length
+    tokens = int(np.sum(lens)) if lens is not None else cfg.batch * cfg.length
     return {
         "value": tokens / t_full,
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"B={cfg.batch} L={cfg.length} N={cfg.dstate} fp32, {dslice} of {cfg.dim} channels, "
-                   f"fwd+bwd (autograd) median of 3 = {t_med:.3f} s, scaled x{cfg.dim / dslice:.1f} "
-                   f"to all channels ({t_full:.2f} s per step)"),
+        "sample": (f"{cfg.name}: B={cfg.batch} L={cfg.length} N={cfg.dstate} ({cfg.dtype} inputs, fp32 math), "
+                   f"{dslice} of {cfg.dim} channels, fwd+bwd (autograd) median of 3 = {t_med:.3f} s, "
+                   f"scaled x{cfg.dim / dslice:.1f} to all channels ({t_full:.2f} s per step)"),
     }
 
 
@@ -258,6 +311,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=8.0,
                     help="approximate CPU work for the CPU baseline (0 disables it)")
+    ap.add_argument("--configs", default="c2,c3,c4",
+                    help="scan configs to measure (c2 is always the headline line)")
+    ap.add_argument("--config-steps", type=int, default=10, help="timed steps for c3/c4")
     ap.add_argument("--train-steps", type=int, default=10,
                     help="timed config-5 training steps (0 skips the training measurement)")
     ap.add_argument("--train-warmup", type=int, default=3)
@@ -272,13 +328,14 @@ def main():
         sys.exit(2)
 
     import torch
-    from mamba_amd.configs import C2, algorithmic_bytes
+    from mamba_amd.configs import CONFIGS, C2, algorithmic_bytes
 
-    cfg = C2
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    ms, fwd_ms, bwd_ms, red_ms = run_gpu(torch, cfg, args.steps, args.warmup)
+    cfg = C2
+    r2 = run_gpu(torch, cfg, args.steps, args.warmup)
+    ms, fwd_ms, bwd_ms, red_ms = r2["ms"], r2["fwd"], r2["bwd_scan"], r2["bwd_reduce"]
     fwd_bytes, bwd_bytes = algorithmic_bytes(cfg)
     tokens = cfg.batch * cfg.length
     # Dominant kernel: the backward scan (backward algorithmic bytes attributed to it; the
@@ -299,12 +356,23 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] calibration copy of {args.calibration_copy_mib} MiB done")
         del src, dst
+    per_config = {"c2": scan_report(cfg, r2)}
+    others = [c for c in args.configs.split(",") if c and c != "c2"]
+    results = {}
+    for name in others:
+        c = CONFIGS[name]
+        results[name] = run_gpu(torch, c, args.config_steps, max(1, args.config_steps // 4))
+        per_config[name] = scan_report(c, results[name])
     train = None
     if args.train_steps > 0:
         train = run_train_c5(torch, args.train_steps, args.train_warmup)
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, cfg, args.cpu_seconds)
+        per_config["c2"]["cpu_baseline"] = cpu
+        for name in others:
+            per_config[name]["cpu_baseline"] = cpu_baseline(torch, CONFIGS[name], args.cpu_seconds / 2,
+                                                            results[name]["lens"], d0=8)
     step_bytes = fwd_bytes + bwd_bytes
     result = {
         "metric": METRIC,
@@ -326,6 +394,7 @@ def main():
         "cpu_baseline": cpu,
         "fwd_bwd_hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "kernels_ms": {"fwd": round(fwd_ms, 5), "bwd_scan": round(bwd_ms, 5), "bwd_reduce": round(red_ms, 5)},
+        "configs": per_config,
         "train_c5": train,
     }
     print(json.dumps(result), flush=True)

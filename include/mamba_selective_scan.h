@@ -133,7 +133,8 @@ typedef struct mss_bwd_args {
   mss_strides strides;   /* the forward's strides; also those of dout/du/ddelta/dz, dB/dC */
 } mss_bwd_args;
 
-/* Size of the scratch mss_bwd needs for these shapes (0 on invalid arguments). */
+/* Size of the scratch mss_bwd needs for these shapes and for whether seq_lens is given
+ * (0 on invalid arguments). */
 size_t mss_bwd_workspace_bytes(const mss_bwd_args* args);
 
 int mss_fwd(const mss_fwd_args* args, void* stream);

@@ -27,7 +27,8 @@ namespace mss {
 
 constexpr int kBwdT = 8;
 constexpr int kBwdW = 12;
-constexpr int kMaxChanPerBlock = 64;
+constexpr int kMaxChanPerBlock = 240;  // 20 rounds of 12 waves
+constexpr int kCUs = 256;               // MI355X compute units
 
 template <int kT, int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
 __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
@@ -429,14 +430,18 @@ static hipError_t launch_bwd_io(const BwdParams& p, int zoh, hipStream_t stream)
             : launch_bwd_t<false, false, io_t, bc_t>(p, stream);
 }
 
-int bwd_chan_per_block(int batch, int dim) {
-  // Enough channel rounds per workgroup that ~one workgroup per CU (256 CUs) covers the
-  // problem, bounded by the LDS bookkeeping size. Depends on shapes only.
-  const long long groups = (static_cast<long long>(batch) * dim + kBwdW - 1) / kBwdW;
-  long long k = groups / 256;
+int bwd_chan_per_block(int batch, int dim, int varlen) {
+  // One workgroup per CU holds the dB/dC accumulator (LDS), so the grid should fit one
+  // pass over the 256 CUs: the fewest channel rounds K with batch * ceil(dim / (kW*K))
+  // <= 256 (more rounds also mean fewer dB/dC partials to reduce). With variable lengths
+  // rows finish at different times, so workgroups stay ~4x smaller and the hardware
+  // balances them. Bounded by the LDS bookkeeping size; depends on shapes only.
+  const long long per_row = (dim + kBwdW - 1) / kBwdW;  // rounds needed for a whole row
+  const long long target = varlen ? 4 * kCUs : kCUs;
+  long long k = (static_cast<long long>(batch) * per_row + target - 1) / target;
   if (k < 1) k = 1;
+  while (k < per_row && static_cast<long long>(batch) * ((per_row + k - 1) / k) > target) ++k;
   if (k > kMaxChanPerBlock / kBwdW) k = kMaxChanPerBlock / kBwdW;
-  const long long per_row = (dim + kBwdW - 1) / kBwdW;
   if (k > per_row) k = per_row;
   return static_cast<int>(k) * kBwdW;
 }

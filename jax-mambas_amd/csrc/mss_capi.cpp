@@ -22,7 +22,7 @@ hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16
                            hipStream_t stream);
 hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB, void* dC,
                              float* dD, float* dbias, hipStream_t stream);
-int bwd_chan_per_block(int batch, int dim);
+int bwd_chan_per_block(int batch, int dim, int varlen);
 hipError_t launch_conv(const ConvParams& p, bool bwd, bool vec, bool silu, bool io_bf16,
                        hipStream_t stream);
 hipError_t launch_conv_reduce(const ConvParams& p, int n_tiles, float* dw, float* dbias,
@@ -106,9 +106,9 @@ struct BwdLayout {
   size_t off_dA = 0, off_dD = 0, off_db = 0, total = 0;
 };
 
-BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate) {
+BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate, bool varlen) {
   BwdLayout l;
-  l.chan_per_block = mss::bwd_chan_per_block(batch, dim);
+  l.chan_per_block = mss::bwd_chan_per_block(batch, dim, varlen ? 1 : 0);
   l.n_blocks_d = (dim + l.chan_per_block - 1) / l.chan_per_block;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   l.part_stride = (static_cast<size_t>(batch) * 2 * dstate * seqlen + 63) / 64 * 64;
@@ -240,7 +240,7 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
 }
 
 int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream) {
-  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate);
+  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr);
   char* ws = static_cast<char*>(a->workspace);
   bool owned = false;
   if (ws == nullptr) {
@@ -337,7 +337,7 @@ const char* mss_last_hip_error(void) { return g_last_hip_error.c_str(); }
 
 size_t mss_bwd_workspace_bytes(const mss_bwd_args* a) {
   if (a == nullptr || check_dims(a->batch, a->dim, a->seqlen, a->dstate) != MSS_OK) return 0;
-  return bwd_layout(a->batch, a->dim, a->seqlen, a->dstate).total;
+  return bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr).total;
 }
 
 int mss_fwd(const mss_fwd_args* args, void* stream) {
