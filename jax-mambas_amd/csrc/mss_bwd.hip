@@ -21,6 +21,8 @@
 // partials in a fixed order.
 // This replaces the reference's one-global-atomic-per-(b,d,n,t) scheme
 // (selective_scan_bwd_kernel.cuh:295-318).
+#include <type_traits>
+
 #include "mss_common.h"
 
 namespace mss {
@@ -86,8 +88,13 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   for (int c = n_chunks - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
     const int tl = t0 + lane * kT;
-    const bool fast = vec_io && (t0 + kChunk <= L);     // wave-uniform
-    const bool fast_bc = vec_bc && (t0 + kChunk <= L);  // wave-uniform
+    // A chunk wholly inside the row's length, with vector-aligned rows, runs a specialised
+    // body without bounds checks or validity masks (every chunk but a ragged last one).
+    const bool full = vec_io && vec_bc && (t0 + kChunk <= len);  // wave-uniform
+    auto chunk_body = [&](auto full_tag) {
+    constexpr bool kFull = decltype(full_tag)::value;
+    const bool fast = kFull || (vec_io && (t0 + kChunk <= L));     // wave-uniform
+    const bool fast_bc = kFull || (vec_bc && (t0 + kChunk <= L));  // wave-uniform
     for (int k = 0; k < K; ++k) {
       const int cl = k * kW + w;
       const int d_raw = blk * p.chan_per_block + cl;
@@ -98,7 +105,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       io_t* __restrict__ du_row = static_cast<io_t*>(p.du) + row;
       io_t* __restrict__ dd_row = static_cast<io_t*>(p.ddelta) + row;
 
-      if (t0 >= len) {  // whole chunk past this row's length: zero gradients, carry passes
+      if (!kFull && t0 >= len) {  // whole chunk past this row's length: zero gradients, carry passes
         if (!active) continue;
         float zero[kT];
 #pragma unroll
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         load_seg<kT>(static_cast<const io_t*>(p.y_pre) + row, tl, L, fast, yp);
 #pragma unroll
         for (int j = 0; j < kT; ++j) {
-          const bool valid = tl + j < len;
+          const bool valid = kFull || tl + j < len;
           const float go = valid ? g[j] : 0.f;
           const float sz = sigmoid(zr[j]);
           yp[j] = go * yp[j] * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       }
 #pragma unroll
       for (int j = 0; j < kT; ++j) {
-        const bool valid = tl + j < len;
+        const bool valid = kFull || tl + j < len;
         const float x = dlt[j] + bias;
         float dv = p.delta_softplus ? softplus(x) : x;
         dv = valid ? dv : 0.f;
@@ -246,7 +253,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
           accn[j * 128] = accv[2 * j];
           accn[j * 128 + 64] = accv[2 * j + 1];
         }
-        if (i + 1 < N) {
+        {  // next state's rows (after the last state: an unused in-bounds reload)
           const int nn = n + 1 == N ? 0 : n + 1;
           load_seg<kT>(Bb + nn * p.bc_sn, tl, L, fast_bc, bv);
           load_seg<kT>(Cb + nn * p.bc_sn, tl, L, fast_bc, cv);
@@ -265,7 +272,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       float duv[kT], ddv[kT];
 #pragma unroll
       for (int j = 0; j < kT; ++j) {
-        const bool valid = tl + j < len;
+        const bool valid = kFull || tl + j < len;
         float du_j, dd_j;
         if constexpr (kZOH) {
           du_j = __builtin_fmaf(Dv, g[j], s1[j]);
@@ -293,6 +300,13 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         s_dD[cl] += dD_sum;
         s_db[cl] += db_sum;
       }
+    }
+
+    };
+    if (full) {
+      chunk_body(std::true_type{});
+    } else {
+      chunk_body(std::false_type{});
     }
 
     // ---- flush this chunk's dB/dC sums over the block's channels
