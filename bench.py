@@ -186,10 +186,11 @@ C5_BATCH, C5_LENGTH = 8, 2048
 
 def run_train_c5(torch, steps, warmup):
     """Config 5: one training step of the Mamba-1 130M-shape LM (random init, uniform random
-    tokens): bf16 activations with fp32 master weights and residual stream, forward, fp32
-    cross-entropy over all next-token positions, backward (HIP scan backward inside),
+    tokens): bf16 activations with fp32 master weights and residual stream, forward,
+    cross-entropy (fp32 math on bf16 logits, HIP kernel) over all next-token positions,
+    backward (HIP scan, conv, norm and loss backward inside),
     fused AdamW step. Timed with events on the current stream around exactly `steps` steps."""
-    import torch.nn.functional as F
+    from mamba_amd.lm_ops import cross_entropy
     from mamba_amd.mamba1 import MambaLM
 
     torch.manual_seed(0)
@@ -205,7 +206,7 @@ def run_train_c5(torch, steps, warmup):
 
     def step():
         logits = model(inp, act_dtype=torch.bfloat16)
-        loss = F.cross_entropy(logits.float(), tgt)
+        loss = cross_entropy(logits, tgt)
         loss.backward()
         opt.step()
         opt.zero_grad(set_to_none=True)

@@ -180,6 +180,57 @@ size_t mss_conv_bwd_workspace_bytes(const mss_conv_args* args);
 int mss_conv_fwd(const mss_conv_args* args, void* stream);
 int mss_conv_bwd(const mss_conv_args* args, void* stream);
 
+/* --- Residual add + RMSNorm over the features of a channel-major stream. ----------
+ * No counterpart symbol in the reference (mamba/mamba1.py:300-337 applies
+ * nnx.RMSNorm(epsilon) to the residual stream and adds each block's output back).
+ * Matrices are [features][tokens], row-major (tokens contiguous):
+ *   forward   hn = h + delta (delta optional; hn written only then),
+ *             rstd[t] = 1/sqrt(mean_f hn^2 + eps),  x = hn * rstd * w
+ *   backward  xhat = hn*rstd,  c = mean_f w dx xhat,
+ *             dhn = dhn_in + rstd*(w dx - xhat c)  (dhn_in optional), ddelta = dhn in the
+ *             activation dtype (optional), dw = sum_t dx xhat. */
+typedef struct mss_norm_args {
+  int32_t features, tokens;
+  float eps;
+  int32_t io_dtype;    /* dtype of delta, x, dx, ddelta (the stream h/hn/dhn is float32) */
+  const float* h;      /* forward input; backward: the forward's normalised input (hn) */
+  const void* delta;   /* optional */
+  const float* weight; /* [features] */
+  float* hn;           /* written when delta is given */
+  void* x;
+  float* rstd;         /* [tokens] */
+  const void* dx;      /* backward */
+  const float* dhn_in; /* optional */
+  float* dhn;
+  void* ddelta;        /* optional */
+  float* dweight;
+  void* workspace;     /* NULL = library allocates stream-ordered */
+  size_t workspace_bytes;
+} mss_norm_args;
+
+size_t mss_norm_bwd_workspace_bytes(const mss_norm_args* args);
+int mss_norm_fwd(const mss_norm_args* args, void* stream);
+int mss_norm_bwd(const mss_norm_args* args, void* stream);
+
+/* --- Cross-entropy over bf16 logits [rows][vocab] with fp32 math. -------------------
+ * No counterpart symbol in the reference (its training loss is optax softmax
+ * cross-entropy, experiments/mamba_inductionheads.py:129-136):
+ *   forward   lse[r] = log sum_v exp(z[r][v]),  loss[r] = lse[r] - z[r][target[r]]
+ *             (NaN for a target outside [0, vocab))
+ *   backward  dz[r][v] = (*grad_scale) * (softmax(z[r])[v] - [v == target[r]])  (bf16) */
+typedef struct mss_xent_args {
+  int32_t rows, vocab;
+  const void* logits;        /* bf16 */
+  const int64_t* targets;    /* [rows] */
+  float* loss;               /* [rows] */
+  float* lse;                /* [rows] */
+  const float* grad_scale;   /* backward: device scalar */
+  void* dlogits;             /* backward: bf16 */
+} mss_xent_args;
+
+int mss_xent_fwd(const mss_xent_args* args, void* stream);
+int mss_xent_bwd(const mss_xent_args* args, void* stream);
+
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------
  * Same argument order, attribute meaning and buffer shapes as the reference's XLA-FFI
  * handlers; physical layouts as listed at the top of this file. */

@@ -28,6 +28,10 @@ hipError_t launch_conv(const ConvParams& p, bool bwd, bool vec, bool silu, bool 
 hipError_t launch_conv_reduce(const ConvParams& p, int n_tiles, float* dw, float* dbias,
                               hipStream_t stream);
 int conv_tile_steps(int vec, int io_bf16);
+hipError_t launch_norm_fwd(const NormParams& p, bool io_bf16, hipStream_t stream);
+hipError_t launch_norm_bwd(const NormParams& p, bool io_bf16, float* dw, hipStream_t stream);
+int norm_blocks(int tokens);
+hipError_t launch_xent(const XentParams& p, bool bwd, bool vec, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -404,6 +408,105 @@ int mss_conv_bwd(const mss_conv_args* args, void* stream) {
     if (e == hipSuccess) e = f;
   }
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching conv1d backward");
+}
+
+static int validate_norm(const mss_norm_args* a, bool bwd) {
+  if (a == nullptr || a->features <= 0 || a->tokens <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (!(a->eps >= 0.f)) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->io_dtype != MSS_F32 && a->io_dtype != MSS_BF16) return MSS_ERR_INVALID_ARGUMENT;
+  if (!a->h || !a->weight || !a->rstd) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->delta && !a->hn) return MSS_ERR_INVALID_ARGUMENT;
+  if (!bwd && !a->x) return MSS_ERR_INVALID_ARGUMENT;
+  if (bwd && (!a->dx || !a->dhn || !a->dweight)) return MSS_ERR_INVALID_ARGUMENT;
+  return MSS_OK;
+}
+
+static mss::NormParams pack_norm(const mss_norm_args* a) {
+  mss::NormParams p{};
+  p.features = a->features;
+  p.tokens = a->tokens;
+  p.eps = a->eps;
+  p.h = a->h;
+  p.delta = a->delta;
+  p.w = a->weight;
+  p.hn = a->hn;
+  p.x = a->x;
+  p.rstd = a->rstd;
+  p.dx = a->dx;
+  p.dhn_in = a->dhn_in;
+  p.dhn = a->dhn;
+  p.ddelta = a->ddelta;
+  return p;
+}
+
+size_t mss_norm_bwd_workspace_bytes(const mss_norm_args* a) {
+  if (a == nullptr || a->features <= 0 || a->tokens <= 0) return 0;
+  return static_cast<size_t>(mss::norm_blocks(a->tokens)) * a->features * sizeof(float);
+}
+
+int mss_norm_fwd(const mss_norm_args* args, void* stream) {
+  const int s = validate_norm(args, false);
+  if (s != MSS_OK) return s;
+  const hipError_t e = mss::launch_norm_fwd(pack_norm(args), args->io_dtype == MSS_BF16,
+                                            static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching rmsnorm forward");
+}
+
+int mss_norm_bwd(const mss_norm_args* args, void* stream) {
+  const int s = validate_norm(args, true);
+  if (s != MSS_OK) return s;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t need = mss_norm_bwd_workspace_bytes(args);
+  char* ws = static_cast<char*>(args->workspace);
+  bool owned = false;
+  if (ws == nullptr) {
+    const hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ws), need, st);
+    if (e != hipSuccess) return hip_fail(e, "allocating rmsnorm workspace");
+    owned = true;
+  } else if (args->workspace_bytes < need) {
+    return MSS_ERR_WORKSPACE;
+  }
+  mss::NormParams p = pack_norm(args);
+  p.dw_part = reinterpret_cast<float*>(ws);
+  hipError_t e = mss::launch_norm_bwd(p, args->io_dtype == MSS_BF16, args->dweight, st);
+  if (owned) {
+    const hipError_t f = hipFreeAsync(ws, st);
+    if (e == hipSuccess) e = f;
+  }
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching rmsnorm backward");
+}
+
+static int validate_xent(const mss_xent_args* a, bool bwd) {
+  if (a == nullptr || a->rows <= 0 || a->vocab <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (!a->logits || !a->targets || !a->lse) return MSS_ERR_INVALID_ARGUMENT;
+  if (!bwd && !a->loss) return MSS_ERR_INVALID_ARGUMENT;
+  if (bwd && (!a->grad_scale || !a->dlogits)) return MSS_ERR_INVALID_ARGUMENT;
+  return MSS_OK;
+}
+
+static int run_xent(const mss_xent_args* a, bool bwd, hipStream_t st) {
+  mss::XentParams p{};
+  p.rows = a->rows;
+  p.vocab = a->vocab;
+  p.z = static_cast<const mss::bf16_t*>(a->logits);
+  p.target = reinterpret_cast<const long long*>(a->targets);
+  p.loss = a->loss;
+  p.lse = a->lse;
+  p.grad_scale = a->grad_scale;
+  p.dz = static_cast<mss::bf16_t*>(a->dlogits);
+  const bool vec = (a->vocab % 8 == 0) && aligned16(a->logits) && aligned16(a->dlogits);
+  const hipError_t e = mss::launch_xent(p, bwd, vec, st);
+  return e == hipSuccess ? MSS_OK : hip_fail(e, bwd ? "launching cross-entropy backward" : "launching cross-entropy forward");
+}
+
+int mss_xent_fwd(const mss_xent_args* args, void* stream) {
+  const int s = validate_xent(args, false);
+  return s != MSS_OK ? s : run_xent(args, false, static_cast<hipStream_t>(stream));
+}
+
+int mss_xent_bwd(const mss_xent_args* args, void* stream) {
+  const int s = validate_xent(args, true);
+  return s != MSS_OK ? s : run_xent(args, true, static_cast<hipStream_t>(stream));
 }
 
 int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,

@@ -239,6 +239,33 @@ __device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L
 
 // ---------------------------------------------------------------------------------
 // Kernel parameter blocks (host fills them after validation).
+struct NormParams {
+  int features, tokens;
+  float eps;
+  const float* h;
+  const void* delta;    // optional, activation dtype
+  const float* w;
+  float* hn;            // written when delta is given
+  void* x;              // activation dtype
+  float* rstd;
+  // backward
+  const void* dx;       // activation dtype
+  const float* dhn_in;  // optional
+  float* dhn;
+  void* ddelta;         // optional, activation dtype
+  float* dw_part;       // [n_blocks][features]
+};
+
+struct XentParams {
+  int rows, vocab;
+  const bf16_t* z;
+  const long long* target;
+  float* loss;  // [rows]
+  float* lse;   // [rows]
+  const float* grad_scale;
+  bf16_t* dz;
+};
+
 struct ConvParams {
   int batch, dim, seqlen, width;
   long long sb, sd;  // row strides (elements) of x, y, dy, dx: batch, channel

@@ -40,6 +40,11 @@ EXPORTED_SYMBOLS = (
     "mss_conv_bwd_workspace_bytes",
     "mss_conv_fwd",
     "mss_conv_bwd",
+    "mss_norm_bwd_workspace_bytes",
+    "mss_norm_fwd",
+    "mss_norm_bwd",
+    "mss_xent_fwd",
+    "mss_xent_bwd",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -90,6 +95,22 @@ class ConvArgs(ctypes.Structure):
     ]
 
 
+class NormArgs(ctypes.Structure):
+    _fields_ = [
+        ("features", _i32), ("tokens", _i32), ("eps", ctypes.c_float), ("io_dtype", _i32),
+        ("h", _p), ("delta", _p), ("weight", _p), ("hn", _p), ("x", _p), ("rstd", _p),
+        ("dx", _p), ("dhn_in", _p), ("dhn", _p), ("ddelta", _p), ("dweight", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class XentArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", _i32), ("vocab", _i32), ("logits", _p), ("targets", _p), ("loss", _p), ("lse", _p),
+        ("grad_scale", _p), ("dlogits", _p),
+    ]
+
+
 _LIBRARY = None
 _LIBRARY_PATH = None
 
@@ -134,6 +155,14 @@ def register_hip_kernel(library_path=None):
         getattr(lib, name).restype = ctypes.c_int
     lib.mss_conv_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ConvArgs)]
     lib.mss_conv_bwd_workspace_bytes.restype = ctypes.c_size_t
+    for name in ("mss_norm_fwd", "mss_norm_bwd"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(NormArgs), _p]
+        getattr(lib, name).restype = ctypes.c_int
+    lib.mss_norm_bwd_workspace_bytes.argtypes = [ctypes.POINTER(NormArgs)]
+    lib.mss_norm_bwd_workspace_bytes.restype = ctypes.c_size_t
+    for name in ("mss_xent_fwd", "mss_xent_bwd"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(XentArgs), _p]
+        getattr(lib, name).restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

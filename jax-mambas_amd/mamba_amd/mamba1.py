@@ -29,6 +29,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .conv1d_hip import causal_conv1d_fn
+from .lm_ops import add_rmsnorm
 from .selective_scan_hip import selective_scan_fn
 
 __all__ = ["S6", "MambaBlock", "MambaLM", "RMSNormCM"]
@@ -51,17 +52,17 @@ def _matrix(x):
 
 
 class RMSNormCM(nn.Module):
-    """RMSNorm over the feature axis (dim 0) of an (features, tokens) matrix; fp32 math."""
+    """RMSNorm over the feature axis (dim 0) of a (features, tokens) fp32 stream, fused
+    with the residual add of the previous block's output (HIP kernel, lm_ops.add_rmsnorm)."""
 
     def __init__(self, dim, eps=1e-5, device=None):
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(dim, device=device))
 
-    def forward(self, x, out_dtype=None):
-        xf = x.float()
-        r = torch.rsqrt(xf.pow(2).mean(0, keepdim=True) + self.eps)
-        return (xf * r * self.weight[:, None]).to(out_dtype or x.dtype)
+    def forward(self, h, delta=None, out_dtype=torch.bfloat16):
+        """Returns (h + delta, rmsnorm(h + delta) * weight in out_dtype)."""
+        return add_rmsnorm(h, delta, self.weight, self.eps, out_dtype)
 
 
 class S6(nn.Module):
@@ -126,15 +127,17 @@ class MambaBlock(nn.Module):
         self.out_proj = nn.Parameter(_uniform_(torch.empty(d_model, d_inner, device=device),
                                                d_inner ** -0.5 * n_layers ** -0.5))
 
-    def forward(self, h, batch, seq_lens=None, act_dtype=torch.bfloat16):
-        """h: (d_model, B*L) residual stream (fp32); returns the updated stream."""
-        x = self.norm(h, act_dtype)
+    def forward(self, h, delta, batch, seq_lens=None, act_dtype=torch.bfloat16):
+        """h: (d_model, B*L) fp32 residual stream before the previous block's output `delta`
+        (act_dtype, or None for the first block) is added. Returns (h + delta, this block's
+        output): the residual add is fused into the next norm."""
+        h, x = self.norm(h, delta, act_dtype)
         xin = self.in_proj.to(act_dtype) @ x
         z = self.z_proj.to(act_dtype) @ x
         # causal depthwise conv + silu (HIP kernel), masked past each row's length
         u = _matrix(causal_conv1d_fn(_rows(xin, batch), self.conv_weight, self.conv_bias, seq_lens))
         y = self.s6(u, batch, z=z, seq_lens=seq_lens)
-        return h + (self.out_proj.to(act_dtype) @ y).float()
+        return h, self.out_proj.to(act_dtype) @ y
 
 
 class MambaLM(nn.Module):
@@ -154,7 +157,8 @@ class MambaLM(nn.Module):
         """tokens (B, L) int64 -> logits (B*L, vocab) in act_dtype (rows in (b, t) order)."""
         batch = tokens.shape[0]
         h = self.embedding[tokens.reshape(-1)].t().contiguous()   # (d_model, B*L) fp32
+        delta = None
         for blk in self.blocks:
-            h = blk(h, batch, seq_lens, act_dtype)
-        hn = self.final_norm(h, act_dtype)
+            h, delta = blk(h, delta, batch, seq_lens, act_dtype)
+        _, hn = self.final_norm(h, delta, act_dtype)
         return hn.t() @ self.embedding.to(act_dtype).t()
