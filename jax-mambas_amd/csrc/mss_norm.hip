@@ -23,7 +23,7 @@
 
 namespace mss {
 
-constexpr int kNormW = 8;
+constexpr int kNormW = 16;  // waves per workgroup (features split 16 ways)
 
 
 template <typename io_t>
@@ -38,6 +38,7 @@ __global__ __launch_bounds__(kNormW * 64) void add_rmsnorm_fwd_kernel(NormParams
   const size_t T = p.tokens;
   float ss = 0.f;
   if (ok) {
+#pragma unroll 4
     for (int f = wv; f < p.features; f += kNormW) {
       float v = p.h[f * T + t];
       if (delta) {
@@ -56,6 +57,7 @@ __global__ __launch_bounds__(kNormW * 64) void add_rmsnorm_fwd_kernel(NormParams
   if (!ok) return;
   if (wv == 0) p.rstd[t] = r;
   const float* src = delta ? p.hn : p.h;
+#pragma unroll 4
   for (int f = wv; f < p.features; f += kNormW) {
     store_as(xo + f * T + t, src[f * T + t] * r * p.w[f]);
   }
@@ -75,6 +77,7 @@ __global__ __launch_bounds__(kNormW * 64) void add_rmsnorm_bwd_kernel(NormParams
   const float r = ok ? p.rstd[t] : 0.f;
   float c = 0.f;
   if (ok) {
+#pragma unroll 4
     for (int f = wv; f < p.features; f += kNormW) {
       const float xh = hn[f * T + t] * r;
       c = __builtin_fmaf(p.w[f] * to_f32(dx[f * T + t]), xh, c);
@@ -102,13 +105,26 @@ __global__ __launch_bounds__(kNormW * 64) void add_rmsnorm_bwd_kernel(NormParams
   }
 }
 
-__global__ __launch_bounds__(256) void norm_dw_reduce_kernel(const float* __restrict__ part, int n_blk,
-                                                             int features, float* dw) {
-  const int f = blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= features) return;
+// dw[f] = sum over workgroup partials, fixed order: a workgroup owns 64 features (lanes);
+// its 16 waves take every 16th partial and meet in LDS.
+__global__ __launch_bounds__(1024) void norm_dw_reduce_kernel(const float* __restrict__ part, int n_blk,
+                                                              int features, float* dw) {
+  __shared__ float s_sum[16][64];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int f = blockIdx.x * 64 + lane;
   float s = 0.f;
-  for (int i = 0; i < n_blk; ++i) s += part[static_cast<size_t>(i) * features + f];
-  dw[f] = s;
+  if (f < features) {
+    for (int i = wv; i < n_blk; i += 16) s += part[static_cast<size_t>(i) * features + f];
+  }
+  s_sum[wv][lane] = s;
+  __syncthreads();
+  if (wv == 0 && f < features) {
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tot += s_sum[i][lane];
+    dw[f] = tot;
+  }
 }
 
 int norm_blocks(int tokens) { return (tokens + 63) / 64; }
@@ -126,7 +142,7 @@ hipError_t launch_norm_bwd(const NormParams& p, bool io_bf16, float* dw, hipStre
   else hipLaunchKernelGGL(add_rmsnorm_bwd_kernel<float>, dim3(nb), dim3(kNormW * 64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(norm_dw_reduce_kernel, dim3((p.features + 255) / 256), dim3(256), 0, stream,
+  hipLaunchKernelGGL(norm_dw_reduce_kernel, dim3((p.features + 63) / 64), dim3(1024), 0, stream,
                      p.dw_part, nb, p.features, dw);
   return hipGetLastError();
 }
