@@ -184,49 +184,64 @@ C5_MODEL = dict(vocab=50280, d_model=768, n_layers=24, expand=2, d_state=16, dt_
 C5_BATCH, C5_LENGTH = 8, 2048
 
 
-def run_train_c5(torch, steps, warmup):
+def run_train_c5(torch, steps, warmup, graph=True):
     """Config 5: one training step of the Mamba-1 130M-shape LM (random init, uniform random
     tokens): bf16 activations with fp32 master weights and residual stream, forward,
     cross-entropy (fp32 math on bf16 logits, HIP kernel) over all next-token positions,
-    backward (HIP scan, conv, norm and loss backward inside),
-    fused AdamW step. Timed with events on the current stream around exactly `steps` steps."""
+    backward (HIP scan, conv, norm and loss backward inside), fused AdamW step. Timed with
+    events on the current stream around exactly `steps` steps: first eagerly, then (graph)
+    as one captured HIP graph replayed per step; `value` is the graphed rate when taken."""
     from mamba_amd.lm_ops import cross_entropy
-    from mamba_amd.mamba1 import MambaLM
+    from mamba_amd.mamba1 import GraphedTrainStep, MambaLM
 
     torch.manual_seed(0)
     m = C5_MODEL
     model = MambaLM(m["vocab"], m["d_model"], m["n_layers"], m["expand"], m["d_state"], m["dt_rank"],
                     m["d_conv"], device="cuda")
     n_params = sum(p.numel() for p in model.parameters())
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=True)
     gen = torch.Generator(device="cuda").manual_seed(0)
     tokens = torch.randint(0, m["vocab"], (C5_BATCH, C5_LENGTH + 1), device="cuda", generator=gen)
     inp = tokens[:, :-1].contiguous()
-    tgt = tokens[:, 1:].reshape(-1)
+    tgt = tokens[:, 1:].reshape(-1).contiguous()
 
-    def step():
-        logits = model(inp, act_dtype=torch.bfloat16)
-        loss = cross_entropy(logits, tgt)
+    def eager_step():
+        opt.zero_grad(set_to_none=True)
+        loss = cross_entropy(model(inp, act_dtype=torch.bfloat16), tgt)
         loss.backward()
         opt.step()
-        opt.zero_grad(set_to_none=True)
         return loss
 
+    def timed(fn, n):
+        stream = torch.cuda.current_stream()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(n):
+            loss = fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n, loss
+
     for _ in range(warmup):
-        loss = step()
+        loss = eager_step()
     torch.cuda.synchronize()
     log(f"[bench] c5 warmup done ({warmup} steps, loss {loss.item():.4f}, {n_params / 1e6:.1f} M params)")
-    stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    eager_ms, loss = timed(eager_step, steps)
+    log(f"[bench] c5 eager: timed {steps} steps: {eager_ms:.2f} ms/step, loss {loss.item():.4f}")
+    # Drop the last eager autograd graph: its AccumulateGrad nodes are bound to the stream
+    # they ran on, and capture needs them recreated on the capture stream.
+    del loss
     torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(steps):
-        loss = step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    log(f"[bench] c5 timed {steps} steps: {ms:.2f} ms/step, loss {loss.item():.4f}")
+    ms = eager_ms
+    if graph:
+        gs = GraphedTrainStep(model, opt, cross_entropy, inp, tgt, warmup=1)
+        gs.step()
+        graph_ms, loss = timed(gs.step, steps)
+        log(f"[bench] c5 hip graph: timed {steps} steps: {graph_ms:.2f} ms/step, loss {loss.item():.4f}")
+        ms = graph_ms
+        del gs
     del model, opt
     torch.cuda.empty_cache()
     return {
@@ -234,6 +249,8 @@ def run_train_c5(torch, steps, warmup):
         "value": round(C5_BATCH * C5_LENGTH / (ms * 1e-3), 1),
         "unit": "tokens/s",
         "ms_per_step": round(ms, 3),
+        "eager_ms_per_step": round(eager_ms, 3),
+        "hip_graph": bool(graph),
         "steps": steps,
         "warmup": warmup,
         "dtype": "bf16",
@@ -318,6 +335,8 @@ def main():
     ap.add_argument("--train-steps", type=int, default=10,
                     help="timed config-5 training steps (0 skips the training measurement)")
     ap.add_argument("--train-warmup", type=int, default=3)
+    ap.add_argument("--train-eager", action="store_true",
+                    help="time the config-5 step eagerly only (no HIP graph capture)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the timed region, copy a device buffer of this many MiB twice "
                          "(a kernel of known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -366,7 +385,7 @@ def main():
         per_config[name] = scan_report(c, results[name])
     train = None
     if args.train_steps > 0:
-        train = run_train_c5(torch, args.train_steps, args.train_warmup)
+        train = run_train_c5(torch, args.train_steps, args.train_warmup, graph=not args.train_eager)
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, cfg, args.cpu_seconds)

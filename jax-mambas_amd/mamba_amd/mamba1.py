@@ -32,7 +32,86 @@ from .conv1d_hip import causal_conv1d_fn
 from .lm_ops import add_rmsnorm
 from .selective_scan_hip import selective_scan_fn
 
-__all__ = ["S6", "MambaBlock", "MambaLM", "RMSNormCM"]
+__all__ = ["S6", "MambaBlock", "MambaLM", "RMSNormCM", "ShadowWeights", "GraphedTrainStep"]
+
+
+_MM_FP32_OUT = None  # whether torch.mm(bf16, bf16, out_dtype=float32) runs on this device
+
+
+def _mm_fp32(a, b):
+    """a @ b with float32 output (accumulation is float32 either way)."""
+    global _MM_FP32_OUT
+    if _MM_FP32_OUT is None:
+        try:
+            torch.mm(a[:1, :1], b[:1, :1], out_dtype=torch.float32)
+            _MM_FP32_OUT = True
+        except (RuntimeError, NotImplementedError, TypeError):
+            _MM_FP32_OUT = False
+    if _MM_FP32_OUT:
+        return torch.mm(a, b, out_dtype=torch.float32)
+    return torch.mm(a, b).float()
+
+
+class _WeightMM(torch.autograd.Function):
+    """y = W_act @ x with a low-precision shadow W_act of the float32 master weight W:
+    dx = W_act^T dy; dW = dy x^T, produced in float32 for the master weight."""
+
+    @staticmethod
+    def forward(ctx, x, w, w_act):
+        ctx.save_for_backward(x, w_act)
+        return w_act @ x
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w_act = ctx.saved_tensors
+        dx = w_act.t() @ dy if ctx.needs_input_grad[0] else None
+        dw = _mm_fp32(dy, x.t()) if ctx.needs_input_grad[1] else None
+        return dx, dw, None
+
+
+class _TiedHeadMM(torch.autograd.Function):
+    """logits = x^T E_act^T for x (features, tokens) and the tied embedding E (vocab,
+    features); dE in float32 for the master embedding."""
+
+    @staticmethod
+    def forward(ctx, x, e, e_act):
+        ctx.save_for_backward(x, e_act)
+        return x.t() @ e_act.t()
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, e_act = ctx.saved_tensors
+        dx = e_act.t() @ dy.t() if ctx.needs_input_grad[0] else None
+        de = _mm_fp32(dy.t(), x.t()) if ctx.needs_input_grad[1] else None
+        return dx, de, None
+
+
+class ShadowWeights:
+    """Low-precision copies of float32 weights, refreshed together in one multi-tensor
+    copy per step (instead of one cast per weight per use, plus one per gradient)."""
+
+    def __init__(self, params):
+        self.params = list(params)
+        self.bufs = None
+        self.by_id = {}
+
+    def refresh(self, dtype):
+        if self.bufs is None or self.bufs[0].dtype != dtype:
+            self.bufs = [torch.empty_like(p, dtype=dtype) for p in self.params]
+            self.by_id = {id(p): b for p, b in zip(self.params, self.bufs)}
+        with torch.no_grad():
+            torch._foreach_copy_(self.bufs, [p.detach() for p in self.params])
+
+    def mm(self, w, x):
+        """w @ x: plain autograd in float32, else through the shadow of w."""
+        if x.dtype == torch.float32 or not self.by_id:
+            return w.to(x.dtype) @ x
+        return _WeightMM.apply(x, w, self.by_id[id(w)])
+
+    def head(self, x, e):
+        if x.dtype == torch.float32 or not self.by_id:
+            return x.t() @ e.to(x.dtype).t()
+        return _TiedHeadMM.apply(x, e, self.by_id[id(e)])
 
 
 def _uniform_(t, bound):
@@ -93,11 +172,13 @@ class S6(nn.Module):
         dt = torch.clamp(torch.exp(log_dt), min=1e-4)
         self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
 
-    def forward(self, u, batch, z=None, seq_lens=None):
-        """u, z: (d_inner, B*L) matrices; returns (d_inner, B*L): (scan(u) + D u) * silu(z)."""
+    def forward(self, u, batch, z=None, seq_lens=None, weights=None):
+        """u, z: (d_inner, B*L) matrices; returns (d_inner, B*L): (scan(u) + D u) * silu(z).
+        `weights` (ShadowWeights) supplies low-precision copies of the projections."""
         r, n = self.dt_rank, self.d_state
-        x_dbl = self.x_proj.to(u.dtype) @ u                     # (R + 2N, B*L)
-        dt = self.dt_proj.to(u.dtype) @ x_dbl[:r]               # (d_inner, B*L), bias fused below
+        weights = weights or _PLAIN
+        x_dbl = weights.mm(self.x_proj, u)                      # (R + 2N, B*L)
+        dt = weights.mm(self.dt_proj, x_dbl[:r])                # (d_inner, B*L), bias fused below
         A = -torch.exp(self.A_log.float())
         y = selective_scan_fn(
             _rows(u, batch), _rows(dt, batch), A, _rows(x_dbl[r:r + n], batch),
@@ -105,6 +186,9 @@ class S6(nn.Module):
             z=None if z is None else _rows(z, batch), delta_bias=self.dt_bias.float(),
             delta_softplus=True, seq_lens=seq_lens, discretization=self.discretization)
         return _matrix(y)
+
+
+_PLAIN = ShadowWeights([])  # no shadows: weights cast per use
 
 
 class MambaBlock(nn.Module):
@@ -127,17 +211,21 @@ class MambaBlock(nn.Module):
         self.out_proj = nn.Parameter(_uniform_(torch.empty(d_model, d_inner, device=device),
                                                d_inner ** -0.5 * n_layers ** -0.5))
 
-    def forward(self, h, delta, batch, seq_lens=None, act_dtype=torch.bfloat16):
+    def gemm_weights(self):
+        return [self.in_proj, self.z_proj, self.out_proj, self.s6.x_proj, self.s6.dt_proj]
+
+    def forward(self, h, delta, batch, seq_lens=None, act_dtype=torch.bfloat16, weights=None):
         """h: (d_model, B*L) fp32 residual stream before the previous block's output `delta`
         (act_dtype, or None for the first block) is added. Returns (h + delta, this block's
         output): the residual add is fused into the next norm."""
+        weights = weights or _PLAIN
         h, x = self.norm(h, delta, act_dtype)
-        xin = self.in_proj.to(act_dtype) @ x
-        z = self.z_proj.to(act_dtype) @ x
+        xin = weights.mm(self.in_proj, x)
+        z = weights.mm(self.z_proj, x)
         # causal depthwise conv + silu (HIP kernel), masked past each row's length
         u = _matrix(causal_conv1d_fn(_rows(xin, batch), self.conv_weight, self.conv_bias, seq_lens))
-        y = self.s6(u, batch, z=z, seq_lens=seq_lens)
-        return h, self.out_proj.to(act_dtype) @ y
+        y = self.s6(u, batch, z=z, seq_lens=seq_lens, weights=weights)
+        return h, weights.mm(self.out_proj, y)
 
 
 class MambaLM(nn.Module):
@@ -152,13 +240,53 @@ class MambaLM(nn.Module):
                        use_euler_barB_approx=use_euler_barB_approx, device=device)
             for _ in range(n_layers))
         self.final_norm = RMSNormCM(d_model, device=device)
+        self._shadows = ShadowWeights([self.embedding] + [w for b in self.blocks for w in b.gemm_weights()])
 
-    def forward(self, tokens, seq_lens=None, act_dtype=torch.bfloat16):
-        """tokens (B, L) int64 -> logits (B*L, vocab) in act_dtype (rows in (b, t) order)."""
+    def forward(self, tokens, seq_lens=None, act_dtype=torch.bfloat16, shadow_weights=True):
+        """tokens (B, L) int64 -> logits (B*L, vocab) in act_dtype (rows in (b, t) order).
+        Low-precision GEMM weights are refreshed from the float32 masters once per call
+        (shadow_weights=False casts each weight at its use instead)."""
         batch = tokens.shape[0]
+        weights = _PLAIN
+        if act_dtype != torch.float32 and shadow_weights:
+            self._shadows.refresh(act_dtype)
+            weights = self._shadows
         h = self.embedding[tokens.reshape(-1)].t().contiguous()   # (d_model, B*L) fp32
         delta = None
         for blk in self.blocks:
-            h, delta = blk(h, delta, batch, seq_lens, act_dtype)
+            h, delta = blk(h, delta, batch, seq_lens, act_dtype, weights)
         _, hn = self.final_norm(h, delta, act_dtype)
-        return hn.t() @ self.embedding.to(act_dtype).t()
+        return weights.head(hn, self.embedding)
+
+
+class GraphedTrainStep:
+    """One training step (forward, loss, backward, optimizer step) captured once in a HIP
+    graph and replayed: removes the host's per-kernel launch work (~1200 launches per step
+    for the 130M model). The inputs are static tensors the caller refills between replays;
+    `loss` is the static loss of the last replay. The optimizer must be capturable
+    (e.g. AdamW(capturable=True)). Capture follows torch.cuda.graph's whole-network recipe:
+    warm-up steps on a side stream, then one captured step with gradients allocated inside
+    the graph's memory pool. Callers must hold no autograd graph of earlier steps (e.g. a
+    loss tensor): it keeps the parameters' gradient-accumulation nodes bound to the stream
+    they ran on, which breaks the capture."""
+
+    def __init__(self, model, optimizer, loss_fn, tokens, targets, warmup=3, act_dtype=torch.bfloat16):
+        self.tokens, self.targets = tokens, targets
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                optimizer.zero_grad(set_to_none=True)
+                loss_fn(model(tokens, act_dtype=act_dtype), targets).backward()
+                optimizer.step()
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        optimizer.zero_grad(set_to_none=True)
+        with torch.cuda.graph(self.graph):
+            self.loss = loss_fn(model(tokens, act_dtype=act_dtype), targets)
+            self.loss.backward()
+            optimizer.step()
+
+    def step(self):
+        self.graph.replay()
+        return self.loss

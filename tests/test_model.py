@@ -11,7 +11,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from mamba_amd.mamba1 import MambaLM
+from mamba_amd.mamba1 import GraphedTrainStep, MambaLM
 from oracle import mamba1_torch as ref
 from oracle import scan64
 
@@ -121,3 +121,87 @@ def test_model_matches_oracle_on_gpu(euler):
         err = float((got - v.grad).abs().max())
         print(f"  grad {k:28s} max|g|={scale:.3e} max_err={err:.3e}", flush=True)
         assert err <= 1e-3 * scale + 1e-7, k
+
+
+@pytest.mark.gpu
+def test_bf16_shadow_weights_match_per_use_casts():
+    """bf16 training path: weights refreshed once into shadows vs cast at each use. Same
+    bf16 weights and products, so identical logits; weight gradients differ only by the
+    per-use path's final rounding of each gradient to bf16."""
+    print("case model bf16 shadow weights", flush=True)
+    torch.manual_seed(1)
+    cfg = C1
+    model = MambaLM(cfg["vocab"], cfg["d_model"], cfg["n_layers"], cfg["expand"], cfg["d_state"], None,
+                    cfg["d_conv"], device="cuda")
+    g = torch.Generator().manual_seed(2)
+    tokens = torch.randint(0, cfg["vocab"], (cfg["batch"], cfg["length"]), generator=g).cuda()
+    targets = torch.roll(tokens, -1, dims=1).reshape(-1)
+    grads = []
+    logits_all = []
+    for shadow in (True, False):
+        model.zero_grad(set_to_none=True)
+        logits = model(tokens, act_dtype=torch.bfloat16, shadow_weights=shadow)
+        F.cross_entropy(logits.float(), targets).backward()
+        torch.cuda.synchronize()
+        logits_all.append(logits.detach())
+        grads.append({k: p.grad.detach().clone() for k, p in model.named_parameters()})
+    assert torch.equal(logits_all[0], logits_all[1])
+    for k in grads[0]:
+        a, b = grads[0][k].double(), grads[1][k].double()
+        scale = float(b.abs().max()) + 1e-12
+        assert float((a - b).abs().max()) <= 1e-2 * scale, k
+
+
+@pytest.mark.gpu
+def test_graphed_train_step_matches_eager():
+    """The HIP-graph training step against eager steps from the same initial weights: the
+    loss of every replay and the final weights agree (replays are checked one by one, with
+    eager work and synchronisations between them)."""
+    print("case graphed train step", flush=True)
+    from mamba_amd.lm_ops import cross_entropy
+
+    cfg = dict(C1, vocab=256)
+    g = torch.Generator().manual_seed(3)
+    tokens = torch.randint(0, cfg["vocab"], (cfg["batch"], cfg["length"] + 1), generator=g).cuda()
+    inp, tgt = tokens[:, :-1].contiguous(), tokens[:, 1:].reshape(-1).contiguous()
+
+    def make():
+        torch.manual_seed(4)
+        m = MambaLM(cfg["vocab"], cfg["d_model"], cfg["n_layers"], cfg["expand"], cfg["d_state"], None,
+                    cfg["d_conv"], device="cuda")
+        return m, torch.optim.AdamW(m.parameters(), lr=1e-3, fused=True, capturable=True)
+
+    warm, steps = 3, 4
+    m_e, o_e = make()
+    eager_losses = []
+    for i in range(warm + 1 + steps):
+        o_e.zero_grad(set_to_none=True)
+        loss = cross_entropy(m_e(inp), tgt)
+        loss.backward()
+        o_e.step()
+        eager_losses.append(loss.item())
+    m_g, o_g = make()
+    # eager steps on the default stream first (as a benchmark does), dropping their
+    # autograd graphs before the capture
+    for _ in range(2):
+        o_g.zero_grad(set_to_none=True)
+        loss = cross_entropy(m_g(inp), tgt)
+        loss.backward()
+        o_g.step()
+    del loss
+    torch.cuda.synchronize()
+    gs = GraphedTrainStep(m_g, o_g, cross_entropy, inp, tgt, warmup=warm - 2)
+    torch.cuda.synchronize()
+    # capture does not execute: replay i is step warm + i of the eager run
+    graph_losses = []
+    for i in range(1 + steps):
+        graph_losses.append(gs.step().item())
+        torch.cuda.synchronize()
+        _ = (m_g.embedding.sum() * 0).item()  # eager work between replays
+    print("  eager", [round(x, 5) for x in eager_losses[warm:]], flush=True)
+    print("  graph", [round(x, 5) for x in graph_losses], flush=True)
+    for a, b in zip(eager_losses[warm:], graph_losses):
+        assert abs(a - b) <= 2e-3 * abs(a), (a, b)
+    for (k, pe), pg in zip(m_e.named_parameters(), m_g.parameters()):
+        scale = float(pe.detach().abs().max()) + 1e-12
+        assert float((pe.detach() - pg.detach()).abs().max()) <= 2e-2 * scale, k
