@@ -180,6 +180,50 @@ size_t mss_conv_bwd_workspace_bytes(const mss_conv_args* args);
 int mss_conv_fwd(const mss_conv_args* args, void* stream);
 int mss_conv_bwd(const mss_conv_args* args, void* stream);
 
+/* --- Single-token recurrent step (decode). ----------------------------------------
+ * Replaces S6.step / Mamba.step (mamba/mamba1.py:200-214, 339-363; no FFI symbol in the
+ * reference). For each (b, d), with the scan's fused extras:
+ *   delta = softplus(delta_raw + bias) (if delta_softplus),  a_bar = exp(delta A[d][n]),
+ *   state[b][d][n] = a_bar*state + b_bar*u  (Euler b_bar = delta*B, ZOH expm1(delta A)/A*B),
+ *   y = sum_n C state + D u,  out = y * silu(z) (if z)
+ * state is [batch][dim][dstate] float32, updated in place (the scan's last_state layout).
+ * u/delta/z/out are [batch][dim] and B/C [batch][dstate] with the row strides of
+ * `strides` (0 = contiguous; e.g. io_batch=1, io_dim=batch for a (dim, batch) matrix). */
+typedef struct mss_step_args {
+  int32_t batch, dim, dstate;
+  int32_t discretization, delta_softplus;
+  int32_t io_dtype, bc_dtype;
+  float* state;
+  const void* u;
+  const void* delta;
+  const float* A;
+  const void* B;
+  const void* C;
+  const float* D;          /* optional */
+  const void* z;           /* optional */
+  const float* delta_bias; /* optional */
+  void* out;
+  mss_strides strides;
+} mss_step_args;
+
+int mss_scan_step(const mss_step_args* args, void* stream);
+
+/* Causal-conv window update for one token: window = [conv_state[b][d][0..width-2], x];
+ * y = act(bias + sum_k weight[d][k] window[k]); conv_state shifts left and takes x.
+ * conv_state is [batch][dim][width-1] in the activation dtype, updated in place; x/y use
+ * the io strides of `strides`. */
+typedef struct mss_conv_step_args {
+  int32_t batch, dim, width, io_dtype, activation;
+  void* conv_state;
+  const void* x;
+  const float* weight; /* [dim][width] */
+  const float* bias;   /* optional */
+  void* y;
+  mss_strides strides;
+} mss_conv_step_args;
+
+int mss_conv_step(const mss_conv_step_args* args, void* stream);
+
 /* --- Residual add + RMSNorm over the features of a channel-major stream. ----------
  * No counterpart symbol in the reference (mamba/mamba1.py:300-337 applies
  * nnx.RMSNorm(epsilon) to the residual stream and adds each block's output back).

@@ -32,6 +32,8 @@ hipError_t launch_norm_fwd(const NormParams& p, bool io_bf16, hipStream_t stream
 hipError_t launch_norm_bwd(const NormParams& p, bool io_bf16, float* dw, hipStream_t stream);
 int norm_blocks(int tokens);
 hipError_t launch_xent(const XentParams& p, bool bwd, bool vec, hipStream_t stream);
+hipError_t launch_ssm_step(const StepParams& p, bool zoh, bool io_bf16, bool bc_bf16, hipStream_t stream);
+hipError_t launch_conv_step(const ConvStepParams& p, bool io_bf16, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -507,6 +509,66 @@ int mss_xent_fwd(const mss_xent_args* args, void* stream) {
 int mss_xent_bwd(const mss_xent_args* args, void* stream) {
   const int s = validate_xent(args, true);
   return s != MSS_OK ? s : run_xent(args, true, static_cast<hipStream_t>(stream));
+}
+
+int mss_scan_step(const mss_step_args* a, void* stream) {
+  if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
+  int s = check_dims(a->batch, a->dim, 1, a->dstate);
+  if (s != MSS_OK) return s;
+  s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
+  if (s != MSS_OK) return s;
+  if (!a->state || !a->u || !a->delta || !a->A || !a->B || !a->C || !a->out) return MSS_ERR_INVALID_ARGUMENT;
+  Strides st;
+  // Rows of one step: the per-row "length" is 1.
+  s = resolve_strides(a->strides, a->batch, a->dim, 1, a->dstate, &st);
+  if (s != MSS_OK) return s;
+  mss::StepParams p{};
+  p.batch = a->batch;
+  p.dim = a->dim;
+  p.dstate = a->dstate;
+  p.delta_softplus = a->delta_softplus;
+  p.io_sb = st.io_sb;
+  p.io_sd = st.io_sd;
+  p.bc_sb = st.bc_sb;
+  p.bc_sn = st.bc_sn;
+  p.state = a->state;
+  p.u = a->u;
+  p.delta = a->delta;
+  p.z = a->z;
+  p.B = a->B;
+  p.C = a->C;
+  p.A = a->A;
+  p.D = a->D;
+  p.delta_bias = a->delta_bias;
+  p.out = a->out;
+  const hipError_t e = mss::launch_ssm_step(p, a->discretization == MSS_ZOH, a->io_dtype == MSS_BF16,
+                                            a->bc_dtype == MSS_BF16, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching scan step");
+}
+
+int mss_conv_step(const mss_conv_step_args* a, void* stream) {
+  if (a == nullptr || a->batch <= 0 || a->dim <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->width < 1 || a->width > 4) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->io_dtype != MSS_F32 && a->io_dtype != MSS_BF16) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->activation != 0 && a->activation != 1) return MSS_ERR_INVALID_ARGUMENT;
+  if (!a->x || !a->weight || !a->y || (a->width > 1 && !a->conv_state)) return MSS_ERR_INVALID_ARGUMENT;
+  Strides st;
+  const int s = resolve_strides(a->strides, a->batch, a->dim, 1, 1, &st);
+  if (s != MSS_OK) return s;
+  mss::ConvStepParams p{};
+  p.batch = a->batch;
+  p.dim = a->dim;
+  p.width = a->width;
+  p.act = a->activation;
+  p.sb = st.io_sb;
+  p.sd = st.io_sd;
+  p.state = a->conv_state;
+  p.x = a->x;
+  p.w = a->weight;
+  p.bias = a->bias;
+  p.y = a->y;
+  const hipError_t e = mss::launch_conv_step(p, a->io_dtype == MSS_BF16, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching conv step");
 }
 
 int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,

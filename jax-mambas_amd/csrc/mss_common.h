@@ -266,6 +266,31 @@ struct XentParams {
   bf16_t* dz;
 };
 
+struct StepParams {
+  int batch, dim, dstate, delta_softplus;
+  long long io_sb, io_sd, bc_sb, bc_sn;
+  float* state;  // [B][D][N], updated in place
+  const void* u;
+  const void* delta;
+  const void* z;  // optional
+  const void* B;
+  const void* C;
+  const float* A;
+  const float* D;           // optional
+  const float* delta_bias;  // optional
+  void* out;
+};
+
+struct ConvStepParams {
+  int batch, dim, width, act;
+  long long sb, sd;  // strides of x and y
+  void* state;       // [B][D][width-1], activation dtype, updated in place
+  const void* x;
+  const float* w;
+  const float* bias;  // optional
+  void* y;
+};
+
 struct ConvParams {
   int batch, dim, seqlen, width;
   long long sb, sd;  // row strides (elements) of x, y, dy, dx: batch, channel

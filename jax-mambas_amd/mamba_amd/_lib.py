@@ -45,6 +45,8 @@ EXPORTED_SYMBOLS = (
     "mss_norm_bwd",
     "mss_xent_fwd",
     "mss_xent_bwd",
+    "mss_scan_step",
+    "mss_conv_step",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -111,6 +113,22 @@ class XentArgs(ctypes.Structure):
     ]
 
 
+class StepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i32), ("dim", _i32), ("dstate", _i32), ("discretization", _i32), ("delta_softplus", _i32),
+        ("io_dtype", _i32), ("bc_dtype", _i32),
+        ("state", _p), ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p), ("D", _p), ("z", _p),
+        ("delta_bias", _p), ("out", _p), ("strides", Strides),
+    ]
+
+
+class ConvStepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i32), ("dim", _i32), ("width", _i32), ("io_dtype", _i32), ("activation", _i32),
+        ("conv_state", _p), ("x", _p), ("weight", _p), ("bias", _p), ("y", _p), ("strides", Strides),
+    ]
+
+
 _LIBRARY = None
 _LIBRARY_PATH = None
 
@@ -163,6 +181,10 @@ def register_hip_kernel(library_path=None):
     for name in ("mss_xent_fwd", "mss_xent_bwd"):
         getattr(lib, name).argtypes = [ctypes.POINTER(XentArgs), _p]
         getattr(lib, name).restype = ctypes.c_int
+    lib.mss_scan_step.argtypes = [ctypes.POINTER(StepArgs), _p]
+    lib.mss_scan_step.restype = ctypes.c_int
+    lib.mss_conv_step.argtypes = [ctypes.POINTER(ConvStepArgs), _p]
+    lib.mss_conv_step.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

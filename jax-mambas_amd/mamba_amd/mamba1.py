@@ -29,6 +29,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .conv1d_hip import causal_conv1d_fn
+from .decode import causal_conv1d_update, selective_state_update
 from .lm_ops import add_rmsnorm
 from .selective_scan_hip import selective_scan_fn
 
@@ -180,12 +181,26 @@ class S6(nn.Module):
         x_dbl = weights.mm(self.x_proj, u)                      # (R + 2N, B*L)
         dt = weights.mm(self.dt_proj, x_dbl[:r])                # (d_inner, B*L), bias fused below
         A = -torch.exp(self.A_log.float())
-        y = selective_scan_fn(
+        y, last = selective_scan_fn(
             _rows(u, batch), _rows(dt, batch), A, _rows(x_dbl[r:r + n], batch),
             _rows(x_dbl[r + n:], batch), D=None if self.D is None else self.D.float(),
             z=None if z is None else _rows(z, batch), delta_bias=self.dt_bias.float(),
-            delta_softplus=True, seq_lens=seq_lens, discretization=self.discretization)
+            delta_softplus=True, return_last_state=True, seq_lens=seq_lens,
+            discretization=self.discretization)
+        self.last_state = last if not torch.is_grad_enabled() else None
         return _matrix(y)
+
+    def step(self, u, z, state, weights=None):
+        """One token: u, z (d_inner, B) matrices; state (B, d_inner, N) updated in place."""
+        r, n = self.dt_rank, self.d_state
+        weights = weights or _PLAIN
+        x_dbl = weights.mm(self.x_proj, u)
+        dt = weights.mm(self.dt_proj, x_dbl[:r])
+        y = selective_state_update(
+            state, u.t(), dt.t(), -torch.exp(self.A_log.float()), x_dbl[r:r + n].t(), x_dbl[r + n:].t(),
+            D=None if self.D is None else self.D.float(), z=None if z is None else z.t(),
+            delta_bias=self.dt_bias.float(), delta_softplus=True, discretization=self.discretization)
+        return y.t()
 
 
 _PLAIN = ShadowWeights([])  # no shadows: weights cast per use
@@ -225,6 +240,24 @@ class MambaBlock(nn.Module):
         # causal depthwise conv + silu (HIP kernel), masked past each row's length
         u = _matrix(causal_conv1d_fn(_rows(xin, batch), self.conv_weight, self.conv_bias, seq_lens))
         y = self.s6(u, batch, z=z, seq_lens=seq_lens, weights=weights)
+        if not torch.is_grad_enabled():  # inference: keep the decode caches of this prompt
+            k = self.conv_weight.shape[1]
+            tail = _rows(xin, batch)[:, :, max(0, xin.shape[1] // batch - (k - 1)):]
+            conv = torch.zeros(batch, xin.shape[0], k - 1, dtype=xin.dtype, device=xin.device)
+            if k > 1:
+                conv[:, :, conv.shape[2] - tail.shape[2]:] = tail
+            self.cache = {"conv": conv, "ssm": self.s6.last_state}
+        return h, weights.mm(self.out_proj, y)
+
+    def step(self, h, delta, cache, act_dtype=torch.bfloat16, weights=None):
+        """One token per row: h (d_model, B) stream; cache {"conv": (B, d_inner, K-1),
+        "ssm": (B, d_inner, N)} updated in place (Mamba.step, mamba/mamba1.py:339-363)."""
+        weights = weights or _PLAIN
+        h, x = self.norm(h, delta, act_dtype)
+        xin = weights.mm(self.in_proj, x)
+        z = weights.mm(self.z_proj, x)
+        u = causal_conv1d_update(cache["conv"], xin.t(), self.conv_weight, self.conv_bias).t()
+        y = self.s6.step(u, z, cache["ssm"], weights)
         return h, weights.mm(self.out_proj, y)
 
 
@@ -255,6 +288,33 @@ class MambaLM(nn.Module):
         delta = None
         for blk in self.blocks:
             h, delta = blk(h, delta, batch, seq_lens, act_dtype, weights)
+        _, hn = self.final_norm(h, delta, act_dtype)
+        return weights.head(hn, self.embedding)
+
+    @torch.no_grad()
+    def prefill(self, tokens, act_dtype=torch.bfloat16):
+        """Runs a prompt (B, L) without gradients; returns (logits of its last position
+        (B, vocab), per-block decode caches). Right-aligned prompts only (no seq_lens)."""
+        logits = self.forward(tokens, act_dtype=act_dtype)
+        caches = []
+        for blk in self.blocks:
+            caches.append(blk.cache)
+            blk.cache = None
+            blk.s6.last_state = None
+        b, l = tokens.shape
+        return logits.view(b, l, -1)[:, -1], caches
+
+    @torch.no_grad()
+    def step(self, token, caches, act_dtype=torch.bfloat16):
+        """One decode step: token (B,) int64 -> logits (B, vocab); caches update in place."""
+        weights = _PLAIN
+        if act_dtype != torch.float32:
+            self._shadows.refresh(act_dtype)
+            weights = self._shadows
+        h = self.embedding[token].t().contiguous()  # (d_model, B)
+        delta = None
+        for blk, cache in zip(self.blocks, caches):
+            h, delta = blk.step(h, delta, cache, act_dtype, weights)
         _, hn = self.final_norm(h, delta, act_dtype)
         return weights.head(hn, self.embedding)
 

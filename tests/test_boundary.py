@@ -106,7 +106,8 @@ def test_grid_limit_is_unsupported(lib):
 def test_struct_layout_matches_header(tmp_path):
     """The ctypes mirrors have the C structs' size and field offsets (compiled with gcc)."""
     structs = {"mss_fwd_args": _lib.FwdArgs, "mss_bwd_args": _lib.BwdArgs, "mss_strides": _lib.Strides,
-               "mss_conv_args": _lib.ConvArgs}
+               "mss_conv_args": _lib.ConvArgs, "mss_norm_args": _lib.NormArgs, "mss_xent_args": _lib.XentArgs,
+               "mss_step_args": _lib.StepArgs, "mss_conv_step_args": _lib.ConvStepArgs}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "mamba_selective_scan.h"',
              "int main(void) {"]
     for cname, cls in structs.items():

@@ -1,0 +1,110 @@
+"""Single-token recurrent step (decode): S6.step / Mamba.step (mamba/mamba1.py:200-214,
+339-363) as HIP kernels, and the model's prefill + step against its own full forward.
+
+CPU: argument validation. GPU: T sequential steps of selective_state_update against the
+float64 oracle scan over the same T steps from the same initial state (fp32 within rtol
+1e-4 / atol 1e-5), causal_conv1d_update against the oracle conv of [prefix, x], and
+MambaLM.prefill + step logits against MambaLM.forward logits on the whole sequence.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mamba_amd import _lib
+from mamba_amd.decode import causal_conv1d_update, selective_state_update
+from mamba_amd.mamba1 import MambaLM
+from oracle import mamba1_torch as ref
+from oracle import scan64
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.register_hip_kernel()
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(dstate=17), _lib.MSS_ERR_UNSUPPORTED), (dict(dstate=0), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(state=None), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(out=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(discretization=3), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(batch=0), _lib.MSS_ERR_INVALID_ARGUMENT),
+])
+def test_step_validation(lib, kw, status):
+    base = dict(batch=2, dim=3, dstate=4, state=1, u=1, delta=1, A=1, B=1, C=1, out=1)
+    base.update(kw)
+    assert lib.mss_scan_step(_lib.StepArgs(**base), None) == status
+
+
+@pytest.mark.parametrize("kw", [dict(width=0), dict(width=5), dict(conv_state=None), dict(x=None),
+                                dict(activation=2)])
+def test_conv_step_validation(lib, kw):
+    base = dict(batch=2, dim=3, width=4, activation=1, conv_state=1, x=1, weight=1, y=1)
+    base.update(kw)
+    assert lib.mss_conv_step(_lib.ConvStepArgs(**base), None) == _lib.MSS_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("zoh", [False, True])
+@pytest.mark.parametrize("layout", ["bd", "db"])
+def test_state_update_steps_match_oracle_scan(zoh, layout):
+    print(f"case state update zoh={zoh} layout={layout}", flush=True)
+    rng = np.random.default_rng(11)
+    b, d, n, steps = 3, 40, 16, 6
+    f = np.float32
+    u = rng.standard_normal((b, d, steps)).astype(f)
+    dr = rng.standard_normal((b, d, steps)).astype(f)
+    z = rng.standard_normal((b, d, steps)).astype(f)
+    Bm = rng.standard_normal((b, n, steps)).astype(f)
+    Cm = rng.standard_normal((b, n, steps)).astype(f)
+    A = (-np.exp(rng.standard_normal((d, n)))).astype(f)
+    D = rng.standard_normal(d).astype(f)
+    bias = (0.5 * rng.standard_normal(d) - 2.0).astype(f)
+    x0 = rng.standard_normal((b, d, n)).astype(f)
+    fw = scan64.forward(u, dr, A, Bm, Cm, D=D, z=z, delta_bias=bias, delta_softplus=True, initial_state=x0,
+                        discretization="zoh" if zoh else "euler")
+    state = torch.from_numpy(x0).cuda()
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    for t in range(steps):
+        if layout == "db":  # (dim, batch) activation matrices, as the LM's decode uses them
+            ut, dt, zt = (cu(a[:, :, t].T).t() for a in (u, dr, z))
+            Bt, Ct = cu(Bm[:, :, t].T).t(), cu(Cm[:, :, t].T).t()
+        else:
+            ut, dt, zt = (cu(a[:, :, t]) for a in (u, dr, z))
+            Bt, Ct = cu(Bm[:, :, t]), cu(Cm[:, :, t])
+        out = selective_state_update(state, ut, dt, cu(A), Bt, Ct, D=cu(D), z=zt, delta_bias=cu(bias),
+                                     discretization="zoh" if zoh else "euler")
+        torch.testing.assert_close(out.double().cpu(), torch.from_numpy(fw["out"][:, :, t]), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(state.double().cpu(), torch.from_numpy(fw["last_state"]), rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [2, 4])
+def test_conv_update_matches_full_conv(k):
+    print(f"case conv update k={k}", flush=True)
+    g = torch.Generator().manual_seed(k)
+    b, d, prefix, steps = 2, 24, 9, 5
+    x = torch.randn(b, prefix + steps, d, generator=g, dtype=torch.float64)
+    w = torch.randn(d, k, generator=g, dtype=torch.float64)
+    bias = torch.randn(d, generator=g, dtype=torch.float64)
+    want = F.silu(ref.causal_depthwise_conv(x, w, bias))
+    state = x[:, prefix - (k - 1):prefix, :].permute(0, 2, 1).contiguous().float().cuda()
+    for t in range(steps):
+        y = causal_conv1d_update(state, x[:, prefix + t, :].float().cuda(), w.float().cuda(), bias.float().cuda())
+        torch.testing.assert_close(y.double().cpu(), want[:, prefix + t, :], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("euler", [True, False])
+def test_prefill_and_steps_match_full_forward(euler):
+    print(f"case prefill + steps euler={euler}", flush=True)
+    torch.manual_seed(5)
+    model = MambaLM(16, 64, 2, 2, 16, None, 4, use_euler_barB_approx=euler, device="cuda")
+    g = torch.Generator().manual_seed(6)
+    b, prompt, steps = 3, 37, 6
+    tokens = torch.randint(0, 16, (b, prompt + steps), generator=g).cuda()
+    with torch.no_grad():
+        full = model(tokens, act_dtype=torch.float32).view(b, prompt + steps, -1)
+    last, caches = model.prefill(tokens[:, :prompt], act_dtype=torch.float32)
+    torch.testing.assert_close(last, full[:, prompt - 1], rtol=1e-4, atol=1e-4)
+    for t in range(steps):
+        logits = model.step(tokens[:, prompt + t], caches, act_dtype=torch.float32)
+        torch.testing.assert_close(logits, full[:, prompt + t], rtol=1e-4, atol=1e-4)
