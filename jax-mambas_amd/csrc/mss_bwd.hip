@@ -177,15 +177,13 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         n = n >= N ? n - N : n;
         __syncthreads();
         if (!active) continue;
-        // This wave owns accumulator row n until the next barrier: fetch it now so the LDS
-        // latency overlaps the state's arithmetic; it is written back at the end.
+        // This wave owns accumulator row n until the next barrier. Its dC half is fetched
+        // now and updated by the forward re-run (where h_t is produced), its dB half is
+        // fetched after that and updated by the reverse pass: half a row of registers live.
         float* accn = acc_w + n * 2 * kChunk + lane;
-        float accv[2 * kT];
+        float accC[kT];
 #pragma unroll
-        for (int j = 0; j < kT; ++j) {
-          accv[2 * j] = accn[j * 128];
-          accv[2 * j + 1] = accn[j * 128 + 64];
-        }
+        for (int j = 0; j < kT; ++j) accC[j] = accn[j * 128 + 64];
         const float An = s_a[w][n];
         const float a2 = An * kLog2e;
         float a[kT];
@@ -211,8 +209,14 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
             const float bu = kZOH ? (expm1f(dlt[j] * An) * fast_rcp(An)) * bv[j] * uu[j] : dlu[j] * bv[j];
             h = __builtin_fmaf(a[j], h, bu);
             hh[j] = h;
+            accC[j] = __builtin_fmaf(g[j], h, accC[j]);
           }
         }
+#pragma unroll
+        for (int j = 0; j < kT; ++j) accn[j * 128 + 64] = accC[j];
+        float accB[kT];
+#pragma unroll
+        for (int j = 0; j < kT; ++j) accB[j] = accn[j * 128];
         // ---- reverse: local aggregate of lambda, reverse scan, re-run with true lambda
         float lam = cv[kT - 1] * g[kT - 1];
 #pragma unroll
@@ -245,14 +249,10 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
             dA_acc = __builtin_fmaf(dlt[j], q, dA_acc);
             dBv = lam * dlu[j];
           }
-          accv[2 * j] += dBv;
-          accv[2 * j + 1] = __builtin_fmaf(g[j], hh[j], accv[2 * j + 1]);
+          accB[j] += dBv;
         }
 #pragma unroll
-        for (int j = 0; j < kT; ++j) {
-          accn[j * 128] = accv[2 * j];
-          accn[j * 128 + 64] = accv[2 * j + 1];
-        }
+        for (int j = 0; j < kT; ++j) accn[j * 128] = accB[j];
         {  // next state's rows (after the last state: an unused in-bounds reload)
           const int nn = n + 1 == N ? 0 : n + 1;
           load_seg<kT>(Bb + nn * p.bc_sn, tl, L, fast_bc, bv);
@@ -267,6 +267,12 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       }
 
       if (!active) continue;
+      if constexpr (!kZOH) {
+        // Euler needs u only from here on: reload it rather than hold it across the loop.
+        load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
+#pragma unroll
+        for (int j = 0; j < kT; ++j) uu[j] = (kFull || tl + j < len) ? uu[j] : 0.f;
+      }
       // ---- per-step gradients of the row
       float dD_acc = 0.f, db_acc = 0.f;
       float duv[kT], ddv[kT];
