@@ -19,6 +19,7 @@ Fields beyond the driver contract:
                 tokens/s, algorithmic MB and HBM fractions, and a CPU baseline of its own
   train_c5      the metric's second half: tokens/s of one training step of the Mamba-1
                 130M-shape LM (config 5) through the HIP scan
+  decode_c5     single-token decode of the same model after a 2048-token prefill
 Inputs are drawn on the GPU from each config's recipe (seeded torch generator).
 """
 from __future__ import annotations
@@ -261,6 +262,58 @@ def run_train_c5(torch, steps, warmup, graph=True):
     }
 
 
+def run_decode_c5(torch, steps, prompt_len=2048, graph=True):
+    """Decode with the config-5 model (B=8, bf16): prefill a `prompt_len` prompt, then time
+    `steps` single-token steps (HIP state/conv-window updates in place), eagerly and as one
+    captured HIP graph per step (the caches and the token are static buffers)."""
+    from mamba_amd.mamba1 import MambaLM
+
+    torch.manual_seed(0)
+    m = C5_MODEL
+    model = MambaLM(m["vocab"], m["d_model"], m["n_layers"], m["expand"], m["d_state"], m["dt_rank"],
+                    m["d_conv"], device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    prompt = torch.randint(0, m["vocab"], (C5_BATCH, prompt_len), device="cuda", generator=gen)
+    _, caches = model.prefill(prompt)
+    token = torch.randint(0, m["vocab"], (C5_BATCH,), device="cuda", generator=gen)
+
+    def timed(fn, n):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(n):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n
+
+    eager = lambda: model.step(token, caches)
+    for _ in range(3):
+        eager()
+    eager_ms = timed(eager, steps)
+    ms = eager_ms
+    if graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            model.step(token, caches)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            model.step(token, caches)
+        g.replay()
+        ms = timed(g.replay, steps)
+        del g
+    log(f"[bench] c5 decode: {eager_ms:.3f} ms/token eager, {ms:.3f} ms/token {'graph' if graph else 'eager'}")
+    del model, caches
+    torch.cuda.empty_cache()
+    return {"metric": "Mamba-1 130M decode tokens/s", "value": round(C5_BATCH / (ms * 1e-3), 1),
+            "unit": "tokens/s", "ms_per_token_step": round(ms, 4), "eager_ms_per_token_step": round(eager_ms, 4),
+            "hip_graph": bool(graph), "batch": C5_BATCH, "prompt_len": prompt_len, "steps": steps,
+            "dtype": "bf16"}
+
+
 def cpu_baseline(torch, cfg, target_s, lens=None, d0=32):
     """Reference composition on the CPU: softplus(delta + bias) (x validity mask for
     variable lengths, mamba/mamba1.py:165-168) -> pure-JAX-style scan (oracle/assoc_torch.py,
@@ -335,6 +388,8 @@ def main():
     ap.add_argument("--train-steps", type=int, default=10,
                     help="timed config-5 training steps (0 skips the training measurement)")
     ap.add_argument("--train-warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=50,
+                    help="timed single-token decode steps of the config-5 model (0 skips them)")
     ap.add_argument("--train-eager", action="store_true",
                     help="time the config-5 step eagerly only (no HIP graph capture)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -386,6 +441,9 @@ def main():
     train = None
     if args.train_steps > 0:
         train = run_train_c5(torch, args.train_steps, args.train_warmup, graph=not args.train_eager)
+    decode = None
+    if args.decode_steps > 0:
+        decode = run_decode_c5(torch, args.decode_steps, graph=not args.train_eager)
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, cfg, args.cpu_seconds)
@@ -416,6 +474,7 @@ def main():
         "kernels_ms": {"fwd": round(fwd_ms, 5), "bwd_scan": round(bwd_ms, 5), "bwd_reduce": round(red_ms, 5)},
         "configs": per_config,
         "train_c5": train,
+        "decode_c5": decode,
     }
     print(json.dumps(result), flush=True)
 

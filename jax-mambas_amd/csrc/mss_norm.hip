@@ -127,9 +127,44 @@ __global__ __launch_bounds__(1024) void norm_dw_reduce_kernel(const float* __res
   }
 }
 
+// Few tokens (decode): one workgroup per token, threads over the features, so the work
+// spreads over `tokens` workgroups instead of one. Same arithmetic as the wide kernel.
+template <typename io_t>
+__global__ __launch_bounds__(256) void add_rmsnorm_fwd_rows_kernel(NormParams p) {
+  __shared__ float s_part[4];
+  const io_t* __restrict__ delta = static_cast<const io_t*>(p.delta);
+  io_t* __restrict__ xo = static_cast<io_t*>(p.x);
+  const int t = blockIdx.x;
+  const size_t T = p.tokens;
+  float ss = 0.f;
+  for (int f = threadIdx.x; f < p.features; f += 256) {
+    float v = p.h[f * T + t];
+    if (delta) {
+      v += to_f32(delta[f * T + t]);
+      p.hn[f * T + t] = v;
+    }
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+  const float r = 1.f / __builtin_sqrtf(tot / p.features + p.eps);
+  if (threadIdx.x == 0) p.rstd[t] = r;
+  const float* src = delta ? p.hn : p.h;
+  for (int f = threadIdx.x; f < p.features; f += 256) store_as(xo + f * T + t, src[f * T + t] * r * p.w[f]);
+}
+
+constexpr int kNormRowsMaxTokens = 256;
+
 int norm_blocks(int tokens) { return (tokens + 63) / 64; }
 
 hipError_t launch_norm_fwd(const NormParams& p, bool io_bf16, hipStream_t stream) {
+  if (p.tokens <= kNormRowsMaxTokens) {
+    if (io_bf16) hipLaunchKernelGGL(add_rmsnorm_fwd_rows_kernel<bf16_t>, dim3(p.tokens), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(add_rmsnorm_fwd_rows_kernel<float>, dim3(p.tokens), dim3(256), 0, stream, p);
+    return hipGetLastError();
+  }
   const dim3 grid(norm_blocks(p.tokens)), block(kNormW * 64);
   if (io_bf16) hipLaunchKernelGGL(add_rmsnorm_fwd_kernel<bf16_t>, grid, block, 0, stream, p);
   else hipLaunchKernelGGL(add_rmsnorm_fwd_kernel<float>, grid, block, 0, stream, p);

@@ -190,14 +190,16 @@ class S6(nn.Module):
         self.last_state = last if not torch.is_grad_enabled() else None
         return _matrix(y)
 
-    def step(self, u, z, state, weights=None):
-        """One token: u, z (d_inner, B) matrices; state (B, d_inner, N) updated in place."""
+    def step(self, u, z, state, weights=None, A=None):
+        """One token: u, z (d_inner, B) matrices; state (B, d_inner, N) updated in place.
+        A: -exp(A_log) computed once per generation (recomputed when None)."""
         r, n = self.dt_rank, self.d_state
         weights = weights or _PLAIN
         x_dbl = weights.mm(self.x_proj, u)
         dt = weights.mm(self.dt_proj, x_dbl[:r])
+        A = -torch.exp(self.A_log.float()) if A is None else A
         y = selective_state_update(
-            state, u.t(), dt.t(), -torch.exp(self.A_log.float()), x_dbl[r:r + n].t(), x_dbl[r + n:].t(),
+            state, u.t(), dt.t(), A, x_dbl[r:r + n].t(), x_dbl[r + n:].t(),
             D=None if self.D is None else self.D.float(), z=None if z is None else z.t(),
             delta_bias=self.dt_bias.float(), delta_softplus=True, discretization=self.discretization)
         return y.t()
@@ -246,7 +248,7 @@ class MambaBlock(nn.Module):
             conv = torch.zeros(batch, xin.shape[0], k - 1, dtype=xin.dtype, device=xin.device)
             if k > 1:
                 conv[:, :, conv.shape[2] - tail.shape[2]:] = tail
-            self.cache = {"conv": conv, "ssm": self.s6.last_state}
+            self.cache = {"conv": conv, "ssm": self.s6.last_state, "A": -torch.exp(self.s6.A_log.float())}
         return h, weights.mm(self.out_proj, y)
 
     def step(self, h, delta, cache, act_dtype=torch.bfloat16, weights=None):
@@ -257,7 +259,7 @@ class MambaBlock(nn.Module):
         xin = weights.mm(self.in_proj, x)
         z = weights.mm(self.z_proj, x)
         u = causal_conv1d_update(cache["conv"], xin.t(), self.conv_weight, self.conv_bias).t()
-        y = self.s6.step(u, z, cache["ssm"], weights)
+        y = self.s6.step(u, z, cache["ssm"], weights, cache.get("A"))
         return h, weights.mm(self.out_proj, y)
 
 
@@ -306,10 +308,13 @@ class MambaLM(nn.Module):
 
     @torch.no_grad()
     def step(self, token, caches, act_dtype=torch.bfloat16):
-        """One decode step: token (B,) int64 -> logits (B, vocab); caches update in place."""
+        """One decode step: token (B,) int64 -> logits (B, vocab); caches update in place.
+        Uses the low-precision weights of the last prefill (weights do not change while
+        generating)."""
         weights = _PLAIN
         if act_dtype != torch.float32:
-            self._shadows.refresh(act_dtype)
+            if not self._shadows.by_id or self._shadows.bufs[0].dtype != act_dtype:
+                self._shadows.refresh(act_dtype)
             weights = self._shadows
         h = self.embedding[token].t().contiguous()  # (d_model, B)
         delta = None
