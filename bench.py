@@ -91,10 +91,10 @@ def gpu_step_setup(torch, cfg):
     dev = "cuda"
     b, d, l, n = cfg.batch, cfg.dim, cfg.length, cfg.dstate
     io = _lib.MSS_BF16 if cfg.dtype == "bf16" else _lib.MSS_F32
-    n_carry = (l + _lib.MSS_CARRY_CHUNK - 1) // _lib.MSS_CARRY_CHUNK
+    n_seg = (l + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
     t["out"] = torch.empty_like(t["u"])
     t["last"] = torch.empty(b, d, n, device=dev)
-    t["carries"] = torch.empty(b, d, n_carry, n, device=dev)
+    t["carries"] = torch.empty(b, d, n, n_seg, device=dev)
     t["y_pre"] = torch.empty_like(t["u"])
     t["dlast"] = torch.zeros(b, d, n, device=dev)
     for k in ("u", "delta", "z", "A", "B", "C", "D", "delta_bias"):

@@ -17,8 +17,9 @@
  *   D, dD, delta_bias, ddelta_bias        : [dim]                    (float32)
  *   initial_state, last_state, dlast_state, dinitial_state : [batch][dim][dstate] (float32)
  *   seq_lens                              : [batch] int32 (optional variable lengths)
- *   carries                               : [batch][dim][ceil(seqlen/512)][dstate] float32
- *                                           state h at the end of every 512-step chunk
+ *   carries                               : [batch][dim][dstate][ceil(seqlen/8)] float32
+ *                                           state h entering every 8-step segment
+ *                                           (segment 0: initial_state)
  *   y_pre                                 : [batch][dim][seqlen] y before the z gate
  *
  * All entry points are asynchronous on the given stream (a hipStream_t passed as
@@ -44,9 +45,9 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 2
+#define MSS_ABI_VERSION 3
 #define MSS_MAX_DSTATE 16
-#define MSS_CARRY_CHUNK 512 /* step granularity of the `carries` residual */
+#define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
 
 typedef enum mss_status {

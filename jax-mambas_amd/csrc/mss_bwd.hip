@@ -2,56 +2,156 @@
 //
 // Reference behaviour followed (not its structure):
 // native/upstream_mamba/selective_scan_bwd_kernel.cuh:136-299 (reverse chunk loop, forward
-// recompute from chunk-start states, reverse adjoint scan seeded by the final-state
+// states recomputed from stored residuals, reverse adjoint scan seeded by the final-state
 // cotangent, du/ddelta/dA/dB/dC formulas) and its dormant fused branches :151-203,
 // :442-485 (softplus, z gate, D, delta bias, initial-state gradient).
 //
-// Mapping: one wave per channel, lane = segment of kT steps, chunk = 64*kT = 512 steps
-// (the granularity of the forward's `carries` residual, so no forward recompute across
-// chunks is needed). A workgroup of kW waves walks K rounds of kW channels of one batch
-// row ("channel block") and every chunk from last to first. Per chunk, per state n:
-//   forward  local aggregate + 64-lane DPP scan from the stored chunk-start state, then a
-//            re-run that keeps h_t and a_bar*h_{t-1} in registers
-//   reverse  local aggregate of the adjoint + 64-lane reverse scan seeded by the carry from
-//            the chunk to the right (or dlast), then a re-run producing lambda_t and all
-//            per-step gradient terms
+// Mapping: one wave per channel, lane = segment of kT = 8 steps, chunk = 64 segments = 512
+// steps. Lanes hold segments in REVERSED time order (lane 0 = the chunk's last segment), so
+// the adjoint, which runs backwards in time, is joined across lanes by the cheap upward
+// DPP scan (row shifts + row broadcasts). A workgroup of kW waves walks K rounds of kW
+// channels of one batch row and every chunk from last to first. Per chunk the B/C rows of
+// all states are staged once in LDS (direct-to-LDS loads) and shared by every wave and
+// round. Per (channel, state):
+//   forward  from the forward pass's stored state at the segment start (no scan): a_t,
+//            a_t*h_{t-1}, h_t; dC partial g_t*h_t
+//   reverse  local adjoint aggregate, 64-lane scan seeded by the message from the chunk to
+//            the right (dlast for the last chunk), then a re-run producing lambda_t and
+//            every per-step gradient term; dB partial lambda_t*delta_t*u_t
 // dB/dC are sums over channels: each wave adds its per-(n, t) terms into an LDS
-// accumulator shared by the workgroup (rows owned in rotation, plain read-add-write),
-// flushed once per chunk to a per-channel-block partial; a second kernel sums the
-// partials in a fixed order.
-// This replaces the reference's one-global-atomic-per-(b,d,n,t) scheme
-// (selective_scan_bwd_kernel.cuh:295-318).
-#include <type_traits>
-
+// accumulator shared by the workgroup (rows owned in rotation, plain read-add-write, one
+// barrier per state), flushed once per chunk to a per-channel-block partial; a second
+// kernel sums the partials in a fixed order. This replaces the reference's
+// one-global-atomic-per-(b,d,n,t) scheme (selective_scan_bwd_kernel.cuh:295-318).
 #include "mss_common.h"
 
 namespace mss {
 
-constexpr int kBwdT = 8;
-constexpr int kBwdW = 12;
-constexpr int kMaxChanPerBlock = 240;  // 20 rounds of 12 waves
-constexpr int kCUs = 256;               // MI355X compute units
+constexpr int kBwdT = kSegSteps;  // steps per lane: the granularity of the forward's carries
+constexpr int kBwdW = 12;         // waves per workgroup (3 per SIMD, one workgroup per CU)
+constexpr int kBwdChunk = 64 * kBwdT;
+constexpr int kMaxChanPerBlock = 96;  // 8 rounds of 12 waves
+constexpr int kCUs = 256;             // MI355X compute units
 
-template <int kT, int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
-__global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
-  constexpr int kChunk = 64 * kT;
-  static_assert(kChunk == kCarryChunk, "backward chunk must match the carry residual");
-  // dB/dC partial sums of the workgroup's channels for one chunk: [copy][n][j][which][lane]
-  // (step j of lane `lane`'s segment): conflict-free for the 64 lanes of a wave, and every
-  // access of a state is a constant offset from one per-lane base, so the read-add-writes
-  // batch freely. At state iteration i wave w owns row n = (i + w) mod N of
-  // copy w / N, so rows are updated with plain read-add-write in a fixed order
-  // (LDS float atomics run ~40x slower than stores on gfx950 and are avoided).
-  __shared__ float acc[2 * kMaxN * kChunk];
-  __shared__ float s_mu[kMaxChanPerBlock][kMaxN];
+// Floats of LDS holding the dB/dC accumulator (ceil(kW/N) copies of 2N rows of a chunk,
+// see the kernel) followed by the B/C stage (2N rows of the chunk in bc_t), maximised over
+// N in [1, kMaxN]: N = 11 needs two accumulator copies (22 rows) and is the largest.
+constexpr int bwd_lds_floats(int bc_bytes) {
+  int m = 0;
+  for (int n = 1; n <= kMaxN; ++n) {
+    const int v = ((kBwdW + n - 1) / n) * n * 2 * kBwdChunk + n * 2 * kBwdChunk * bc_bytes / 4;
+    m = v > m ? v : m;
+  }
+  return m;
+}
+
+// Upward (lane i takes lane i - 2^k) scan step of two chains at once: an affine map (P, H)
+// and a plain sum S. Each of the three DPP reads comes two VALU instructions after the
+// write of its source, which is the wait a DPP read needs; the caller pads the first and
+// last step (MSS_DPP_PAD).
+#define MSS_DPP_AFFINE_SUM_STEP(CTRL, RM, H, P, S)                                     \
+  asm volatile("v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
+               "v_add_f32_dpp %2, %2, %2 " CTRL " row_mask:" RM " bank_mask:0xf\n\t"  \
+               "v_mul_f32_dpp %1, %1, %1 " CTRL " row_mask:" RM " bank_mask:0xf"      \
+               : "+v"(H), "+v"(P), "+v"(S))
+#define MSS_DPP_PAD() asm volatile("s_nop 1")
+
+// Inclusive upward scan over the 64 lanes of maps m -> P*m + H (lower lanes applied
+// first: (Pl, Hl) then (Pr, Hr) gives (Pl*Pr, Pr*Hl + Hr), the operator of reference
+// native/selective_scan_cuda.cu:58-63) and of plain sums S. Lane 63 ends with the
+// whole wave's map and sum.
+__device__ __forceinline__ void wave_scan_affine_sum(float& P, float& H, float& S) {
+  MSS_DPP_PAD();
+  MSS_DPP_AFFINE_SUM_STEP("row_shr:1", "0xf", H, P, S);
+  MSS_DPP_AFFINE_SUM_STEP("row_shr:2", "0xf", H, P, S);
+  MSS_DPP_AFFINE_SUM_STEP("row_shr:4", "0xf", H, P, S);
+  MSS_DPP_AFFINE_SUM_STEP("row_shr:8", "0xf", H, P, S);
+  MSS_DPP_AFFINE_SUM_STEP("row_bcast:15", "0xa", H, P, S);
+  MSS_DPP_AFFINE_SUM_STEP("row_bcast:31", "0xc", H, P, S);
+  MSS_DPP_PAD();
+}
+
+// Sum over the 64 lanes, complete in lane 63 (other lanes hold prefix sums).
+__device__ __forceinline__ float wave_sum_to_last(float v) {
+  v += dpp_mov<kRowShr1, 0xF>(0.f, v);
+  v += dpp_mov<kRowShr2, 0xF>(0.f, v);
+  v += dpp_mov<kRowShr4, 0xF>(0.f, v);
+  v += dpp_mov<kRowShr8, 0xF>(0.f, v);
+  v += dpp_mov<kRowBcast15, 0xA>(0.f, v);
+  v += dpp_mov<kRowBcast31, 0xC>(0.f, v);
+  return v;
+}
+
+// Stage the B and C rows of all N states, steps [t0, t0 + 64*kT), into
+// dst[n][B|C][slot]; segment s's q-th 16-byte slot sits at kQ*s + (q ^ slot_swz(s)) so the
+// reads of 16 consecutive lanes hit distinct bank groups. dma: rows are 16-byte aligned
+// and L is a multiple of the slot width; past-the-end slots re-read the last valid slot
+// (finite values that only meet zero coefficients). Otherwise scalar loads, zero past L.
+template <int kT, int kW, typename bc_t>
+__device__ __forceinline__ void stage_chunk(const bc_t* __restrict__ Bb, const bc_t* __restrict__ Cb,
+                                            int N, int t0, int L, long long sn, bool dma,
+                                            uint4 (*dst)[2][64 * kT * sizeof(bc_t) / 16], int tid) {
+  constexpr int kE = BcStage<bc_t>::kElemsPerSlot;
+  constexpr int kQ = kT / kE;
+  constexpr int kSlots = 64 * kQ;  // per row, a multiple of 64
+  if (dma) {
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    for (int f0 = w * 64; f0 < N * 2 * kSlots; f0 += kW * 64) {
+      const int rowi = f0 / kSlots;  // wave-uniform
+      const int n = rowi >> 1;
+      const int which = rowi & 1;
+      const int s0 = f0 - rowi * kSlots;
+      const int s = s0 + lane;
+      const int i = s / kQ;
+      const int q = (s % kQ) ^ slot_swz<kQ>(i);
+      int e = t0 + i * kT + q * kE;
+      e = e < L ? e : L - kE;
+      const bc_t* src = (which ? Cb : Bb) + n * sn + e;
+      __builtin_amdgcn_global_load_lds((gbl_void_t)src, (lds_void_t)(&dst[n][which][s0]), 16, 0, 0);
+    }
+  } else {
+    for (int f = tid; f < N * 2 * 64 * kT; f += kW * 64) {
+      const int rowi = f / (64 * kT);
+      const int n = rowi >> 1;
+      const int which = rowi & 1;
+      const int e = f - rowi * 64 * kT;
+      const int i = e / kT;
+      const int r = e % kT;
+      const int sl = kQ * i + ((r / kE) ^ slot_swz<kQ>(i));
+      const int t = t0 + e;
+      bc_t v;
+      if (t < L) {
+        v = ((which ? Cb : Bb) + n * sn)[t];
+      } else {
+        store_as(&v, 0.f);
+      }
+      reinterpret_cast<bc_t*>(&dst[n][which][0])[sl * kE + (r % kE)] = v;
+    }
+  }
+}
+
+template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
+__global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
+  constexpr int kT = kBwdT;
+  constexpr int kW = kBwdW;
+  constexpr int kChunk = kBwdChunk;
+  constexpr int kRowSlots = kChunk * static_cast<int>(sizeof(bc_t)) / 16;
+  // One LDS buffer: first the dB/dC partial sums of the workgroup's channels for one
+  // chunk, acc[copy][n][j][B|C][lane] (step j of lane `lane`'s segment), conflict-free for
+  // the 64 lanes of a wave. At state iteration i wave w owns row n = (i + w) mod N of copy
+  // w / N, so rows are updated with plain read-add-write in a fixed order (LDS float
+  // atomics are avoided: far slower than a read, an add and a write on gfx950). Then the
+  // B/C rows of the current chunk, all states: stage[n][B|C][slot].
+  __shared__ __attribute__((aligned(16))) float lds[bwd_lds_floats(sizeof(bc_t))];
+  __shared__ float s_mu[kMaxChanPerBlock][kMaxN];  // adjoint message entering the chunk
   __shared__ float s_dA[kMaxChanPerBlock][kMaxN];
   __shared__ float s_dD[kMaxChanPerBlock];
   __shared__ float s_db[kMaxChanPerBlock];
-  __shared__ float s_a[kW][kMaxN];
-  __shared__ float s_h0[kW][kMaxN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const int seg = 63 - lane;  // this lane's segment within a chunk (reversed time order)
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.y;
   const int blk = blockIdx.x;
@@ -60,14 +160,17 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   const int K = p.chan_per_block / kW;
   const int len = p.seq_lens ? min(max(p.seq_lens[b], 0), L) : L;
   const bool vec_io = p.vec_io != 0;
-  const bool vec_bc = p.vec_bc != 0;
+  const bool dma = p.vec_bc != 0;
   const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + b * p.bc_sb;
   const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + b * p.bc_sb;
 
-  const int n_copy = (kW + N - 1) / N;  // n_copy * N <= 2 * kMaxN for N <= kMaxN
-  const int w_mod_n = w % N;
+  const int n_copy = (kW + N - 1) / N;
+  const int acc_floats = n_copy * N * 2 * kChunk;
+  float* const acc = lds;
+  uint4(*const stage)[2][kRowSlots] = reinterpret_cast<uint4(*)[2][kRowSlots]>(lds + acc_floats);
+  const int wmod = w % N;
   float* const acc_w = acc + (w / N) * 2 * N * kChunk;
-  for (int i = tid; i < 2 * kMaxN * kChunk; i += kW * 64) acc[i] = 0.f;
+  for (int i = tid; i < acc_floats; i += kW * 64) acc[i] = 0.f;
   for (int k = 0; k < K; ++k) {
     const int cl = k * kW + w;
     const int d = blk * p.chan_per_block + cl;
@@ -82,19 +185,48 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       s_db[cl] = 0.f;
     }
   }
-  __syncthreads();
 
   const int n_chunks = (L + kChunk - 1) / kChunk;
+  const int n_live = (len + kChunk - 1) / kChunk;  // chunks holding at least one valid step
+  if (n_live > 0) stage_chunk<kT, kW, bc_t>(Bb, Cb, N, (n_live - 1) * kChunk, L, p.bc_sn, dma, stage, tid);
+  wait_vmem_all();
+  __syncthreads();
+
   for (int c = n_chunks - 1; c >= 0; --c) {
     const int t0 = c * kChunk;
-    const int tl = t0 + lane * kT;
-    // A chunk wholly inside the row's length, with vector-aligned rows, runs a specialised
-    // body without bounds checks or validity masks (every chunk but a ragged last one).
-    const bool full = vec_io && vec_bc && (t0 + kChunk <= len);  // wave-uniform
-    auto chunk_body = [&](auto full_tag) {
-    constexpr bool kFull = decltype(full_tag)::value;
-    const bool fast = kFull || (vec_io && (t0 + kChunk <= L));     // wave-uniform
-    const bool fast_bc = kFull || (vec_bc && (t0 + kChunk <= L));  // wave-uniform
+    const int tl = t0 + seg * kT;  // first step of this lane's segment
+    const bool fast = vec_io && (t0 + kChunk <= L);  // wave-uniform
+    const int seg_idx = t0 / kT + seg;               // index into a carries row
+    const bool seg_ok = seg_idx < p.n_seg;
+
+    if (c >= n_live) {
+      // Whole chunk past this row's length: zero gradients; the adjoint message passes
+      // through the identity steps unchanged.
+      for (int k = 0; k < K; ++k) {
+        const int cl = k * kW + w;
+        const int d = blk * p.chan_per_block + cl;
+        if (d >= p.dim) continue;
+        const long long row = b * p.io_sb + d * p.io_sd;
+        float zero[kT];
+#pragma unroll
+        for (int j = 0; j < kT; ++j) zero[j] = 0.f;
+        store_seg<kT>(static_cast<io_t*>(p.du) + row, tl, L, fast, zero);
+        store_seg<kT>(static_cast<io_t*>(p.ddelta) + row, tl, L, fast, zero);
+        if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, zero);
+        if (c == 0 && p.dinit && lane < N)
+          p.dinit[(static_cast<size_t>(b) * p.dim + d) * N + lane] = s_mu[cl][lane];
+      }
+      // ... and this block's dB/dC partials of the chunk are zero.
+      const size_t nl = static_cast<size_t>(N) * L;
+      float* part = p.part_dBC + static_cast<size_t>(blk) * p.part_stride + static_cast<size_t>(b) * 2 * nl;
+      const int width = min(kChunk, L - t0);
+      for (int e = tid; e < 2 * N * width; e += kW * 64) {
+        const int rowi = e / width;
+        part[static_cast<size_t>(rowi) * L + t0 + (e - rowi * width)] = 0.f;
+      }
+      continue;
+    }
+
     for (int k = 0; k < K; ++k) {
       const int cl = k * kW + w;
       const int d_raw = blk * p.chan_per_block + cl;
@@ -102,190 +234,160 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       const int d = active ? d_raw : p.dim - 1;
       const size_t chan = static_cast<size_t>(b) * p.dim + d;
       const long long row = b * p.io_sb + d * p.io_sd;
-      io_t* __restrict__ du_row = static_cast<io_t*>(p.du) + row;
-      io_t* __restrict__ dd_row = static_cast<io_t*>(p.ddelta) + row;
+      const float* __restrict__ carry_row = p.carries + chan * N * p.n_seg + seg_idx;
 
-      if (!kFull && t0 >= len) {  // whole chunk past this row's length: zero gradients, carry passes
-        if (!active) continue;
-        float zero[kT];
-#pragma unroll
-        for (int j = 0; j < kT; ++j) zero[j] = 0.f;
-        store_seg<kT>(du_row, tl, L, fast, zero);
-        store_seg<kT>(dd_row, tl, L, fast, zero);
-        if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, zero);
-        if (c == 0 && p.dinit && lane < N) {
-          // len == 0: x0 flows through identity steps to the last state.
-          p.dinit[chan * N + lane] = s_mu[cl][lane];
-        }
-        continue;
-      }
-
-      if (lane < N) {
-        s_a[w][lane] = p.A[static_cast<size_t>(d) * N + lane];
-        s_h0[w][lane] = c == 0 ? (p.x0 ? p.x0[chan * N + lane] : 0.f)
-                               : p.carries[(chan * p.n_carry + (c - 1)) * N + lane];
-      }
+      // ---- per-step inputs of the row
+      const float a_lane = lane < N ? p.A[static_cast<size_t>(d) * N + lane] : 0.f;
       const float Dv = p.D ? p.D[d] : 0.f;
       const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
       float dlt[kT], dlu[kT], uu[kT], g[kT], s1[kT], s2[kT];
       float ssum = 0.f;
-      load_seg<kT>(static_cast<const io_t*>(p.delta) + row, tl, L, fast, dlt);
-      load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
-      load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, fast, g);
-      if constexpr (kHasZ) {
-        // Gate: g = dout * silu(z); dz = dout * y * sigmoid(z) * (1 + z * (1 - sigmoid(z)))
-        // with y the pre-gate output kept by the forward.
-        float zr[kT], yp[kT];
-        load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zr);
-        load_seg<kT>(static_cast<const io_t*>(p.y_pre) + row, tl, L, fast, yp);
+      float hin_next = 0.f;
+      if (active) {
+        if (seg_ok) hin_next = carry_row[static_cast<size_t>(wmod) * p.n_seg];
+        load_seg<kT>(static_cast<const io_t*>(p.delta) + row, tl, L, fast, dlt);
+        load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
+        load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, fast, g);
+        if constexpr (kHasZ) {
+          // g = dout * silu(z); dz = dout * y * sigmoid(z) * (1 + z * (1 - sigmoid(z))),
+          // y the pre-gate output kept by the forward.
+          float zr[kT], yp[kT];
+          load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zr);
+          load_seg<kT>(static_cast<const io_t*>(p.y_pre) + row, tl, L, fast, yp);
+#pragma unroll
+          for (int j = 0; j < kT; ++j) {
+            const float go = tl + j < len ? g[j] : 0.f;
+            const float sz = sigmoid(zr[j]);
+            yp[j] = go * yp[j] * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
+            g[j] = go * zr[j] * sz;
+          }
+          store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);
+        }
 #pragma unroll
         for (int j = 0; j < kT; ++j) {
-          const bool valid = kFull || tl + j < len;
-          const float go = valid ? g[j] : 0.f;
-          const float sz = sigmoid(zr[j]);
-          yp[j] = go * yp[j] * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
-          g[j] = go * zr[j] * sz;
+          const bool valid = tl + j < len;
+          const float x = dlt[j] + bias;
+          float dv = p.delta_softplus ? softplus(x) : x;
+          dv = valid ? dv : 0.f;
+          uu[j] = valid ? uu[j] : 0.f;
+          dlt[j] = dv;
+          dlu[j] = kZOH ? uu[j] : dv * uu[j];
+          if constexpr (!kHasZ) g[j] = valid ? g[j] : 0.f;
+          s1[j] = 0.f;
+          s2[j] = 0.f;
+          ssum += dv;
         }
-        store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);
-      }
-#pragma unroll
-      for (int j = 0; j < kT; ++j) {
-        const bool valid = kFull || tl + j < len;
-        const float x = dlt[j] + bias;
-        float dv = p.delta_softplus ? softplus(x) : x;
-        dv = valid ? dv : 0.f;
-        const float uv = valid ? uu[j] : 0.f;
-        dlt[j] = dv;
-        uu[j] = uv;
-        dlu[j] = dv * uv;
-        if constexpr (!kHasZ) g[j] = valid ? g[j] : 0.f;
-        s1[j] = 0.f;
-        s2[j] = 0.f;
-        ssum += dv;
       }
 
-      // States in a per-wave rotated order (see the accumulator above); the barrier per
-      // iteration keeps every wave inside the same iteration. B/C rows of the next state are
-      // requested at the end of each iteration, into the registers of the current ones.
-      float bv[kT], cv[kT];
-      if (active) {
-        load_seg<kT>(Bb + w_mod_n * p.bc_sn, tl, L, fast_bc, bv);
-        load_seg<kT>(Cb + w_mod_n * p.bc_sn, tl, L, fast_bc, cv);
-      }
+      // ---- states, in the wave's rotated order (see the accumulator). dA of state n rides
+      // on the next state's scan; the last one is reduced after the loop.
+      float dA_pend = 0.f;
+      int n_pend = -1;
       for (int i = 0; i < N; ++i) {
-        int n = i + w_mod_n;
+        int n = i + wmod;
         n = n >= N ? n - N : n;
+        const float hin = hin_next;
+        if (active && seg_ok && i + 1 < N) {
+          const int nn = n + 1 == N ? 0 : n + 1;
+          hin_next = carry_row[static_cast<size_t>(nn) * p.n_seg];
+        }
         __syncthreads();
         if (!active) continue;
-        // This wave owns accumulator row n until the next barrier. Its dC half is fetched
-        // now and updated by the forward re-run (where h_t is produced), its dB half is
-        // fetched after that and updated by the reverse pass: half a row of registers live.
-        float* accn = acc_w + n * 2 * kChunk + lane;
-        float accC[kT];
-#pragma unroll
-        for (int j = 0; j < kT; ++j) accC[j] = accn[j * 128 + 64];
-        const float An = s_a[w][n];
+        const float An = readlane(a_lane, n);
         const float a2 = An * kLog2e;
-        float a[kT];
-        // ---- forward: local aggregate, scan, re-run from the true carry-in
-        float H = 0.f;
-#pragma unroll
-        for (int j = 0; j < kT; ++j) {
-          a[j] = fast_exp2(dlt[j] * a2);
-          const float bu = kZOH ? (expm1f(dlt[j] * An) * fast_rcp(An)) * bv[j] * uu[j] : dlu[j] * bv[j];
-          H = __builtin_fmaf(a[j], H, bu);
-        }
-        const float pseg = fast_exp2(a2 * ssum);
-        float P = pseg;
-        wave_scan_affine_fwd(P, H);
-        const float run = s_h0[w][n];
-        const float hend = __builtin_fmaf(P, run, H);
-        const float hin = dpp_mov<kWaveShr1, 0xF>(run, hend);  // state before the lane's first step
-        float hh[kT];
+        const float mu = s_mu[cl][n];
+        float bv[kT], cg[kT];
+        read_staged<kT, bc_t>(stage[n][0], seg, bv);
+        read_staged<kT, bc_t>(stage[n][1], seg, cg);
+        // This wave owns accumulator row n until the next barrier.
+        float* accn = acc_w + n * 2 * kChunk + lane;
+        float a[kT], ah[kT];
         {
+          float accC[kT];
+#pragma unroll
+          for (int j = 0; j < kT; ++j) accC[j] = accn[j * 128 + 64];
           float h = hin;
 #pragma unroll
           for (int j = 0; j < kT; ++j) {
+            a[j] = fast_exp2(dlt[j] * a2);
             const float bu = kZOH ? (expm1f(dlt[j] * An) * fast_rcp(An)) * bv[j] * uu[j] : dlu[j] * bv[j];
-            h = __builtin_fmaf(a[j], h, bu);
-            hh[j] = h;
+            ah[j] = a[j] * h;  // a_bar_t * h_{t-1}
+            h = ah[j] + bu;
             accC[j] = __builtin_fmaf(g[j], h, accC[j]);
           }
-        }
 #pragma unroll
-        for (int j = 0; j < kT; ++j) accn[j * 128 + 64] = accC[j];
+          for (int j = 0; j < kT; ++j) accn[j * 128 + 64] = accC[j];
+        }
+        // ---- reverse: local adjoint aggregate, scan, re-run with the true message
+#pragma unroll
+        for (int j = 0; j < kT; ++j) cg[j] *= g[j];
+        float lam = cg[kT - 1];
+#pragma unroll
+        for (int j = kT - 2; j >= 0; --j) lam = __builtin_fmaf(a[j + 1], lam, cg[j]);
+        float P = fast_exp2(a2 * ssum);  // product of the segment's a_bar
+        float Q = a[0] * lam;            // message the segment sends left, zero input
+        float S = dA_pend;
+        wave_scan_affine_sum(P, Q, S);
+        const float mo = __builtin_fmaf(P, mu, Q);       // message leaving this lane's segment
+        const float m_in = dpp_mov<kWaveShr1, 0xF>(mu, mo);  // message entering it
+        if (lane == 63) {
+          s_mu[cl][n] = mo;
+          if (c == 0 && p.dinit) p.dinit[chan * N + n] = mo;  // d h_{-1} = a_bar_0 * lambda_0
+          if (n_pend >= 0) s_dA[cl][n_pend] += S;
+        }
         float accB[kT];
 #pragma unroll
         for (int j = 0; j < kT; ++j) accB[j] = accn[j * 128];
-        // ---- reverse: local aggregate of lambda, reverse scan, re-run with true lambda
-        float lam = cv[kT - 1] * g[kT - 1];
-#pragma unroll
-        for (int j = kT - 2; j >= 0; --j) lam = __builtin_fmaf(a[j + 1], lam, cv[j] * g[j]);
-        float ra = pseg, rb = a[0] * lam;
-        wave_scan_affine_rev(ra, rb, lane);
-        const float mu_in = s_mu[cl][n];
-        const float mu_out = readlane(__builtin_fmaf(ra, mu_in, rb), 0);
-        const float ra_s = dpp_mov<kWaveShl1, 0xF>(1.f, ra);
-        const float rb_s = dpp_mov<kWaveShl1, 0xF>(0.f, rb);
-        lam = __builtin_fmaf(ra_s, mu_in, rb_s) + cv[kT - 1] * g[kT - 1];
-        float dA_acc = 0.f;
+        lam = m_in + cg[kT - 1];
+        float dA_l = 0.f;
 #pragma unroll
         for (int j = kT - 1; j >= 0; --j) {
-          if (j < kT - 1) lam = __builtin_fmaf(a[j + 1], lam, cv[j] * g[j]);
-          const float ah = a[j] * (j > 0 ? hh[j - 1] : hin);  // a_bar_t * h_{t-1}
-          const float q = lam * ah;
-          float dBv;
+          if (j < kT - 1) lam = __builtin_fmaf(a[j + 1], lam, cg[j]);
+          const float q = lam * ah[j];
           if constexpr (kZOH) {
             const float e = expm1f(dlt[j] * An) * fast_rcp(An);
             const float lb = lam * bv[j];
             s1[j] = __builtin_fmaf(lb, e, s1[j]);
             s2[j] = __builtin_fmaf(An, q, __builtin_fmaf(lb * uu[j], a[j], s2[j]));
             const float dedA = (dlt[j] * a[j] - e) * fast_rcp(An);
-            dA_acc = __builtin_fmaf(dlt[j], q, __builtin_fmaf(lb * uu[j], dedA, dA_acc));
-            dBv = lam * e * uu[j];
+            dA_l = __builtin_fmaf(dlt[j], q, __builtin_fmaf(lb * uu[j], dedA, dA_l));
+            accB[j] = __builtin_fmaf(lam * e, uu[j], accB[j]);
           } else {
             s1[j] = __builtin_fmaf(lam, bv[j], s1[j]);
             s2[j] = __builtin_fmaf(An, q, s2[j]);
-            dA_acc = __builtin_fmaf(dlt[j], q, dA_acc);
-            dBv = lam * dlu[j];
+            dA_l = __builtin_fmaf(dlt[j], q, dA_l);
+            accB[j] = __builtin_fmaf(lam, dlu[j], accB[j]);
           }
-          accB[j] += dBv;
         }
 #pragma unroll
         for (int j = 0; j < kT; ++j) accn[j * 128] = accB[j];
-        {  // next state's rows (after the last state: an unused in-bounds reload)
-          const int nn = n + 1 == N ? 0 : n + 1;
-          load_seg<kT>(Bb + nn * p.bc_sn, tl, L, fast_bc, bv);
-          load_seg<kT>(Cb + nn * p.bc_sn, tl, L, fast_bc, cv);
-        }
-        const float dA_sum = wave_sum(dA_acc);
-        if (lane == 0) {
-          s_mu[cl][n] = mu_out;
-          s_dA[cl][n] += dA_sum;
-          if (c == 0 && p.dinit) p.dinit[chan * N + n] = mu_out;
-        }
+        dA_pend = dA_l;
+        n_pend = n;
+      }
+      if (!active) continue;
+      {
+        const float S = wave_sum_to_last(dA_pend);
+        if (lane == 63) s_dA[cl][n_pend] += S;
       }
 
-      if (!active) continue;
+      // ---- per-step gradients of the row
       if constexpr (!kZOH) {
         // Euler needs u only from here on: reload it rather than hold it across the loop.
         load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
-#pragma unroll
-        for (int j = 0; j < kT; ++j) uu[j] = (kFull || tl + j < len) ? uu[j] : 0.f;
       }
-      // ---- per-step gradients of the row
       float dD_acc = 0.f, db_acc = 0.f;
       float duv[kT], ddv[kT];
 #pragma unroll
       for (int j = 0; j < kT; ++j) {
-        const bool valid = kFull || tl + j < len;
+        const bool valid = tl + j < len;
+        const float uv = valid ? uu[j] : 0.f;
         float du_j, dd_j;
         if constexpr (kZOH) {
           du_j = __builtin_fmaf(Dv, g[j], s1[j]);
           dd_j = s2[j];
         } else {
           du_j = __builtin_fmaf(dlt[j], s1[j], Dv * g[j]);
-          dd_j = __builtin_fmaf(uu[j], s1[j], s2[j]);
+          dd_j = __builtin_fmaf(uv, s1[j], s2[j]);
         }
         if (p.delta_softplus) {
           // d softplus(x)/dx = sigmoid(x) = 1 - exp(-softplus(x)); identity above 20.
@@ -293,56 +395,58 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         }
         du_j = valid ? du_j : 0.f;
         dd_j = valid ? dd_j : 0.f;
-        dD_acc = __builtin_fmaf(g[j], uu[j], dD_acc);
+        dD_acc = __builtin_fmaf(g[j], uv, dD_acc);
         db_acc += dd_j;
         duv[j] = du_j;
         ddv[j] = dd_j;
       }
-      store_seg<kT>(du_row, tl, L, fast, duv);
-      store_seg<kT>(dd_row, tl, L, fast, ddv);
-      const float dD_sum = wave_sum(dD_acc);
-      const float db_sum = wave_sum(db_acc);
-      if (lane == 0) {
+      store_seg<kT>(static_cast<io_t*>(p.du) + row, tl, L, fast, duv);
+      store_seg<kT>(static_cast<io_t*>(p.ddelta) + row, tl, L, fast, ddv);
+      const float dD_sum = wave_sum_to_last(dD_acc);
+      const float db_sum = wave_sum_to_last(db_acc);
+      if (lane == 63) {
         s_dD[cl] += dD_sum;
         s_db[cl] += db_sum;
       }
     }
 
-    };
-    if (full) {
-      chunk_body(std::true_type{});
-    } else {
-      chunk_body(std::false_type{});
-    }
-
-    // ---- flush this chunk's dB/dC sums over the block's channels
+    // ---- all waves are done with this chunk's stage and accumulator: start staging the
+    // next chunk (to the left), then flush this chunk's dB/dC sums over the block's channels.
     __syncthreads();
+    if (c > 0) stage_chunk<kT, kW, bc_t>(Bb, Cb, N, t0 - kChunk, L, p.bc_sn, dma, stage, tid);
     const size_t nl = static_cast<size_t>(N) * L;
     float* part = p.part_dBC + static_cast<size_t>(blk) * p.part_stride + static_cast<size_t>(b) * 2 * nl;
-    for (int row_i = 0; row_i < 2 * N; ++row_i) {  // (which, n) rows of the accumulator
-      const int which = row_i >= N;
-      const int n = row_i - which * N;
-      float* dst = part + which * nl + static_cast<size_t>(n) * L + t0;
-      // Thread -> (segment ln, quarter q): steps 4q..4q+3 of segment ln, summed over copies.
-      for (int pos = tid; pos < 64 * (kT / 4); pos += kW * 64) {
-        const int ln = pos & 63, q = pos >> 6;
-        float v[4];
+    const bool vec_part = (L % 4) == 0;
+    for (int task = tid; task < 2 * N * 128; task += kW * 64) {
+      // Row (which, n); acc lane ln (segment 63 - ln); steps 4qq..4qq+3 of the segment.
+      const int rowi = task >> 7;
+      const int which = rowi >= N;
+      const int n = rowi - which * N;
+      const int ln = task & 63;
+      const int qq = (task >> 6) & 1;
+      float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int off = n * 2 * kChunk + (4 * q + e) * 128 + which * 64 + ln;
-          float sum = 0.f;
-          for (int cp = 0; cp < n_copy; ++cp) {
-            sum += acc[cp * 2 * N * kChunk + off];
-            acc[cp * 2 * N * kChunk + off] = 0.f;
-          }
-          v[e] = sum;
+      for (int e = 0; e < 4; ++e) {
+        const int off = n * 2 * kChunk + (4 * qq + e) * 128 + which * 64 + ln;
+        float sum = 0.f;
+        for (int cp = 0; cp < n_copy; ++cp) {
+          sum += acc[cp * 2 * N * kChunk + off];
+          acc[cp * 2 * N * kChunk + off] = 0.f;
         }
-        const int toff = ln * kT + 4 * q;
+        v[e] = sum;
+      }
+      const int t = t0 + (63 - ln) * kT + 4 * qq;
+      float* dst = part + which * nl + static_cast<size_t>(n) * L + t;
+      if (vec_part && t + 4 <= L) {
+        const f32x4 x = {v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(dst) = x;
+      } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (t0 + toff + e < L) dst[toff + e] = v[e];
+          if (t + e < L) dst[e] = v[e];
       }
     }
+    wait_vmem_all();
     __syncthreads();
   }
 
@@ -436,8 +540,7 @@ __global__ __launch_bounds__(256) void reduce_small_kernel(const float* __restri
 template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
 static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
   dim3 grid(p.n_blocks_d, p.batch);
-  hipLaunchKernelGGL((bwd_kernel<kBwdT, kBwdW, kZOH, kHasZ, io_t, bc_t>), grid, dim3(kBwdW * 64), 0,
-                     stream, p);
+  hipLaunchKernelGGL((bwd_kernel<kZOH, kHasZ, io_t, bc_t>), grid, dim3(kBwdW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -451,11 +554,12 @@ static hipError_t launch_bwd_io(const BwdParams& p, int zoh, hipStream_t stream)
 }
 
 int bwd_chan_per_block(int batch, int dim, int varlen) {
-  // One workgroup per CU holds the dB/dC accumulator (LDS), so the grid should fit one
-  // pass over the 256 CUs: the fewest channel rounds K with batch * ceil(dim / (kW*K))
-  // <= 256 (more rounds also mean fewer dB/dC partials to reduce). With variable lengths
-  // rows finish at different times, so workgroups stay ~4x smaller and the hardware
-  // balances them. Bounded by the LDS bookkeeping size; depends on shapes only.
+  // One workgroup per CU holds the B/C stage and the dB/dC accumulator (LDS), so the grid
+  // should fit one pass over the 256 CUs: the fewest channel rounds K with
+  // batch * ceil(dim / (kW*K)) <= 256 (more rounds also mean fewer dB/dC partials to
+  // reduce). With variable lengths rows finish at different times, so workgroups stay ~4x
+  // smaller and the hardware balances them. Bounded by the LDS bookkeeping size; depends
+  // on shapes only.
   const long long per_row = (dim + kBwdW - 1) / kBwdW;  // rounds needed for a whole row
   const long long target = varlen ? 4 * kCUs : kCUs;
   long long k = (static_cast<long long>(batch) * per_row + target - 1) / target;

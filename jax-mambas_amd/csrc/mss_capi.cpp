@@ -104,7 +104,7 @@ bool strides_aligned(long long s0, long long s1, size_t esz) {
   return (static_cast<size_t>(s0) * esz) % 16 == 0 && (static_cast<size_t>(s1) * esz) % 16 == 0;
 }
 
-int n_carry_of(int32_t seqlen) { return (seqlen + MSS_CARRY_CHUNK - 1) / MSS_CARRY_CHUNK; }
+int n_seg_of(int32_t seqlen) { return (seqlen + MSS_SEG_STEPS - 1) / MSS_SEG_STEPS; }
 
 struct BwdLayout {
   int chan_per_block = 0, n_blocks_d = 0;
@@ -172,7 +172,7 @@ int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
   // B/C staging also needs L to be a multiple of the 16-byte slot width.
   p.vec_bc = (bc_row % 16 == 0) && strides_aligned(st.bc_sb, st.bc_sn, bc_e) && aligned16(a->B) &&
              aligned16(a->C);
-  p.n_carry = n_carry_of(a->seqlen);
+  p.n_seg = n_seg_of(a->seqlen);
   p.n_ref = (a->seqlen + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK;
   p.u = a->u;
   p.delta = a->delta;
@@ -216,7 +216,7 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
              aligned16(a->dz) && aligned16(a->y_pre);
   p.vec_bc = (bc_row % 16 == 0) && strides_aligned(st.bc_sb, st.bc_sn, bc_e) && aligned16(a->B) &&
              aligned16(a->C);
-  p.n_carry = n_carry_of(a->seqlen);
+  p.n_seg = n_seg_of(a->seqlen);
   p.chan_per_block = l.chan_per_block;
   p.n_blocks_d = l.n_blocks_d;
   p.u = a->u;
@@ -623,10 +623,10 @@ int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32
       !ddeltas || !dB || !dC || !du || !dinitial_x)
     return MSS_ERR_INVALID_ARGUMENT;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  // The backward needs the state at every 1024-step boundary; the reference residual
+  // The backward needs the state before every 8-step segment; the reference residual
   // only holds 2048-step ones, so a states-only forward refreshes them.
   const size_t carry_bytes =
-      static_cast<size_t>(batch) * dim * n_carry_of(length) * dstate * sizeof(float);
+      static_cast<size_t>(batch) * dim * dstate * n_seg_of(length) * sizeof(float);
   float* carries = nullptr;
   hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&carries), carry_bytes, st);
   if (e != hipSuccess) return hip_fail(e, "allocating carry states");
@@ -642,7 +642,7 @@ int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32
   const size_t row = static_cast<size_t>(length) * sizeof(float);
   p.vec_io = (row % 16 == 0) && aligned16(u) && aligned16(deltas);
   p.vec_bc = (row % 16 == 0) && aligned16(B) && aligned16(C);
-  p.n_carry = n_carry_of(length);
+  p.n_seg = n_seg_of(length);
   p.n_ref = (length + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK;
   p.u = u;
   p.delta = deltas;

@@ -16,7 +16,8 @@ namespace mss {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxN = 16;
-constexpr int kCarryChunk = 512;
+// Step granularity of the `carries` residual: the state before every kSegSteps-step segment.
+constexpr int kSegSteps = 8;
 constexpr int kRefChunk = 2048;
 
 struct bf16_t {
@@ -238,6 +239,54 @@ __device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L
 }
 
 // ---------------------------------------------------------------------------------
+// LDS staging of B/C rows with gfx950 direct-to-LDS loads (global_load_lds, 16 bytes per
+// lane). A staged row holds 64 segments of kT steps.
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef __attribute__((address_space(1))) void* gbl_void_t;
+
+// Staging layout of one chunk row: 16-byte slots; segment i (lane i) owns slots
+// [kQ*i, kQ*i + kQ) with its q-th slot stored at kQ*i + (q ^ swz(i)) so that 16
+// consecutive lanes reading their q-th slot hit 16 distinct 4-bank groups.
+template <int kQ>
+__device__ __forceinline__ int slot_swz(int i) {
+  static_assert(kQ >= 1 && kQ <= 16 && (kQ & (kQ - 1)) == 0, "kQ must be a power of two <= 16");
+  constexpr int kShift = kQ == 16 ? 0 : (kQ == 8 ? 1 : (kQ == 4 ? 2 : (kQ == 2 ? 3 : 4)));
+  return (i >> kShift) & (kQ - 1);
+}
+
+template <typename bc_t>
+struct BcStage {
+  static constexpr int kElemsPerSlot = 16 / static_cast<int>(sizeof(bc_t));
+};
+
+// Read lane `lane`'s kT staged values of one row (fp32 or bf16 in LDS) as floats.
+template <int kT, typename bc_t>
+__device__ __forceinline__ void read_staged(const uint4* __restrict__ row, int lane, float (&v)[kT]) {
+  constexpr int kE = BcStage<bc_t>::kElemsPerSlot;
+  constexpr int kQ = kT / kE;
+  const int sw = slot_swz<kQ>(lane);
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const uint4 x = row[kQ * lane + (q ^ sw)];
+    if constexpr (sizeof(bc_t) == 4) {
+      v[4 * q + 0] = __uint_as_float(x.x);
+      v[4 * q + 1] = __uint_as_float(x.y);
+      v[4 * q + 2] = __uint_as_float(x.z);
+      v[4 * q + 3] = __uint_as_float(x.w);
+    } else {
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[8 * q + 2 * k + 0] = __uint_as_float(w[k] << 16);
+        v[8 * q + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ---------------------------------------------------------------------------------
 // Kernel parameter blocks (host fills them after validation).
 struct NormParams {
   int features, tokens;
@@ -309,7 +358,7 @@ struct FwdParams {
   int delta_softplus;
   int vec_io;  // 16-byte vector access legal for u/delta/z/out rows
   int vec_bc;  // ... for B/C rows
-  int n_carry;  // ceil(L / kCarryChunk)
+  int n_seg;  // ceil(L / kSegSteps): carries row length
   int n_ref;    // ceil(L / 2048)
   long long io_sb, io_sd;  // row strides (elements) of u/delta/z/out/y_pre: batch, channel
   long long bc_sb, bc_sn;  // row strides of B/C: batch, state
@@ -325,7 +374,7 @@ struct FwdParams {
   const int* seq_lens;
   void* out;
   float* last;
-  float* carries;
+  float* carries;  // [B][D][N][n_seg]: state before each kSegSteps-step segment
   float* ref_states;
   void* y_pre;
 };
@@ -334,7 +383,7 @@ struct BwdParams {
   int batch, dim, seqlen, dstate;
   int delta_softplus;
   int vec_io, vec_bc;
-  int n_carry;
+  int n_seg;
   int chan_per_block;  // channels one workgroup walks (multiple of the wave count)
   int n_blocks_d;      // ceil(dim / chan_per_block)
   long long io_sb, io_sd;  // row strides of u/delta/z/y_pre/dout/du/ddelta/dz
@@ -349,7 +398,7 @@ struct BwdParams {
   const float* delta_bias;
   const float* x0;
   const int* seq_lens;
-  const float* carries;
+  const float* carries;  // [B][D][N][n_seg] from the forward
   const void* y_pre;
   const void* dout;
   const float* dlast;

@@ -35,49 +35,6 @@
 
 namespace mss {
 
-typedef __attribute__((address_space(3))) void* lds_void_t;
-typedef __attribute__((address_space(1))) void* gbl_void_t;
-
-// Staging layout of one chunk row: 16-byte slots; segment i (lane i) owns slots
-// [kQ*i, kQ*i + kQ) with its q-th slot stored at kQ*i + (q ^ swz(i)) so that 16
-// consecutive lanes reading their q-th slot hit 16 distinct 4-bank groups.
-template <int kQ>
-__device__ __forceinline__ int slot_swz(int i) {
-  static_assert(kQ >= 1 && kQ <= 16 && (kQ & (kQ - 1)) == 0, "kQ must be a power of two <= 16");
-  constexpr int kShift = kQ == 16 ? 0 : (kQ == 8 ? 1 : (kQ == 4 ? 2 : (kQ == 2 ? 3 : 4)));
-  return (i >> kShift) & (kQ - 1);
-}
-
-template <typename bc_t>
-struct BcStage {
-  static constexpr int kElemsPerSlot = 16 / static_cast<int>(sizeof(bc_t));
-};
-
-// Read lane `lane`'s kT staged values of one row (fp32 or bf16 in LDS) as floats.
-template <int kT, typename bc_t>
-__device__ __forceinline__ void read_staged(const uint4* __restrict__ row, int lane, float (&v)[kT]) {
-  constexpr int kE = BcStage<bc_t>::kElemsPerSlot;
-  constexpr int kQ = kT / kE;
-  const int sw = slot_swz<kQ>(lane);
-#pragma unroll
-  for (int q = 0; q < kQ; ++q) {
-    const uint4 x = row[kQ * lane + (q ^ sw)];
-    if constexpr (sizeof(bc_t) == 4) {
-      v[4 * q + 0] = __uint_as_float(x.x);
-      v[4 * q + 1] = __uint_as_float(x.y);
-      v[4 * q + 2] = __uint_as_float(x.z);
-      v[4 * q + 3] = __uint_as_float(x.w);
-    } else {
-      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[8 * q + 2 * k + 0] = __uint_as_float(w[k] << 16);
-        v[8 * q + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-      }
-    }
-  }
-}
-
 // Stage elements [t0, t0 + 64*kT) of `nrows` rows (B rows of states n0.., then C rows)
 // into dst[row][slot] (64*kT elements of bc_t per row), spread over all threads.
 // Row k of B (C) starts at Bb (Cb) + (n0 + k) * sn.
@@ -132,12 +89,11 @@ __device__ __forceinline__ void stage_round(const bc_t* __restrict__ Bb, const b
   }
 }
 
-__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 template <int kT, int kW, int kNB, bool kZOH, typename io_t, typename bc_t>
 __global__ __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(MSS_FWD_OCC, MSS_FWD_OCC)))
 void fwd_kernel(FwdParams p) {
   constexpr int kChunk = 64 * kT;
+  static_assert(kT % kSegSteps == 0, "lane segments must hold whole carry segments");
   constexpr int kRowSlots = kChunk * static_cast<int>(sizeof(bc_t)) / 16;
   // Two stage buffers as distinct objects, selected statically (rounds run in pairs), so
   // the compiler can tell the in-flight copy into one from the reads of the other.
@@ -210,11 +166,6 @@ void fwd_kernel(FwdParams p) {
         for (int j = 0; j < kT; ++j) zero[j] = 0.f;
         if (p.out) store_seg<kT>(out_row, tl, L, fast, zero);
         if (p.out && p.z && p.y_pre) store_seg<kT>(static_cast<io_t*>(p.y_pre) + row, tl, L, fast, zero);
-        const int cidx = (tl + kT) / kCarryChunk - 1;
-        if (p.carries && ((tl + kT) % kCarryChunk == 0) && cidx < p.n_carry) {
-          for (int n = 0; n < N; ++n)
-            p.carries[(chan * p.n_carry + cidx) * N + n] = s_run[w][n];
-        }
         if (p.ref_states && lane == 63 && ref_idx >= 0) {
           for (int n = 0; n < N; ++n) {
             float* rs = p.ref_states + ((chan * p.n_ref + ref_idx) * N + n) * 2;
@@ -280,20 +231,25 @@ void fwd_kernel(FwdParams p) {
         float h = dpp_mov<kWaveShr1, 0xF>(run, hend);   // carry-in (lane 0: running state)
         {
           float cv[kT];
+          float hseg[kT / kSegSteps];  // state before each kSegSteps-step sub-segment
           read_staged<kT, bc_t>(buf[k][1], lane, cv);
 #pragma unroll
           for (int j = 0; j < kT; ++j) {
+            if (j % kSegSteps == 0) hseg[j / kSegSteps] = h;
             h = __builtin_fmaf(a[j], h, bu[j]);
             y[j] = __builtin_fmaf(cv[j], h, y[j]);
+          }
+          // Residual for the backward: the state entering every kSegSteps-step segment.
+          if (p.carries) {
+            float* crow = p.carries + (chan * N + n) * p.n_seg + tl / kSegSteps;
+#pragma unroll
+            for (int q = 0; q < kT / kSegSteps; ++q)
+              if (tl / kSegSteps + q < p.n_seg) crow[q] = hseg[q];
           }
         }
         const float run_new = readlane(hend, 63);
         if (lane == 0) s_run[w][n] = run_new;
-        // Residuals: state at each 512-step boundary; reference (prod, h) at 2048 ends.
-        if (p.carries && ((tl + kT) % kCarryChunk == 0)) {
-          const int cidx = (tl + kT) / kCarryChunk - 1;
-          if (cidx < p.n_carry) p.carries[(chan * p.n_carry + cidx) * N + n] = hend;
-        }
+        // Reference residual: (prod, h) at 2048-step chunk ends.
         if (p.ref_states && lane == 63 && ref_idx >= 0) {
           float* rs = p.ref_states + ((chan * p.n_ref + ref_idx) * N + n) * 2;
           rs[0] = fast_exp2(a2 * dsum_total);

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 2
+MSS_ABI_VERSION = 3
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -24,7 +24,7 @@ MSS_BF16 = 1
 MSS_EULER = 0
 MSS_ZOH = 1
 MSS_MAX_DSTATE = 16
-MSS_CARRY_CHUNK = 512
+MSS_SEG_STEPS = 8
 MSS_REF_CHUNK = 2048
 
 # Every symbol include/mamba_selective_scan.h declares.

@@ -164,10 +164,11 @@ class _SelectiveScan(torch.autograd.Function):
         lib = register_hip_kernel()
         batch, dim, length = u.shape
         n = A.shape[1]
-        n_carry = (length + _lib.MSS_CARRY_CHUNK - 1) // _lib.MSS_CARRY_CHUNK
+        n_seg = (length + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
         out = _empty_rows(u.shape, io_layout, u.dtype, u.device)
         last = torch.empty(batch, dim, n, device=u.device, dtype=torch.float32)
-        carries = torch.empty(batch, dim, n_carry, n, device=u.device, dtype=torch.float32)
+        # Residual: the state entering every 8-step segment, [B][D][N][ceil(L/8)].
+        carries = torch.empty(batch, dim, n, n_seg, device=u.device, dtype=torch.float32)
         # Pre-gate output: the backward's dz needs it (kept only when z is given).
         y_pre = _empty_rows(u.shape, io_layout, u.dtype, u.device) if z is not None else None
         args = _lib.FwdArgs(

@@ -163,7 +163,7 @@ def check_fused(ts, out, last, fw, g, rtol=F32_RTOL, atol=F32_ATOL):
 
 
 @pytest.mark.parametrize("l", [1, 7, 250, 1024, 1500, 3000])
-@pytest.mark.parametrize("n", [1, 4, 16])
+@pytest.mark.parametrize("n", [1, 4, 11, 16])
 def test_fused_fp32(l, n):
     log(f"case fused fp32 L={l} N={n}")
     x, dout, dlast = fused_case(100 + l + n, 2, 24, l, n)
