@@ -296,12 +296,15 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
         const float An = readlane(a_lane, n);
         const float a2 = An * kLog2e;
         const float mu = s_mu[cl][n];
+        const float dA_old = n_pend >= 0 ? s_dA[cl][n_pend] : 0.f;
         float bv[kT], cg[kT];
         read_staged<kT, bc_t>(stage[n][0], seg, bv);
         read_staged<kT, bc_t>(stage[n][1], seg, cg);
         // This wave owns accumulator row n until the next barrier.
         float* accn = acc_w + n * 2 * kChunk + lane;
-        float a[kT], ah[kT];
+        float a[kT], ah[kT], accB[kT];
+#pragma unroll
+        for (int j = 0; j < kT; ++j) accB[j] = accn[j * 128];  // used by the re-run; fetched early
         {
           float accC[kT];
 #pragma unroll
@@ -333,11 +336,8 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
         if (lane == 63) {
           s_mu[cl][n] = mo;
           if (c == 0 && p.dinit) p.dinit[chan * N + n] = mo;  // d h_{-1} = a_bar_0 * lambda_0
-          if (n_pend >= 0) s_dA[cl][n_pend] += S;
+          if (n_pend >= 0) s_dA[cl][n_pend] = dA_old + S;
         }
-        float accB[kT];
-#pragma unroll
-        for (int j = 0; j < kT; ++j) accB[j] = accn[j * 128];
         lam = m_in + cg[kT - 1];
         float dA_l = 0.f;
 #pragma unroll

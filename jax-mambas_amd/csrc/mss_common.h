@@ -125,14 +125,6 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// log1p(w) for w >= 0 via Goldberg's correction: log(1+w) * w / ((1+w)-1).
-__device__ __forceinline__ float log1p_pos(float w) {
-  const float u = 1.f + w;
-  const float d = u - 1.f;
-  const float l = fast_log2(u) * kLn2;
-  return d == 0.f ? w : l * (w * fast_rcp(d));
-}
-
 // 1 - exp(-x) for x >= 0 (= sigmoid(y) when x = softplus(y)); series below 1/64 keeps
 // the relative error near one ulp where 1 - exp(-x) would cancel.
 __device__ __forceinline__ float one_minus_exp_neg(float x) {
@@ -141,12 +133,18 @@ __device__ __forceinline__ float one_minus_exp_neg(float x) {
   return x < 0.015625f ? series : 1.f - e;
 }
 
-// softplus(x) = log(1 + e^x), identity above 20 (threshold of the reference kernel,
-// native/upstream_mamba/selective_scan_bwd_kernel.cuh:157).
+// softplus(x) = max(x, 0) + log1p(exp(-|x|)), branch-free. With w = exp(-|x|) in (0, 1] and
+// u = fl(1 + w), the rounding error e = w - (u - 1) is exact (Fast2Sum), and
+// log1p(w) = log(u) + log1p(e / u) = log(u) + e * (1 - w) to well below an ulp, so small
+// results keep their relative accuracy (for x << 0, u = 1 and the result is w itself).
+// Above x = 20 the correction is below half an ulp of x: the result is x, the reference
+// kernel's identity branch (native/upstream_mamba/selective_scan_bwd_kernel.cuh:157).
 __device__ __forceinline__ float softplus(float x) {
   const float w = fast_exp2(-fabsf(x) * kLog2e);
-  const float r = fmaxf(x, 0.f) + log1p_pos(w);
-  return x > 20.f ? x : r;
+  const float u = 1.f + w;
+  const float e = w - (u - 1.f);
+  const float l = __builtin_fmaf(fast_log2(u), kLn2, __builtin_fmaf(-e, w, e));
+  return fmaxf(x, 0.f) + l;
 }
 
 __device__ __forceinline__ float sigmoid(float x) {

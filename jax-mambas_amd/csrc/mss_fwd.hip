@@ -18,19 +18,28 @@
 // of two buffers while the previous round is computed (one barrier per round).
 #include "mss_common.h"
 
-// Launch shape (steps per lane, waves per workgroup, states per staging round, waves per
-// SIMD the register allocation targets); overridable at build time for tuning sweeps.
-#ifndef MSS_FWD_T
-#define MSS_FWD_T 16
-#endif
+// Launch shapes. A "wide" shape (16 steps per lane, 4 waves per SIMD) for grids that fill
+// the GPU several times over, and a "narrow" one (8 steps per lane, 6 waves per SIMD: 50%
+// more resident workgroups) for grids that fit in one pass of it, where the wide shape
+// would leave a half-occupied tail pass. Waves per workgroup and states per staging round
+// are shared; all are overridable at build time for tuning sweeps.
 #ifndef MSS_FWD_W
 #define MSS_FWD_W 8
 #endif
 #ifndef MSS_FWD_NB
 #define MSS_FWD_NB 4
 #endif
-#ifndef MSS_FWD_OCC
-#define MSS_FWD_OCC 4
+#ifndef MSS_FWD_T_WIDE
+#define MSS_FWD_T_WIDE 16
+#endif
+#ifndef MSS_FWD_OCC_WIDE
+#define MSS_FWD_OCC_WIDE 4
+#endif
+#ifndef MSS_FWD_T_NARROW
+#define MSS_FWD_T_NARROW 8
+#endif
+#ifndef MSS_FWD_OCC_NARROW
+#define MSS_FWD_OCC_NARROW 6
 #endif
 
 namespace mss {
@@ -89,8 +98,8 @@ __device__ __forceinline__ void stage_round(const bc_t* __restrict__ Bb, const b
   }
 }
 
-template <int kT, int kW, int kNB, bool kZOH, typename io_t, typename bc_t>
-__global__ __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(MSS_FWD_OCC, MSS_FWD_OCC)))
+template <int kT, int kW, int kNB, int kOcc, bool kZOH, typename io_t, typename bc_t>
+__global__ __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(kOcc, kOcc)))
 void fwd_kernel(FwdParams p) {
   constexpr int kChunk = 64 * kT;
   static_assert(kT % kSegSteps == 0, "lane segments must hold whole carry segments");
@@ -291,16 +300,21 @@ void fwd_kernel(FwdParams p) {
   }
 }
 
-template <int kT, int kW, int kNB, bool kZOH, typename io_t, typename bc_t>
+template <int kT, int kW, int kNB, int kOcc, bool kZOH, typename io_t, typename bc_t>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   dim3 grid((p.dim + kW - 1) / kW, p.batch);
-  hipLaunchKernelGGL((fwd_kernel<kT, kW, kNB, kZOH, io_t, bc_t>), grid, dim3(kW * 64), 0, stream, p);
+  hipLaunchKernelGGL((fwd_kernel<kT, kW, kNB, kOcc, kZOH, io_t, bc_t>), grid, dim3(kW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
 template <bool kZOH, typename io_t, typename bc_t>
 static hipError_t launch_fwd_z(const FwdParams& p, hipStream_t stream) {
-  return launch_fwd_t<MSS_FWD_T, MSS_FWD_W, MSS_FWD_NB, kZOH, io_t, bc_t>(p, stream);
+  // Resident workgroups of the narrow shape: 256 CUs * kOcc waves per SIMD * 4 SIMDs / kW.
+  constexpr long long kNarrowSlots = 256LL * MSS_FWD_OCC_NARROW * 4 / MSS_FWD_W;
+  const long long groups = static_cast<long long>(p.batch) * ((p.dim + MSS_FWD_W - 1) / MSS_FWD_W);
+  if (groups <= kNarrowSlots)
+    return launch_fwd_t<MSS_FWD_T_NARROW, MSS_FWD_W, MSS_FWD_NB, MSS_FWD_OCC_NARROW, kZOH, io_t, bc_t>(p, stream);
+  return launch_fwd_t<MSS_FWD_T_WIDE, MSS_FWD_W, MSS_FWD_NB, MSS_FWD_OCC_WIDE, kZOH, io_t, bc_t>(p, stream);
 }
 
 hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream) {

@@ -172,6 +172,18 @@ def test_fused_fp32(l, n):
     check_fused(ts, out, last, fw, g)
 
 
+@pytest.mark.parametrize("zoh", [False, True])
+def test_fused_wide_grid(zoh):
+    """2 x 4096 channels: 1024 forward workgroups, more than one pass of the single-pass
+    launch shape, so the forward takes its 16-step-per-lane shape (the other tests' grids are
+    small); 1100 steps give a full and a ragged chunk of it."""
+    log(f"case fused wide grid zoh={zoh}")
+    x, dout, dlast = fused_case(950 + zoh, 2, 4096, 1100, 16, zoh=zoh)
+    ts, out, last = run_fused(x, dout, dlast, "f32", zoh)
+    fw, g = oracle_fused(x, dout, dlast, zoh)
+    check_fused(ts, out, last, fw, g)
+
+
 @pytest.mark.parametrize("l", [5, 300, 2100])
 def test_fused_zoh(l):
     log(f"case fused zoh L={l}")
