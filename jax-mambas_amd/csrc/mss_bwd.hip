@@ -148,6 +148,7 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
   __shared__ float s_dA[kMaxChanPerBlock][kMaxN];
   __shared__ float s_dD[kMaxChanPerBlock];
   __shared__ float s_db[kMaxChanPerBlock];
+  __shared__ float s_A[kW][kMaxN];  // A row of each wave's current channel
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -234,17 +235,22 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
       const int d = active ? d_raw : p.dim - 1;
       const size_t chan = static_cast<size_t>(b) * p.dim + d;
       const long long row = b * p.io_sb + d * p.io_sd;
-      const float* __restrict__ carry_row = p.carries + chan * N * p.n_seg + seg_idx;
+      // Carries of this channel and chunk: a uniform base per state plus the lane's segment,
+      // so the loads take a scalar base and a fixed per-lane offset (no per-load address
+      // registers for later instructions to wait on).
+      const float* __restrict__ carry_chunk = p.carries + chan * N * p.n_seg + t0 / kT;
 
       // ---- per-step inputs of the row
-      const float a_lane = lane < N ? p.A[static_cast<size_t>(d) * N + lane] : 0.f;
+      // A row through LDS: a global load feeding the state loop would put a wait on all
+      // outstanding loads (the carry prefetch included) inside the loop.
+      if (lane < N) s_A[w][lane] = p.A[static_cast<size_t>(d) * N + lane];
       const float Dv = p.D ? p.D[d] : 0.f;
       const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
       float dlt[kT], dlu[kT], uu[kT], g[kT], s1[kT], s2[kT];
       float ssum = 0.f;
       float hin_next = 0.f;
       if (active) {
-        if (seg_ok) hin_next = carry_row[static_cast<size_t>(wmod) * p.n_seg];
+        if (seg_ok) hin_next = (carry_chunk + static_cast<size_t>(wmod) * p.n_seg)[seg];
         load_seg<kT>(static_cast<const io_t*>(p.delta) + row, tl, L, fast, dlt);
         load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
         load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, fast, g);
@@ -289,17 +295,19 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
         const float hin = hin_next;
         if (active && seg_ok && i + 1 < N) {
           const int nn = n + 1 == N ? 0 : n + 1;
-          hin_next = carry_row[static_cast<size_t>(nn) * p.n_seg];
+          hin_next = (carry_chunk + static_cast<size_t>(nn) * p.n_seg)[seg];
         }
-        __syncthreads();
-        if (!active) continue;
-        const float An = readlane(a_lane, n);
-        const float a2 = An * kLog2e;
-        const float mu = s_mu[cl][n];
-        const float dA_old = n_pend >= 0 ? s_dA[cl][n_pend] : 0.f;
+        // The stage does not change within a chunk: its reads go out before the barrier, so
+        // their latency overlaps the wait.
         float bv[kT], cg[kT];
         read_staged<kT, bc_t>(stage[n][0], seg, bv);
         read_staged<kT, bc_t>(stage[n][1], seg, cg);
+        __syncthreads();
+        if (!active) continue;
+        const float An = s_A[w][n];
+        const float a2 = An * kLog2e;
+        const float mu = s_mu[cl][n];
+        const float dA_old = n_pend >= 0 ? s_dA[cl][n_pend] : 0.f;
         // This wave owns accumulator row n until the next barrier.
         float* accn = acc_w + n * 2 * kChunk + lane;
         float a[kT], ah[kT], accB[kT];
@@ -334,8 +342,7 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
         const float mo = __builtin_fmaf(P, mu, Q);       // message leaving this lane's segment
         const float m_in = dpp_mov<kWaveShr1, 0xF>(mu, mo);  // message entering it
         if (lane == 63) {
-          s_mu[cl][n] = mo;
-          if (c == 0 && p.dinit) p.dinit[chan * N + n] = mo;  // d h_{-1} = a_bar_0 * lambda_0
+          s_mu[cl][n] = mo;  // after chunk 0: d h_{-1} = a_bar_0 * lambda_0 (written below)
           if (n_pend >= 0) s_dA[cl][n_pend] = dA_old + S;
         }
         lam = m_in + cg[kT - 1];
@@ -369,6 +376,7 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
         const float S = wave_sum_to_last(dA_pend);
         if (lane == 63) s_dA[cl][n_pend] += S;
       }
+      if (c == 0 && p.dinit && lane < N) p.dinit[chan * N + lane] = s_mu[cl][lane];
 
       // ---- per-step gradients of the row
       if constexpr (!kZOH) {
