@@ -284,15 +284,6 @@ __device__ __forceinline__ void read_staged(const uint4* __restrict__ row, int l
 
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Workgroup barrier that orders LDS only. __syncthreads() is a full workgroup fence, which on
-// gfx950 also drains every outstanding global load (vmcnt(0)) -- including prefetches meant
-// to stay in flight across the barrier. LDS traffic between waves needs only this.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // ---------------------------------------------------------------------------------
 // Kernel parameter blocks (host fills them after validation).
 struct NormParams {
