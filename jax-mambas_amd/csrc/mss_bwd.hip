@@ -472,16 +472,43 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
   }
 }
 
-// dB/dC[b][n][t] = sum over channel blocks of the partials, fixed order. Partials are
-// [block][b][B|C][n][t] (block stride `stride` floats). grid.y = partial row
-// (b, which, n); threads walk the row's steps, 4 at a time (16-byte loads) when kVec
-// (L a multiple of 4), keeping 4 blocks' loads in flight.
+// One launch finishes every cross-block sum, in a fixed order:
+//   blocks [0, n_bc_blocks): dB/dC[b][n][t] = sum over channel blocks of the partials
+//     ([block][b][B|C][n][t], block stride `stride` floats). The block's row is
+//     blockIdx / x_blocks = (b, which, n); threads walk the row's steps, 4 at a time (16-byte
+//     loads) when kVec (L a multiple of 4), keeping 4 blocks' loads in flight;
+//   the remaining blocks: dA[d][n] = sum_b part_dA[b][d][n]; dD[d], dbias[d] likewise.
 template <bool kVec, typename bc_t>
-__global__ __launch_bounds__(256) void reduce_bc_kernel(const float* __restrict__ part, int n_blk,
-                                                        size_t stride, int L, int N,
-                                                        long long sb, long long sn,
-                                                        bc_t* __restrict__ dB, bc_t* __restrict__ dC) {
-  const int r = blockIdx.y;
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part, int n_blk,
+                                                     size_t stride, int L, int N, int x_blocks,
+                                                     int n_bc_blocks, long long sb, long long sn,
+                                                     bc_t* __restrict__ dB, bc_t* __restrict__ dC,
+                                                     const float* __restrict__ part_dA,
+                                                     const float* __restrict__ part_dD,
+                                                     const float* __restrict__ part_db, int batch,
+                                                     int dim, float* dA, float* dD, float* dbias) {
+  if (static_cast<int>(blockIdx.x) >= n_bc_blocks) {
+    const int dn = dim * N;
+    const int i = (blockIdx.x - n_bc_blocks) * blockDim.x + threadIdx.x;
+    if (i < dn) {
+      float s = 0.f;
+      for (int bb = 0; bb < batch; ++bb) s += part_dA[static_cast<size_t>(bb) * dn + i];
+      dA[i] = s;
+    } else if (i < dn + 2 * dim) {
+      const int which = (i - dn) / dim;
+      const int dd = (i - dn) - which * dim;
+      const float* src = which == 0 ? part_dD : part_db;
+      float* dst = which == 0 ? dD : dbias;
+      if (dst != nullptr) {
+        float s = 0.f;
+        for (int bb = 0; bb < batch; ++bb) s += src[static_cast<size_t>(bb) * dim + dd];
+        dst[dd] = s;
+      }
+    }
+    return;
+  }
+  const int r = blockIdx.x / x_blocks;
+  const int xb = blockIdx.x - r * x_blocks;
   const int bb = r / (2 * N);
   const int rem = r - bb * 2 * N;
   const int which = rem >= N;
@@ -490,7 +517,7 @@ __global__ __launch_bounds__(256) void reduce_bc_kernel(const float* __restrict_
   bc_t* dst = (which ? dC : dB) + bb * sb + n * sn;
   constexpr int kE = kVec ? 4 : 1;
   const int nvec = (L + kE - 1) / kE;
-  for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += gridDim.x * blockDim.x) {
+  for (int v = xb * blockDim.x + threadIdx.x; v < nvec; v += x_blocks * blockDim.x) {
     if constexpr (kVec) {
       const f32x4* src = reinterpret_cast<const f32x4*>(src_row) + v;
       const size_t svec = stride / 4;
@@ -515,32 +542,6 @@ __global__ __launch_bounds__(256) void reduce_bc_kernel(const float* __restrict_
       float s = 0.f;
       for (int k = 0; k < n_blk; ++k) s += src_row[static_cast<size_t>(k) * stride + v];
       store_as(dst + v, s);
-    }
-  }
-}
-
-// dA[d][n] = sum_b part_dA[b][d][n]; dD[d], dbias[d] likewise (fixed order).
-__global__ __launch_bounds__(256) void reduce_small_kernel(const float* __restrict__ part_dA,
-                                                           const float* __restrict__ part_dD,
-                                                           const float* __restrict__ part_db,
-                                                           int batch, int dim, int dstate,
-                                                           float* dA, float* dD, float* dbias) {
-  const int dn = dim * dstate;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dn + 2 * dim;
-       i += gridDim.x * blockDim.x) {
-    if (i < dn) {
-      float s = 0.f;
-      for (int bb = 0; bb < batch; ++bb) s += part_dA[static_cast<size_t>(bb) * dn + i];
-      dA[i] = s;
-    } else {
-      const int which = (i - dn) / dim;
-      const int dd = (i - dn) - which * dim;
-      const float* src = which == 0 ? part_dD : part_db;
-      float* dst = which == 0 ? dD : dbias;
-      if (dst == nullptr) continue;
-      float s = 0.f;
-      for (int bb = 0; bb < batch; ++bb) s += src[static_cast<size_t>(bb) * dim + dd];
-      dst[dd] = s;
     }
   }
 }
@@ -591,23 +592,21 @@ hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB
   const int L = p.seqlen;
   const bool vec = (L % 4) == 0;  // partial rows are 16-byte aligned (block stride: 64 floats)
   const int nvec = vec ? L / 4 : L;
-  const dim3 grid((nvec + 255) / 256, p.batch * 2 * p.dstate);
-#define MSS_REDUCE_BC(VEC, T)                                                                 \
-  hipLaunchKernelGGL((reduce_bc_kernel<VEC, T>), grid, dim3(256), 0, stream, p.part_dBC,       \
-                     p.n_blocks_d, p.part_stride, L, p.dstate, p.bc_sb, p.bc_sn,              \
-                     static_cast<T*>(dB), static_cast<T*>(dC))
-  if (bc_bf16) {
-    if (vec) MSS_REDUCE_BC(true, bf16_t); else MSS_REDUCE_BC(false, bf16_t);
-  } else {
-    if (vec) MSS_REDUCE_BC(true, float); else MSS_REDUCE_BC(false, float);
-  }
-#undef MSS_REDUCE_BC
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  const int x_blocks = (nvec + 255) / 256;
+  const int n_bc_blocks = x_blocks * p.batch * 2 * p.dstate;
   const int small = p.dim * p.dstate + 2 * p.dim;
-  hipLaunchKernelGGL(reduce_small_kernel, dim3((small + 255) / 256), dim3(256), 0, stream, p.part_dA,
-                     p.part_dD, p.part_dbias, p.batch, p.dim, p.dstate, static_cast<float*>(dA), dD,
-                     dbias);
+  const dim3 grid(n_bc_blocks + (small + 255) / 256);
+#define MSS_REDUCE(VEC, T)                                                                       \
+  hipLaunchKernelGGL((reduce_kernel<VEC, T>), grid, dim3(256), 0, stream, p.part_dBC, p.n_blocks_d, \
+                     p.part_stride, L, p.dstate, x_blocks, n_bc_blocks, p.bc_sb, p.bc_sn,          \
+                     static_cast<T*>(dB), static_cast<T*>(dC), p.part_dA, p.part_dD, p.part_dbias,  \
+                     p.batch, p.dim, static_cast<float*>(dA), dD, dbias)
+  if (bc_bf16) {
+    if (vec) MSS_REDUCE(true, bf16_t); else MSS_REDUCE(false, bf16_t);
+  } else {
+    if (vec) MSS_REDUCE(true, float); else MSS_REDUCE(false, float);
+  }
+#undef MSS_REDUCE
   return hipGetLastError();
 }
 
