@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 3
+#define MSS_ABI_VERSION 4
 #define MSS_MAX_DSTATE 16
 #define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
@@ -149,6 +149,25 @@ int mss_bwd(const mss_bwd_args* args, void* stream);
  * lets a caller time or defer the cross-channel reduction.) */
 int mss_bwd_scan(const mss_bwd_args* args, void* stream);
 int mss_bwd_reduce(const mss_bwd_args* args, void* stream);
+
+/* --- Complex-A scan (complex SSM). -------------------------------------------------
+ * Replaces the complex_ssm branch of S6.__call__ (reference mamba/mamba1.py:143-176,
+ * 195-198; no FFI symbol there: it runs as jax.lax.associative_scan over complex64 states
+ * and is differentiated by JAX autodiff). Same argument blocks as mss_fwd / mss_bwd, with
+ * complex tensors stored as interleaved (real, imaginary) float32 pairs (complex64 memory):
+ *   A, dA                                 : [dim][dstate][2]
+ *   initial_state, last_state, dlast_state, dinitial_state : [batch][dim][dstate][2]
+ *   carries                               : [batch][dim][dstate][ceil(seqlen/8)][2]
+ * (A, the state buffers and carries 8-byte aligned). Semantics as at the top of this file
+ * with complex a_bar = exp(delta A), ZOH b_bar = expm1(delta A)/A * B, complex h, and
+ * y_t = sum_n C_nt Re(h_t) + D_d u_t. The reference's A = -exp(A_log.real) + i*A_imag
+ * parameterisation (mamba/mamba1.py:162) is the caller's. Gradients of complex inputs are
+ * (dL/dRe, dL/dIm) of the real loss; dlast_state is read in the same convention.
+ * mss_cbwd allocates its workspace (stream-ordered) when args->workspace is NULL; size
+ * from mss_cbwd_workspace_bytes. dB/dC sums inside one workgroup use a fixed order. */
+size_t mss_cbwd_workspace_bytes(const mss_bwd_args* args);
+int mss_cfwd(const mss_fwd_args* args, void* stream);
+int mss_cbwd(const mss_bwd_args* args, void* stream);
 
 /* --- Causal depthwise conv1d + activation (the Mamba-1 block's short convolution). ---
  * No counterpart symbol in the reference: it runs there as an XLA convolution

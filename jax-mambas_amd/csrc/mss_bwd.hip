@@ -486,9 +486,10 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
                                                      const float* __restrict__ part_dA,
                                                      const float* __restrict__ part_dD,
                                                      const float* __restrict__ part_db, int batch,
-                                                     int dim, float* dA, float* dD, float* dbias) {
+                                                     int dim, int na, float* dA, float* dD,
+                                                     float* dbias) {
   if (static_cast<int>(blockIdx.x) >= n_bc_blocks) {
-    const int dn = dim * N;
+    const int dn = dim * na;  // dA row width: dstate (real A) or 2 * dstate (complex A)
     const int i = (blockIdx.x - n_bc_blocks) * blockDim.x + threadIdx.x;
     if (i < dn) {
       float s = 0.f;
@@ -587,20 +588,20 @@ hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16
                  : launch_bwd_io<float, float>(p, zoh, stream);
 }
 
-hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB, void* dC,
-                             float* dD, float* dbias, hipStream_t stream) {
+hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, void* dA, void* dB,
+                             void* dC, float* dD, float* dbias, hipStream_t stream) {
   const int L = p.seqlen;
   const bool vec = (L % 4) == 0;  // partial rows are 16-byte aligned (block stride: 64 floats)
   const int nvec = vec ? L / 4 : L;
   const int x_blocks = (nvec + 255) / 256;
   const int n_bc_blocks = x_blocks * p.batch * 2 * p.dstate;
-  const int small = p.dim * p.dstate + 2 * p.dim;
+  const int small = p.dim * a_width + 2 * p.dim;
   const dim3 grid(n_bc_blocks + (small + 255) / 256);
 #define MSS_REDUCE(VEC, T)                                                                       \
   hipLaunchKernelGGL((reduce_kernel<VEC, T>), grid, dim3(256), 0, stream, p.part_dBC, p.n_blocks_d, \
                      p.part_stride, L, p.dstate, x_blocks, n_bc_blocks, p.bc_sb, p.bc_sn,          \
                      static_cast<T*>(dB), static_cast<T*>(dC), p.part_dA, p.part_dD, p.part_dbias,  \
-                     p.batch, p.dim, static_cast<float*>(dA), dD, dbias)
+                     p.batch, p.dim, a_width, static_cast<float*>(dA), dD, dbias)
   if (bc_bf16) {
     if (vec) MSS_REDUCE(true, bf16_t); else MSS_REDUCE(false, bf16_t);
   } else {

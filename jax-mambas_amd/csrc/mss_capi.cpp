@@ -20,9 +20,12 @@ namespace mss {
 hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
 hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16,
                            hipStream_t stream);
-hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, void* dA, void* dB, void* dC,
-                             float* dD, float* dbias, hipStream_t stream);
+hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, void* dA, void* dB,
+                             void* dC, float* dD, float* dbias, hipStream_t stream);
 int bwd_chan_per_block(int batch, int dim, int varlen);
+hipError_t launch_cfwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
+hipError_t launch_cbwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
+int cbwd_chan_per_block(int batch, int dim);
 hipError_t launch_conv(const ConvParams& p, bool bwd, bool vec, bool silu, bool io_bf16,
                        hipStream_t stream);
 hipError_t launch_conv_reduce(const ConvParams& p, int n_tiles, float* dw, float* dbias,
@@ -48,6 +51,7 @@ int hip_fail(hipError_t e, const char* what) {
 size_t dtype_size(int dt) { return dt == MSS_BF16 ? 2 : 4; }
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 int check_dims(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate) {
   if (batch <= 0 || dim <= 0 || seqlen <= 0) return MSS_ERR_INVALID_ARGUMENT;
@@ -112,15 +116,18 @@ struct BwdLayout {
   size_t off_dA = 0, off_dD = 0, off_db = 0, total = 0;
 };
 
-BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate, bool varlen) {
+// cplx: the complex-A backward (its own channel blocking; dA partials are complex).
+BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate, bool varlen,
+                     bool cplx = false) {
   BwdLayout l;
-  l.chan_per_block = mss::bwd_chan_per_block(batch, dim, varlen ? 1 : 0);
+  l.chan_per_block = cplx ? mss::cbwd_chan_per_block(batch, dim)
+                          : mss::bwd_chan_per_block(batch, dim, varlen ? 1 : 0);
   l.n_blocks_d = (dim + l.chan_per_block - 1) / l.chan_per_block;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   l.part_stride = (static_cast<size_t>(batch) * 2 * dstate * seqlen + 63) / 64 * 64;
   const size_t bc = static_cast<size_t>(l.n_blocks_d) * l.part_stride * sizeof(float);
   l.off_dA = up(bc);
-  l.off_dD = l.off_dA + up(static_cast<size_t>(batch) * dim * dstate * sizeof(float));
+  l.off_dD = l.off_dA + up(static_cast<size_t>(batch) * dim * dstate * (cplx ? 2 : 1) * sizeof(float));
   l.off_db = l.off_dD + up(static_cast<size_t>(batch) * dim * sizeof(float));
   l.total = l.off_db + up(static_cast<size_t>(batch) * dim * sizeof(float));
   return l;
@@ -152,7 +159,7 @@ int validate_bwd(const mss_bwd_args* a) {
   return resolve_strides(a->strides, a->batch, a->dim, a->seqlen, a->dstate, &st);
 }
 
-int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
+int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream, bool cplx = false) {
   mss::FwdParams p{};
   p.batch = a->batch;
   p.dim = a->dim;
@@ -189,8 +196,10 @@ int run_fwd(const mss_fwd_args* a, float* ref_states, hipStream_t stream) {
   p.carries = a->carries;
   p.ref_states = ref_states;
   p.y_pre = a->z ? a->y_pre : nullptr;
-  const hipError_t e = mss::launch_fwd(p, a->discretization == MSS_ZOH, a->io_dtype == MSS_BF16,
-                                       a->bc_dtype == MSS_BF16, stream);
+  const int zoh = a->discretization == MSS_ZOH;
+  const int io_bf16 = a->io_dtype == MSS_BF16, bc_bf16 = a->bc_dtype == MSS_BF16;
+  const hipError_t e = cplx ? mss::launch_cfwd(p, zoh, io_bf16, bc_bf16, stream)
+                            : mss::launch_fwd(p, zoh, io_bf16, bc_bf16, stream);
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching selective scan forward");
 }
 
@@ -245,8 +254,8 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   return p;
 }
 
-int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream) {
-  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr);
+int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream, bool cplx = false) {
+  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr, cplx);
   char* ws = static_cast<char*>(a->workspace);
   bool owned = false;
   if (ws == nullptr) {
@@ -263,9 +272,12 @@ int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream) {
   const int io_bf16 = a->io_dtype == MSS_BF16;
   const int bc_bf16 = a->bc_dtype == MSS_BF16;
   hipError_t e = hipSuccess;
-  if (phases & kPhaseScan) e = mss::launch_bwd_scan(p, zoh, io_bf16, bc_bf16, stream);
+  if (phases & kPhaseScan)
+    e = cplx ? mss::launch_cbwd_scan(p, zoh, io_bf16, bc_bf16, stream)
+             : mss::launch_bwd_scan(p, zoh, io_bf16, bc_bf16, stream);
   if (e == hipSuccess && (phases & kPhaseReduce))
-    e = mss::launch_bwd_reduce(p, bc_bf16, a->dA, a->dB, a->dC, a->dD, a->ddelta_bias, stream);
+    e = mss::launch_bwd_reduce(p, bc_bf16, a->dstate * (cplx ? 2 : 1), a->dA, a->dB, a->dC, a->dD,
+                               a->ddelta_bias, stream);
   if (owned) {
     const hipError_t f = hipFreeAsync(ws, stream);
     if (e == hipSuccess) e = f;
@@ -368,6 +380,29 @@ int mss_bwd_reduce(const mss_bwd_args* args, void* stream) {
   const int s = validate_bwd(args);
   if (s != MSS_OK) return s;
   return run_bwd(args, kPhaseReduce, static_cast<hipStream_t>(stream));
+}
+
+// Complex A: the same argument blocks with A, dA and every state buffer read as interleaved
+// (real, imaginary) float32 pairs; the carry segments hold complex states, 8-byte aligned.
+size_t mss_cbwd_workspace_bytes(const mss_bwd_args* a) {
+  if (a == nullptr || check_dims(a->batch, a->dim, a->seqlen, a->dstate) != MSS_OK) return 0;
+  return bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr, true).total;
+}
+
+int mss_cfwd(const mss_fwd_args* args, void* stream) {
+  const int s = validate_fwd(args);
+  if (s != MSS_OK) return s;
+  if (!aligned8(args->A) || !aligned8(args->initial_state) || !aligned8(args->last_state) ||
+      !aligned8(args->carries))
+    return MSS_ERR_INVALID_ARGUMENT;
+  return run_fwd(args, nullptr, static_cast<hipStream_t>(stream), true);
+}
+
+int mss_cbwd(const mss_bwd_args* args, void* stream) {
+  const int s = validate_bwd(args);
+  if (s != MSS_OK) return s;
+  if (!aligned8(args->A) || !aligned8(args->carries)) return MSS_ERR_INVALID_ARGUMENT;
+  return run_bwd(args, kPhaseBoth, static_cast<hipStream_t>(stream), true);
 }
 
 size_t mss_conv_bwd_workspace_bytes(const mss_conv_args* a) {

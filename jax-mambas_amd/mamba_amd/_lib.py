@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 3
+MSS_ABI_VERSION = 4
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -34,6 +34,9 @@ EXPORTED_SYMBOLS = (
     "mss_bwd",
     "mss_bwd_scan",
     "mss_bwd_reduce",
+    "mss_cbwd_workspace_bytes",
+    "mss_cfwd",
+    "mss_cbwd",
     "mss_scan_fwd",
     "mss_scan_fwd_repeat",
     "mss_scan_bwd",
@@ -157,11 +160,14 @@ def register_hip_kernel(library_path=None):
     lib.mss_fwd.restype = ctypes.c_int
     lib.mss_bwd.argtypes = [ctypes.POINTER(BwdArgs), _p]
     lib.mss_bwd.restype = ctypes.c_int
-    for name in ("mss_bwd_scan", "mss_bwd_reduce"):
+    for name in ("mss_bwd_scan", "mss_bwd_reduce", "mss_cbwd"):
         getattr(lib, name).argtypes = [ctypes.POINTER(BwdArgs), _p]
         getattr(lib, name).restype = ctypes.c_int
-    lib.mss_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
-    lib.mss_bwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.mss_cfwd.argtypes = [ctypes.POINTER(FwdArgs), _p]
+    lib.mss_cfwd.restype = ctypes.c_int
+    for name in ("mss_bwd_workspace_bytes", "mss_cbwd_workspace_bytes"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(BwdArgs)]
+        getattr(lib, name).restype = ctypes.c_size_t
     lib.mss_scan_fwd.argtypes = [_p, _i32, _i32, _i32, _i32, _i32] + [_p] * 9
     lib.mss_scan_fwd.restype = ctypes.c_int
     lib.mss_scan_fwd_repeat.argtypes = [_p, _i32, _i32, _i32, _i32, _i32, _i32] + [_p] * 9

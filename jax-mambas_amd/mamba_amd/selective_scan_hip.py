@@ -228,17 +228,111 @@ class _SelectiveScan(torch.autograd.Function):
         return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit, None, None, None, None, None
 
 
+class _ComplexSelectiveScan(torch.autograd.Function):
+    """Complex A (mss_cfwd / mss_cbwd): A (D, N), initial and last state (B, D, N) complex64,
+    passed to the kernels as interleaved float32 pairs (torch.view_as_real, no copy)."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh,
+                io_layout, bc_layout):
+        lib = register_hip_kernel()
+        batch, dim, length = u.shape
+        n = A.shape[1]
+        n_seg = (length + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
+        out = _empty_rows(u.shape, io_layout, u.dtype, u.device)
+        last = torch.empty(batch, dim, n, device=u.device, dtype=torch.complex64)
+        carries = torch.empty(batch, dim, n, n_seg, device=u.device, dtype=torch.complex64)
+        y_pre = _empty_rows(u.shape, io_layout, u.dtype, u.device) if z is not None else None
+        rv = lambda t: None if t is None else torch.view_as_real(t).data_ptr()
+        args = _lib.FwdArgs(
+            batch=batch, dim=dim, seqlen=length, dstate=n,
+            discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER,
+            delta_softplus=int(bool(delta_softplus)),
+            io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
+            u=_ptr(u), delta=_ptr(delta), A=rv(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
+            delta_bias=_ptr(delta_bias), initial_state=rv(initial_state), seq_lens=_ptr(seq_lens),
+            out=_ptr(out), last_state=rv(last), carries=rv(carries), y_pre=_ptr(y_pre),
+            strides=_strides(u, io_layout, B, bc_layout),
+        )
+        _lib.check(lib.mss_cfwd(args, _stream(u)), "mss_cfwd")
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre)
+        ctx.delta_softplus = bool(delta_softplus)
+        ctx.zoh = bool(zoh)
+        ctx.layouts = (io_layout, bc_layout)
+        return out, last
+
+    @staticmethod
+    def backward(ctx, dout, dlast):
+        lib = register_hip_kernel()
+        u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre = ctx.saved_tensors
+        batch, dim, length = u.shape
+        n = A.shape[1]
+        io_layout, bc_layout = ctx.layouts
+        if dout is None:
+            dout = torch.zeros_like(u)
+        dout = _conform(dout.to(u.dtype), io_layout)
+        # Torch's gradient of a complex tensor for a real loss is dL/dRe + i dL/dIm: the
+        # convention of the C ABI's complex cotangents and gradients.
+        dlast = None if dlast is None else dlast.to(torch.complex64).contiguous()
+        rv = lambda t: None if t is None else torch.view_as_real(t).data_ptr()
+        du = _empty_rows(u.shape, io_layout, u.dtype, u.device)
+        ddelta = _empty_rows(u.shape, io_layout, u.dtype, u.device)
+        dA = torch.empty_like(A)
+        dB = _empty_rows(B.shape, bc_layout, B.dtype, B.device)
+        dC = _empty_rows(C.shape, bc_layout, C.dtype, C.device)
+        dD = None if D is None else torch.empty_like(D)
+        dz = None if z is None else _empty_rows(u.shape, io_layout, u.dtype, u.device)
+        dbias = None if delta_bias is None else torch.empty_like(delta_bias)
+        dinit = None if initial_state is None else torch.empty_like(initial_state)
+        args = _lib.BwdArgs(
+            batch=batch, dim=dim, seqlen=length, dstate=n,
+            discretization=_lib.MSS_ZOH if ctx.zoh else _lib.MSS_EULER,
+            delta_softplus=int(ctx.delta_softplus),
+            io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
+            u=_ptr(u), delta=_ptr(delta), A=rv(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
+            delta_bias=_ptr(delta_bias), initial_state=rv(initial_state), seq_lens=_ptr(seq_lens),
+            carries=rv(carries), y_pre=_ptr(y_pre), dout=_ptr(dout), dlast_state=rv(dlast),
+            du=_ptr(du), ddelta=_ptr(ddelta), dA=rv(dA), dB=_ptr(dB), dC=_ptr(dC), dD=_ptr(dD),
+            dz=_ptr(dz), ddelta_bias=_ptr(dbias), dinitial_state=rv(dinit),
+            strides=_strides(u, io_layout, B, bc_layout),
+        )
+        ws_bytes = int(lib.mss_cbwd_workspace_bytes(args))
+        ws = torch.empty(ws_bytes, device=u.device, dtype=torch.uint8)
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = ws_bytes
+        _lib.check(lib.mss_cbwd(args, _stream(u)), "mss_cbwd")
+        return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit, None, None, None, None, None
+
+
+def _validate_complex(A, initial_state):
+    if A.dtype != torch.complex64:
+        raise TypeError(f"a complex A must be complex64, got {A.dtype}")
+    if initial_state is not None and initial_state.dtype != torch.complex64:
+        raise TypeError(f"with a complex A, initial_state must be complex64, got {initial_state.dtype}")
+
+
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                       return_last_state=False, initial_state=None, seq_lens=None,
                       discretization="euler"):
-    """Fused selective scan in channel-major layout; see the module docstring."""
-    _validate_fused(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, discretization)
+    """Fused selective scan in channel-major layout; see the module docstring. A complex64 A
+    selects the complex-state scan (the reference's complex_ssm branch,
+    mamba/mamba1.py:160-176, 198): complex states, real output y = sum_n C Re(h) + D u,
+    complex64 initial/last state."""
+    cplx = A.is_complex()
+    if cplx:
+        _validate_complex(A, initial_state)
+        _validate_fused(u, delta, torch.view_as_real(A)[..., 0], B, C, D, z, delta_bias,
+                        None if initial_state is None else torch.view_as_real(initial_state)[..., 0],
+                        seq_lens, discretization)
+    else:
+        _validate_fused(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, discretization)
     register_hip_kernel()
     # Rows of u/delta/z (and B/C) may be batch-outer or channel-outer; the others follow
     # u's (B's) layout, copied only when they differ.
     io_layout = _layout_of(u) or "brl"
     bc_layout = _layout_of(B) or "brl"
-    out, last = _SelectiveScan.apply(
+    fn = _ComplexSelectiveScan if cplx else _SelectiveScan
+    out, last = fn.apply(
         _conform(u, io_layout), _conform(delta, io_layout), A.contiguous(),
         _conform(B, bc_layout), _conform(C, bc_layout),
         _contig(D), _conform(z, io_layout), _contig(delta_bias), _contig(initial_state),

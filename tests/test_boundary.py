@@ -262,3 +262,54 @@ def test_bf16_rounding_matches_torch():
     ours = round_to_bf16(x)
     ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(ours, ref)
+
+
+# Complex-A entry points: the same argument blocks; A, the state buffers and the carries
+# must be 8-byte aligned (interleaved complex64). Only rejected calls run here (no GPU).
+def _aligned(kw, fields):
+    return {f: 64 for f in fields} | kw
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(batch=0), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(dstate=17), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(u=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(discretization=3), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(A=4), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(carries=68), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(last_state=20), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(initial_state=36), _lib.MSS_ERR_INVALID_ARGUMENT),
+])
+def test_complex_fwd_validation(lib, kw, status):
+    args = fwd_args(**_aligned(kw, ("u", "delta", "A", "B", "C", "out")))
+    assert lib.mss_cfwd(args, None) == status
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(carries=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(carries=12), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(A=4), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(D=64), _lib.MSS_ERR_INVALID_ARGUMENT),     # D without dD
+    (dict(z=64), _lib.MSS_ERR_INVALID_ARGUMENT),     # z without dz / y_pre
+    (dict(dstate=17), _lib.MSS_ERR_UNSUPPORTED),
+])
+def test_complex_bwd_validation(lib, kw, status):
+    fields = ("u", "delta", "A", "B", "C", "carries", "dout", "du", "ddelta", "dA", "dB", "dC")
+    assert lib.mss_cbwd(bwd_args(**_aligned(kw, fields)), None) == status
+    assert lib.mss_cfwd(None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_cbwd(None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+
+
+def test_complex_workspace_bytes(lib):
+    assert lib.mss_cbwd_workspace_bytes(None) == 0
+    assert lib.mss_cbwd_workspace_bytes(bwd_args(dstate=17)) == 0
+    real = lib.mss_bwd_workspace_bytes(bwd_args(batch=4, dim=1100, seqlen=64, dstate=4))
+    cplx = lib.mss_cbwd_workspace_bytes(bwd_args(batch=4, dim=1100, seqlen=64, dstate=4))
+    # dB/dC partial rows of every channel block (complex blocks hold 16 channels here) plus
+    # complex dA partials [B][D][N][2] and dD / dbias partials [B][D], each 256-byte padded.
+    up = lambda x: (x + 255) // 256 * 256
+    blocks = (1100 + 15) // 16
+    part = (4 * 2 * 4 * 64 + 63) // 64 * 64
+    want = up(blocks * part * 4) + up(4 * 1100 * 4 * 2 * 4) + 2 * up(4 * 1100 * 4)
+    assert cplx == want
+    assert real > 0
