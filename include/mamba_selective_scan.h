@@ -228,6 +228,12 @@ typedef struct mss_step_args {
 
 int mss_scan_step(const mss_step_args* args, void* stream);
 
+/* mss_scan_step with complex A (the complex branch of S6.step, mamba/mamba1.py:200-214):
+ * A [dim][dstate][2] and state [batch][dim][dstate][2] as interleaved (real, imaginary)
+ * float32 pairs, 8-byte aligned (the complex scan's last_state layout); the state is
+ * updated in place and out = (sum_n C Re(state) + D u) * silu(z). */
+int mss_cscan_step(const mss_step_args* args, void* stream);
+
 /* Causal-conv window update for one token: window = [conv_state[b][d][0..width-2], x];
  * y = act(bias + sum_k weight[d][k] window[k]); conv_state shifts left and takes x.
  * conv_state is [batch][dim][width-1] in the activation dtype, updated in place; x/y use

@@ -26,6 +26,7 @@ int bwd_chan_per_block(int batch, int dim, int varlen);
 hipError_t launch_cfwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
 hipError_t launch_cbwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
 int cbwd_chan_per_block(int batch, int dim);
+hipError_t launch_cssm_step(const StepParams& p, bool zoh, bool io_bf16, bool bc_bf16, hipStream_t stream);
 hipError_t launch_conv(const ConvParams& p, bool bwd, bool vec, bool silu, bool io_bf16,
                        hipStream_t stream);
 hipError_t launch_conv_reduce(const ConvParams& p, int n_tiles, float* dw, float* dbias,
@@ -546,13 +547,15 @@ int mss_xent_bwd(const mss_xent_args* args, void* stream) {
   return s != MSS_OK ? s : run_xent(args, true, static_cast<hipStream_t>(stream));
 }
 
-int mss_scan_step(const mss_step_args* a, void* stream) {
+namespace {
+int run_scan_step(const mss_step_args* a, void* stream, bool cplx) {
   if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
   int s = check_dims(a->batch, a->dim, 1, a->dstate);
   if (s != MSS_OK) return s;
   s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
   if (s != MSS_OK) return s;
   if (!a->state || !a->u || !a->delta || !a->A || !a->B || !a->C || !a->out) return MSS_ERR_INVALID_ARGUMENT;
+  if (cplx && (!aligned8(a->state) || !aligned8(a->A))) return MSS_ERR_INVALID_ARGUMENT;
   Strides st;
   // Rows of one step: the per-row "length" is 1.
   s = resolve_strides(a->strides, a->batch, a->dim, 1, a->dstate, &st);
@@ -576,10 +579,18 @@ int mss_scan_step(const mss_step_args* a, void* stream) {
   p.D = a->D;
   p.delta_bias = a->delta_bias;
   p.out = a->out;
-  const hipError_t e = mss::launch_ssm_step(p, a->discretization == MSS_ZOH, a->io_dtype == MSS_BF16,
-                                            a->bc_dtype == MSS_BF16, static_cast<hipStream_t>(stream));
+  const bool zoh = a->discretization == MSS_ZOH;
+  const bool io_bf16 = a->io_dtype == MSS_BF16, bc_bf16 = a->bc_dtype == MSS_BF16;
+  const hipStream_t st_ = static_cast<hipStream_t>(stream);
+  const hipError_t e = cplx ? mss::launch_cssm_step(p, zoh, io_bf16, bc_bf16, st_)
+                            : mss::launch_ssm_step(p, zoh, io_bf16, bc_bf16, st_);
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching scan step");
 }
+}  // namespace
+
+int mss_scan_step(const mss_step_args* a, void* stream) { return run_scan_step(a, stream, false); }
+
+int mss_cscan_step(const mss_step_args* a, void* stream) { return run_scan_step(a, stream, true); }
 
 int mss_conv_step(const mss_conv_step_args* a, void* stream) {
   if (a == nullptr || a->batch <= 0 || a->dim <= 0) return MSS_ERR_INVALID_ARGUMENT;

@@ -583,6 +583,79 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------------
+// Single-token step with complex A (S6.step's complex branch, mamba/mamba1.py:200-214):
+// state [B][D][N][2] float32 (interleaved complex) updated in place, out = (sum_n C Re(h) +
+// D u) * silu(z). Mapping of the real step: a 16-lane DPP row per (b, d) channel, one lane
+// per state, batch fastest.
+template <bool kZOH, typename io_t, typename bc_t>
+__global__ __launch_bounds__(256) void cssm_step_kernel(StepParams p) {
+  const long long idx = (static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x) >> 4;
+  const int n = threadIdx.x & 15;
+  const bool ch_ok = idx < static_cast<long long>(p.batch) * p.dim;
+  const int b = ch_ok ? static_cast<int>(idx % p.batch) : 0;
+  const int d = ch_ok ? static_cast<int>(idx / p.batch) : 0;
+  const int N = p.dstate;
+  const bool on = ch_ok && n < N;
+  const long long io = b * p.io_sb + d * p.io_sd;
+  float yv = 0.f, u = 0.f;
+  if (ch_ok) {
+    u = to_f32(static_cast<const io_t*>(p.u)[io]);
+    float dt = to_f32(static_cast<const io_t*>(p.delta)[io]) + (p.delta_bias ? p.delta_bias[d] : 0.f);
+    if (p.delta_softplus) dt = softplus(dt);
+    if (on) {
+      const CoefA cf = load_coef(p.A, static_cast<size_t>(d) * N + n);
+      const CExp e = cexp_t(dt, cf);
+      const float s = to_f32(static_cast<const bc_t*>(p.B)[b * p.bc_sb + n * p.bc_sn]) * u;
+      float br, bi;
+      if constexpr (kZOH) {
+        float er, ei;
+        zoh_e(dt, cf, e, er, ei);
+        br = er * s;
+        bi = ei * s;
+      } else {
+        br = dt * s;
+        bi = 0.f;
+      }
+      float2* st = reinterpret_cast<float2*>(p.state) + (static_cast<size_t>(b) * p.dim + d) * N + n;
+      const float2 h = *st;
+      const float ar = e.m * e.cy, ai = e.m * e.sy;
+      const float nr = __builtin_fmaf(ar, h.x, __builtin_fmaf(-ai, h.y, br));
+      const float ni = __builtin_fmaf(ar, h.y, __builtin_fmaf(ai, h.x, bi));
+      *st = make_float2(nr, ni);
+      yv = to_f32(static_cast<const bc_t*>(p.C)[b * p.bc_sb + n * p.bc_sn]) * nr;
+    }
+  }
+  yv += dpp_mov<kRowShr1, 0xF>(0.f, yv);
+  yv += dpp_mov<kRowShr2, 0xF>(0.f, yv);
+  yv += dpp_mov<kRowShr4, 0xF>(0.f, yv);
+  yv += dpp_mov<kRowShr8, 0xF>(0.f, yv);
+  if (ch_ok && n == 15) {
+    float y = yv;
+    if (p.D) y = __builtin_fmaf(p.D[d], u, y);
+    if (p.z) {
+      const float z = to_f32(static_cast<const io_t*>(p.z)[io]);
+      y *= z * sigmoid(z);
+    }
+    store_as(static_cast<io_t*>(p.out) + io, y);
+  }
+}
+
+hipError_t launch_cssm_step(const StepParams& p, bool zoh, bool io_bf16, bool bc_bf16, hipStream_t stream) {
+  const long long n = static_cast<long long>(p.batch) * p.dim * 16;
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256)), block(256);
+#define MSS_CSTEP(Z, IO, BC) hipLaunchKernelGGL((cssm_step_kernel<Z, IO, BC>), grid, block, 0, stream, p)
+  if (zoh) {
+    if (io_bf16) { if (bc_bf16) MSS_CSTEP(true, bf16_t, bf16_t); else MSS_CSTEP(true, bf16_t, float); }
+    else { if (bc_bf16) MSS_CSTEP(true, float, bf16_t); else MSS_CSTEP(true, float, float); }
+  } else {
+    if (io_bf16) { if (bc_bf16) MSS_CSTEP(false, bf16_t, bf16_t); else MSS_CSTEP(false, bf16_t, float); }
+    else { if (bc_bf16) MSS_CSTEP(false, float, bf16_t); else MSS_CSTEP(false, float, float); }
+  }
+#undef MSS_CSTEP
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
 template <bool kZOH, typename io_t, typename bc_t>
 static hipError_t launch_cfwd_t(const FwdParams& p, hipStream_t stream) {
   dim3 grid((p.dim + kCFwdW - 1) / kCFwdW, p.batch);

@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "mss_xent_fwd",
     "mss_xent_bwd",
     "mss_scan_step",
+    "mss_cscan_step",
     "mss_conv_step",
     "mss_strerror",
     "mss_last_hip_error",
@@ -187,8 +188,9 @@ def register_hip_kernel(library_path=None):
     for name in ("mss_xent_fwd", "mss_xent_bwd"):
         getattr(lib, name).argtypes = [ctypes.POINTER(XentArgs), _p]
         getattr(lib, name).restype = ctypes.c_int
-    lib.mss_scan_step.argtypes = [ctypes.POINTER(StepArgs), _p]
-    lib.mss_scan_step.restype = ctypes.c_int
+    for name in ("mss_scan_step", "mss_cscan_step"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(StepArgs), _p]
+        getattr(lib, name).restype = ctypes.c_int
     lib.mss_conv_step.argtypes = [ctypes.POINTER(ConvStepArgs), _p]
     lib.mss_conv_step.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]

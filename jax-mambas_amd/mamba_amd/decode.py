@@ -6,6 +6,8 @@ every (b, d) channel, updating ``state`` (B, D, N) float32 in place (the layout 
 scan's last state, so a prefill hands over directly): S6.step, mamba/mamba1.py:200-214,
 with the scan's fused extras (softplus(delta + bias), D skip, silu(z) gate).
 u/delta/z: (B, D); B/C: (B, N); any strides (e.g. views of (D, B) activation matrices).
+A complex64 A selects the complex-state step (state complex64, the complex scan's last
+state; output sum_n C Re(state) + D u).
 
 ``causal_conv1d_update(conv_state, x, weight, bias=None, activation="silu") -> y`` — the
 conv window step of Mamba.step (:339-363): y = act(bias + sum_k weight[:, k] * window[k])
@@ -33,8 +35,10 @@ def _strides2(t):
 
 def selective_state_update(state, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=True,
                            discretization="euler"):
-    if state.dtype != torch.float32 or state.ndim != 3 or not state.is_contiguous():
-        raise ValueError("state must be a contiguous float32 (B, D, N) tensor")
+    cplx = A.is_complex()
+    sdt, adt = (torch.complex64, torch.complex64) if cplx else (torch.float32, torch.float32)
+    if state.dtype != sdt or state.ndim != 3 or not state.is_contiguous():
+        raise ValueError(f"state must be a contiguous {sdt} (B, D, N) tensor")
     batch, dim, n = state.shape
     if not 1 <= n <= _lib.MSS_MAX_DSTATE:
         raise ValueError(f"N must be between 1 and {_lib.MSS_MAX_DSTATE}")
@@ -46,22 +50,26 @@ def selective_state_update(state, u, delta, A, B, C, D=None, z=None, delta_bias=
     for name, t in (("B", B), ("C", C)):
         if tuple(t.shape) != (batch, n) or t.dtype != B.dtype or t.stride() != B.stride():
             raise ValueError(f"{name} must be ({batch}, {n}) with B's dtype and strides")
-    if A.dtype != torch.float32 or tuple(A.shape) != (dim, n):
-        raise ValueError(f"A must be float32 ({dim}, {n})")
+    if A.dtype != adt or tuple(A.shape) != (dim, n):
+        raise ValueError(f"A must be {adt} ({dim}, {n})")
     _require_gpu(state, u, delta, A, B, C, D, z, delta_bias)
     lib = _lib.register_hip_kernel()
     out = torch.empty_strided(u.shape, u.stride(), dtype=u.dtype, device=u.device)
     io_b, io_d = _strides2(u)
     bc_b, bc_n = _strides2(B)
+    Ac = A.contiguous()  # complex A and state: interleaved (real, imaginary) float32 pairs
     a = _lib.StepArgs(batch=batch, dim=dim, dstate=n,
                       discretization=_lib.MSS_ZOH if discretization == "zoh" else _lib.MSS_EULER,
                       delta_softplus=int(bool(delta_softplus)), io_dtype=_io_tag(u.dtype, "u"),
                       bc_dtype=_io_tag(B.dtype, "B"), state=state.data_ptr(), u=u.data_ptr(),
-                      delta=delta.data_ptr(), A=A.contiguous().data_ptr(), B=B.data_ptr(), C=C.data_ptr(),
+                      delta=delta.data_ptr(), A=Ac.data_ptr(), B=B.data_ptr(), C=C.data_ptr(),
                       D=_ptr(None if D is None else D.contiguous()), z=_ptr(z),
                       delta_bias=_ptr(None if delta_bias is None else delta_bias.contiguous()), out=out.data_ptr(),
                       strides=_lib.Strides(io_batch=io_b, io_dim=io_d, bc_batch=bc_b, bc_state=bc_n))
-    _lib.check(lib.mss_scan_step(a, _stream(u)), "mss_scan_step")
+    if cplx:
+        _lib.check(lib.mss_cscan_step(a, _stream(u)), "mss_cscan_step")
+    else:
+        _lib.check(lib.mss_scan_step(a, _stream(u)), "mss_scan_step")
     return out
 
 

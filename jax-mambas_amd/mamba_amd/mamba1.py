@@ -154,16 +154,28 @@ class S6(nn.Module):
     inverse-softplus bias of a log-uniform dt in [1e-3, 1e-1] (``:79-90``). The three
     reference projections of the input (``s_B``, ``s_C``, ``Linear_R``) are one GEMM here
     (rows [dt | B | C] of ``x_proj``), as in the official Mamba.
+
+    ``complex_ssm=True`` is the reference's complex-state variant (``:38, 47, 162, 170-176,
+    198``): ``A = -exp(A_log) + i*A_imag`` with ``A_log + i*A_imag = log(1/2 - i*n)``
+    (n = 0..N-1), complex states, real output ``sum_n C Re(h) + D u``; the complex scan
+    kernels run it.
     """
 
     def __init__(self, d_inner, d_state=16, dt_rank=None, use_euler_barB_approx=True,
-                 use_D_param=True, device=None):
+                 use_D_param=True, complex_ssm=False, device=None):
         super().__init__()
         self.d_inner, self.d_state = d_inner, d_state
         self.dt_rank = dt_rank if dt_rank is not None else max(1, (d_inner + 15) // 16)
         self.discretization = "euler" if use_euler_barB_approx else "zoh"
-        n = torch.arange(1, d_state + 1, dtype=torch.float32, device=device)
-        self.A_log = nn.Parameter(torch.log(n).repeat(d_inner, 1))
+        self.complex_ssm = complex_ssm
+        if complex_ssm:
+            n = torch.arange(d_state, dtype=torch.float64, device=device)
+            a0 = torch.log(torch.complex(torch.full_like(n, 0.5), -n))
+            self.A_log = nn.Parameter(a0.real.float().repeat(d_inner, 1))
+            self.A_imag = nn.Parameter(a0.imag.float().repeat(d_inner, 1))
+        else:
+            n = torch.arange(1, d_state + 1, dtype=torch.float32, device=device)
+            self.A_log = nn.Parameter(torch.log(n).repeat(d_inner, 1))
         self.D = nn.Parameter(torch.ones(d_inner, device=device)) if use_D_param else None
         self.x_proj = nn.Parameter(torch.empty(self.dt_rank + 2 * d_state, d_inner, device=device))
         _uniform_(self.x_proj, d_inner ** -0.5)
@@ -173,6 +185,11 @@ class S6(nn.Module):
         dt = torch.clamp(torch.exp(log_dt), min=1e-4)
         self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
 
+    def a_matrix(self):
+        """The state matrix: -exp(A_log) (float32), or complex64 -exp(A_log) + i*A_imag."""
+        a = -torch.exp(self.A_log.float())
+        return torch.complex(a, self.A_imag.float()) if self.complex_ssm else a
+
     def forward(self, u, batch, z=None, seq_lens=None, weights=None):
         """u, z: (d_inner, B*L) matrices; returns (d_inner, B*L): (scan(u) + D u) * silu(z).
         `weights` (ShadowWeights) supplies low-precision copies of the projections."""
@@ -180,7 +197,7 @@ class S6(nn.Module):
         weights = weights or _PLAIN
         x_dbl = weights.mm(self.x_proj, u)                      # (R + 2N, B*L)
         dt = weights.mm(self.dt_proj, x_dbl[:r])                # (d_inner, B*L), bias fused below
-        A = -torch.exp(self.A_log.float())
+        A = self.a_matrix()
         y, last = selective_scan_fn(
             _rows(u, batch), _rows(dt, batch), A, _rows(x_dbl[r:r + n], batch),
             _rows(x_dbl[r + n:], batch), D=None if self.D is None else self.D.float(),
@@ -192,12 +209,12 @@ class S6(nn.Module):
 
     def step(self, u, z, state, weights=None, A=None):
         """One token: u, z (d_inner, B) matrices; state (B, d_inner, N) updated in place.
-        A: -exp(A_log) computed once per generation (recomputed when None)."""
+        A: the state matrix computed once per generation (recomputed when None)."""
         r, n = self.dt_rank, self.d_state
         weights = weights or _PLAIN
         x_dbl = weights.mm(self.x_proj, u)
         dt = weights.mm(self.dt_proj, x_dbl[:r])
-        A = -torch.exp(self.A_log.float()) if A is None else A
+        A = self.a_matrix() if A is None else A
         y = selective_state_update(
             state, u.t(), dt.t(), A, x_dbl[r:r + n].t(), x_dbl[r + n:].t(),
             D=None if self.D is None else self.D.float(), z=None if z is None else z.t(),
@@ -213,7 +230,7 @@ class MambaBlock(nn.Module):
     + silu -> S6 with D skip -> * silu(z) -> out-projection -> + residual."""
 
     def __init__(self, d_model, expand=2, d_state=16, dt_rank=None, d_conv=4, n_layers=1,
-                 norm="rmsnorm", use_euler_barB_approx=True, device=None):
+                 norm="rmsnorm", use_euler_barB_approx=True, complex_ssm=False, device=None):
         super().__init__()
         d_inner = d_model * expand
         dt_rank = dt_rank if dt_rank is not None else max(1, (d_model + 15) // 16)  # from d_model
@@ -224,7 +241,8 @@ class MambaBlock(nn.Module):
         self.z_proj = nn.Parameter(_uniform_(torch.empty(d_inner, d_model, device=device), d_model ** -0.5))
         self.conv_weight = nn.Parameter(_uniform_(torch.empty(d_inner, d_conv, device=device), d_conv ** -0.5))
         self.conv_bias = nn.Parameter(_uniform_(torch.empty(d_inner, device=device), d_conv ** -0.5))
-        self.s6 = S6(d_inner, d_state, dt_rank, use_euler_barB_approx=use_euler_barB_approx, device=device)
+        self.s6 = S6(d_inner, d_state, dt_rank, use_euler_barB_approx=use_euler_barB_approx,
+                     complex_ssm=complex_ssm, device=device)
         self.out_proj = nn.Parameter(_uniform_(torch.empty(d_model, d_inner, device=device),
                                                d_inner ** -0.5 * n_layers ** -0.5))
 
@@ -248,7 +266,7 @@ class MambaBlock(nn.Module):
             conv = torch.zeros(batch, xin.shape[0], k - 1, dtype=xin.dtype, device=xin.device)
             if k > 1:
                 conv[:, :, conv.shape[2] - tail.shape[2]:] = tail
-            self.cache = {"conv": conv, "ssm": self.s6.last_state, "A": -torch.exp(self.s6.A_log.float())}
+            self.cache = {"conv": conv, "ssm": self.s6.last_state, "A": self.s6.a_matrix()}
         return h, weights.mm(self.out_proj, y)
 
     def step(self, h, delta, cache, act_dtype=torch.bfloat16, weights=None):
@@ -267,12 +285,13 @@ class MambaLM(nn.Module):
     """Stacked Mamba-1 language model: embedding -> blocks -> RMSNorm -> tied head."""
 
     def __init__(self, vocab, d_model, n_layers, expand=2, d_state=16, dt_rank=None, d_conv=4,
-                 use_euler_barB_approx=True, device=None):
+                 use_euler_barB_approx=True, complex_ssm=False, device=None):
         super().__init__()
         self.embedding = nn.Parameter(torch.randn(vocab, d_model, device=device) * 0.02)
         self.blocks = nn.ModuleList(
             MambaBlock(d_model, expand, d_state, dt_rank, d_conv, n_layers,
-                       use_euler_barB_approx=use_euler_barB_approx, device=device)
+                       use_euler_barB_approx=use_euler_barB_approx, complex_ssm=complex_ssm,
+                       device=device)
             for _ in range(n_layers))
         self.final_norm = RMSNormCM(d_model, device=device)
         self._shadows = ShadowWeights([self.embedding] + [w for b in self.blocks for w in b.gemm_weights()])

@@ -6,7 +6,7 @@ dtype (tests use float64 on the CPU), differentiable through torch autograd:
 * ``S6.__call__`` — ``mamba/mamba1.py:160-198``: ``A = -exp(A_log)``; B, C and the
   low-rank delta from linear maps of the input; ``delta = softplus(dt_proj(.) + bias)``;
   scan (``oracle/assoc_torch.py``, the reference's ``selective_scan_reference``);
-  ``y += D * u``.
+  ``y += D * u``. With an ``A_imag`` parameter, the complex_ssm branch (``:143-176, 198``).
 * ``Mamba.__call__`` — ``mamba/mamba1.py:300-337``: norm, two up-projections, causal
   depthwise conv (``nnx.Conv(..., feature_group_count=D, padding="CAUSAL")``,
   ``:250-255``: out[t] = bias + sum_k w[k] x[t - (K-1) + k]) + silu, S6, times
@@ -23,7 +23,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from .assoc_torch import selective_scan_reference
+from .assoc_torch import _compose, associative_scan, selective_scan_reference
 
 
 def rmsnorm(x, weight, eps=1e-5):
@@ -41,10 +41,30 @@ def causal_depthwise_conv(x, weight, bias):
     return out
 
 
+def complex_s6_scan(A, deltas, Bs, Cs, x, euler=True):
+    """The complex_ssm branch of S6.__call__ (``mamba/mamba1.py:143-158, 170-176``):
+    complex discretisation, associative scan of (a_bar, b_bar x) from a zero state,
+    ``einsum("bln,bldn->bld", C, states)``; returns (complex y (B, L, D), last state)."""
+    ctype = A.dtype
+    mul = torch.einsum("bld,dn->bldn", deltas.to(ctype), A)
+    a_bars = torch.exp(mul)
+    if euler:
+        b_bars = torch.einsum("bld,bln->bldn", deltas.to(ctype), Bs.to(ctype))
+    else:
+        b_bars = (torch.expm1(mul) / A[None, None]) * Bs.to(ctype)[:, :, None, :]
+    bx = b_bars * x.to(ctype)[..., None]
+    _, states = associative_scan(_compose, (a_bars, bx), dim=1)
+    return torch.einsum("bln,bldn->bld", Cs.to(ctype), states), states[:, -1]
+
+
 def s6(p, prefix, u, dt_rank, d_state, euler=True):
     x_dbl = u @ p[prefix + "x_proj"].t()
     r, n = dt_rank, d_state
     delta = F.softplus(x_dbl[..., :r] @ p[prefix + "dt_proj"].t() + p[prefix + "dt_bias"])
+    if prefix + "A_imag" in p:  # complex SSM: A = -exp(A.real) + i A.imag (:162), y.real (:198)
+        A = torch.complex(-torch.exp(p[prefix + "A_log"]), p[prefix + "A_imag"])
+        y, _ = complex_s6_scan(A, delta, x_dbl[..., r:r + n], x_dbl[..., r + n:], u, euler)
+        return (y + p[prefix + "D"] * u).real
     A = -torch.exp(p[prefix + "A_log"])
     y, _ = selective_scan_reference(A, delta, x_dbl[..., r:r + n], x_dbl[..., r + n:], u,
                                     use_euler_barB_approx=euler)

@@ -15,7 +15,7 @@ from mamba_amd import _lib
 from mamba_amd.decode import causal_conv1d_update, selective_state_update
 from mamba_amd.mamba1 import MambaLM
 from oracle import mamba1_torch as ref
-from oracle import scan64
+from oracle import cscan64, scan64
 
 
 @pytest.fixture(scope="module")
@@ -32,6 +32,16 @@ def test_step_validation(lib, kw, status):
     base = dict(batch=2, dim=3, dstate=4, state=1, u=1, delta=1, A=1, B=1, C=1, out=1)
     base.update(kw)
     assert lib.mss_scan_step(_lib.StepArgs(**base), None) == status
+    # complex step: same checks, with 8-byte aligned A and state
+    base.update(state=64 if base["state"] else None, A=64)
+    assert lib.mss_cscan_step(_lib.StepArgs(**base), None) == status
+
+
+@pytest.mark.parametrize("kw", [dict(state=68), dict(A=4)])
+def test_complex_step_alignment(lib, kw):
+    base = dict(batch=2, dim=3, dstate=4, state=64, u=64, delta=64, A=64, B=64, C=64, out=64)
+    base.update(kw)
+    assert lib.mss_cscan_step(_lib.StepArgs(**base), None) == _lib.MSS_ERR_INVALID_ARGUMENT
 
 
 @pytest.mark.parametrize("kw", [dict(width=0), dict(width=5), dict(conv_state=None), dict(x=None),
@@ -77,6 +87,32 @@ def test_state_update_steps_match_oracle_scan(zoh, layout):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("zoh", [False, True])
+def test_complex_state_update_steps_match_oracle_scan(zoh):
+    print(f"case complex state update zoh={zoh}", flush=True)
+    rng = np.random.default_rng(12)
+    b, d, n, steps = 3, 40, 16, 6
+    f = np.float32
+    u, dr, z = (rng.standard_normal((b, d, steps)).astype(f) for _ in range(3))
+    Bm, Cm = (rng.standard_normal((b, n, steps)).astype(f) for _ in range(2))
+    A = (-np.exp(rng.standard_normal((d, n))) + 2j * rng.standard_normal((d, n))).astype(np.complex64)
+    D = rng.standard_normal(d).astype(f)
+    bias = (0.5 * rng.standard_normal(d) - 2.0).astype(f)
+    x0 = (rng.standard_normal((b, d, n)) + 1j * rng.standard_normal((b, d, n))).astype(np.complex64)
+    fw = cscan64.forward(u, dr, A, Bm, Cm, D=D, z=z, delta_bias=bias, delta_softplus=True, initial_state=x0,
+                         discretization="zoh" if zoh else "euler")
+    cu = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    state = cu(x0)
+    for t in range(steps):
+        out = selective_state_update(state, cu(u[:, :, t]), cu(dr[:, :, t]), cu(A), cu(Bm[:, :, t]),
+                                     cu(Cm[:, :, t]), D=cu(D), z=cu(z[:, :, t]), delta_bias=cu(bias),
+                                     discretization="zoh" if zoh else "euler")
+        torch.testing.assert_close(out.double().cpu(), torch.from_numpy(fw["out"][:, :, t]), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(state.cpu().to(torch.complex128), torch.from_numpy(fw["last_state"]),
+                               rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("k", [2, 4])
 def test_conv_update_matches_full_conv(k):
     print(f"case conv update k={k}", flush=True)
@@ -93,11 +129,12 @@ def test_conv_update_matches_full_conv(k):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("euler", [True, False])
-def test_prefill_and_steps_match_full_forward(euler):
-    print(f"case prefill + steps euler={euler}", flush=True)
+@pytest.mark.parametrize("euler,complex_ssm", [(True, False), (False, False), (True, True), (False, True)])
+def test_prefill_and_steps_match_full_forward(euler, complex_ssm):
+    print(f"case prefill + steps euler={euler} complex_ssm={complex_ssm}", flush=True)
     torch.manual_seed(5)
-    model = MambaLM(16, 64, 2, 2, 16, None, 4, use_euler_barB_approx=euler, device="cuda")
+    model = MambaLM(16, 64, 2, 2, 16, None, 4, use_euler_barB_approx=euler, complex_ssm=complex_ssm,
+                    device="cuda")
     g = torch.Generator().manual_seed(6)
     b, prompt, steps = 3, 37, 6
     tokens = torch.randint(0, 16, (b, prompt + steps), generator=g).cuda()

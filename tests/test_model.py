@@ -13,7 +13,7 @@ import torch.nn.functional as F
 
 from mamba_amd.mamba1 import GraphedTrainStep, MambaLM
 from oracle import mamba1_torch as ref
-from oracle import scan64
+from oracle import cscan64, scan64
 
 C1 = dict(vocab=16, d_model=64, n_layers=2, expand=2, d_state=16, d_conv=4, batch=8, length=256)
 
@@ -38,9 +38,9 @@ def test_oracle_rmsnorm_matches_torch():
     torch.testing.assert_close(ref.rmsnorm(x, w), F.rms_norm(x, (32,), w, eps=1e-5))
 
 
-def small_params(d_model=8, expand=2, d_state=4, dt_rank=2, vocab=11, n_layers=2, seed=0):
+def small_params(d_model=8, expand=2, d_state=4, dt_rank=2, vocab=11, n_layers=2, seed=0, complex_ssm=False):
     torch.manual_seed(seed)
-    m = MambaLM(vocab, d_model, n_layers, expand, d_state, dt_rank, 4)
+    m = MambaLM(vocab, d_model, n_layers, expand, d_state, dt_rank, 4, complex_ssm=complex_ssm)
     return {k: v.detach().double() for k, v in m.state_dict().items()}, m
 
 
@@ -58,6 +58,37 @@ def test_oracle_s6_matches_scan64(euler):
                         sw(x_dbl[..., 6:]), D=p[pre + "D"].numpy(), delta_bias=p[pre + "dt_bias"].numpy(),
                         delta_softplus=True, discretization="euler" if euler else "zoh")
     np.testing.assert_allclose(got.numpy(), np.swapaxes(fw["out"], 1, 2), rtol=1e-9, atol=1e-12)
+
+
+@pytest.mark.parametrize("euler", [True, False])
+def test_oracle_complex_s6_matches_cscan64(euler):
+    """The oracle model's complex branch (associative scan, mamba/mamba1.py:170-176) against the
+    sequential complex oracle, with the reference's complex A initialisation perturbed."""
+    p, _ = small_params(complex_ssm=True)
+    pre = "blocks.0.s6."
+    rng = np.random.default_rng(3)
+    p[pre + "A_imag"] = p[pre + "A_imag"] + torch.from_numpy(rng.standard_normal(p[pre + "A_imag"].shape))
+    u = torch.from_numpy(rng.standard_normal((2, 30, 16)))
+    got = ref.s6(p, pre, u, 2, 4, euler)
+    x_dbl = (u @ p[pre + "x_proj"].t()).numpy()
+    dt_raw = x_dbl[..., :2] @ p[pre + "dt_proj"].t().numpy()
+    sw = lambda a: np.ascontiguousarray(np.swapaxes(a, 1, 2))
+    A = -np.exp(p[pre + "A_log"].numpy()) + 1j * p[pre + "A_imag"].numpy()
+    fw = cscan64.forward(sw(u.numpy()), sw(dt_raw), A, sw(x_dbl[..., 2:6]), sw(x_dbl[..., 6:]),
+                         D=p[pre + "D"].numpy(), delta_bias=p[pre + "dt_bias"].numpy(),
+                         delta_softplus=True, discretization="euler" if euler else "zoh")
+    np.testing.assert_allclose(got.numpy(), np.swapaxes(fw["out"], 1, 2), rtol=1e-9, atol=1e-12)
+
+
+def test_complex_parameter_initialisation_follows_reference():
+    """A_log + i A_imag = log(1/2 - i n), n = 0..N-1 (mamba/mamba1.py:47), so
+    A = -exp(A_log) + i A_imag = -|1/2 - i n| + i atan2(-n, 1/2) (:162)."""
+    _, m = small_params(d_model=16, d_state=16, complex_ssm=True)
+    a = m.blocks[1].s6.a_matrix().detach()
+    assert a.dtype == torch.complex64 and a.shape == (32, 16)
+    n = np.arange(16)
+    want = -np.sqrt(0.25 + n ** 2) + 1j * np.arctan2(-n, 0.5)
+    np.testing.assert_allclose(a[5].numpy(), want, rtol=1e-6)
 
 
 def test_oracle_block_gate_matches_scan64_gate():
@@ -91,14 +122,14 @@ def test_parameter_initialisation_follows_reference():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("euler", [True, False])
-def test_model_matches_oracle_on_gpu(euler):
-    print(f"case model c1 euler={euler}", flush=True)
+@pytest.mark.parametrize("euler,complex_ssm", [(True, False), (False, False), (True, True), (False, True)])
+def test_model_matches_oracle_on_gpu(euler, complex_ssm):
+    print(f"case model c1 euler={euler} complex_ssm={complex_ssm}", flush=True)
     torch.manual_seed(0)
     cfg = C1
     dev = "cuda"
     model = MambaLM(cfg["vocab"], cfg["d_model"], cfg["n_layers"], cfg["expand"], cfg["d_state"], None,
-                    cfg["d_conv"], use_euler_barB_approx=euler, device=dev)
+                    cfg["d_conv"], use_euler_barB_approx=euler, complex_ssm=complex_ssm, device=dev)
     g = torch.Generator().manual_seed(0)
     tokens = torch.randint(0, cfg["vocab"], (cfg["batch"], cfg["length"]), generator=g)
     targets = torch.roll(tokens, -1, dims=1).reshape(-1)
