@@ -20,6 +20,9 @@ Fields beyond the driver contract:
   train_c5      the metric's second half: tokens/s of one training step of the Mamba-1
                 130M-shape LM (config 5) through the HIP scan
   decode_c5     single-token decode of the same model after a 2048-token prefill
+  complex_c2    the complex-A scan (mss_cfwd + mss_cbwd) at the config-2 shape with the
+                reference's complex A initialisation, and a CPU baseline of the reference's
+                complex path (torch restatement of mamba/mamba1.py:143-176)
 Inputs are drawn on the GPU from each config's recipe (seeded torch generator).
 """
 from __future__ import annotations
@@ -179,6 +182,115 @@ def scan_report(cfg, r):
         rep["seq_lens"] = [int(x) for x in lens]
         rep["valid_fraction"] = round(float(np.sum(lens)) / (cfg.batch * cfg.length), 4)
     return rep
+
+
+def complex_a(torch, d, n, device):
+    """The reference's complex A: -exp(Re log(1/2 - i n)) + i Im log(1/2 - i n), n < N
+    (mamba/mamba1.py:47, 162), the same row for every channel."""
+    k = torch.arange(n, dtype=torch.float64)
+    a_log = torch.log(torch.complex(torch.full_like(k, 0.5), -k))
+    a = torch.complex(-torch.exp(a_log.real), a_log.imag).to(torch.complex64)
+    return a.repeat(d, 1).to(device)
+
+
+def run_complex_c2(torch, steps, warmup):
+    """Complex-A scan fwd + bwd (mss_cfwd, mss_cbwd) on the config-2 inputs and shape."""
+    from mamba_amd import _lib
+    from mamba_amd.configs import C2, algorithmic_bytes
+
+    cfg = C2
+    lib, t, fa, ba, _ = gpu_step_setup(torch, cfg)
+    b, d, l, n = cfg.batch, cfg.dim, cfg.length, cfg.dstate
+    n_seg = (l + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
+    rv = lambda x: torch.view_as_real(x).data_ptr()
+    t["cA"] = complex_a(torch, d, n, "cuda")
+    t["cdA"] = torch.empty_like(t["cA"])
+    t["clast"] = torch.empty(b, d, n, dtype=torch.complex64, device="cuda")
+    t["cdlast"] = torch.zeros(b, d, n, dtype=torch.complex64, device="cuda")
+    t["ccarries"] = torch.empty(b, d, n, n_seg, dtype=torch.complex64, device="cuda")
+    fa.A, fa.last_state, fa.carries = rv(t["cA"]), rv(t["clast"]), rv(t["ccarries"])
+    ba.A, ba.carries, ba.dlast_state, ba.dA = rv(t["cA"]), rv(t["ccarries"]), rv(t["cdlast"]), rv(t["cdA"])
+    ws_bytes = int(lib.mss_cbwd_workspace_bytes(ba))
+    t["cws"] = torch.empty(ws_bytes, device="cuda", dtype=torch.uint8)
+    ba.workspace, ba.workspace_bytes = t["cws"].data_ptr(), ws_bytes
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(evs=None):
+        if evs:
+            evs[0].record(stream)
+        _lib.check(lib.mss_cfwd(fa, sp), "mss_cfwd")
+        if evs:
+            evs[1].record(stream)
+        _lib.check(lib.mss_cbwd(ba, sp), "mss_cbwd")
+        if evs:
+            evs[2].record(stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    fwd = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    bwd = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    log(f"[bench] complex c2: fwd {fwd:.4f} ms, bwd {bwd:.4f} ms")
+    # Algorithmic bytes of the real scan plus the complex parts of A, dA and the states.
+    fwd_b, bwd_b = algorithmic_bytes(cfg)
+    fwd_b += 4 * (d * n + b * d * n)
+    bwd_b += 4 * (2 * d * n + b * d * n)
+    tokens = b * l
+    frac = lambda nbytes, ms: round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    del t
+    torch.cuda.empty_cache()
+    return {"workload": "complex-A selective_scan fp32 B=4 D=1536 L=2048 N=16, reference complex A init, "
+                        "softplus(delta+bias), D skip, silu(z) gate",
+            "ms_fwd": round(fwd, 5), "ms_bwd": round(bwd, 5), "ms_fwd_bwd": round(fwd + bwd, 5),
+            "tokens_per_s": round(tokens / ((fwd + bwd) * 1e-3), 1),
+            "hbm_frac": {"fwd": frac(fwd_b, fwd), "bwd": frac(bwd_b, bwd)}}
+
+
+def cpu_baseline_complex(torch, target_s, d0=8):
+    """The reference's complex path on the CPU (oracle/mamba1_torch.complex_s6_scan:
+    mamba/mamba1.py:143-176, associative scan over complex64 states) with the config-2
+    fusions, forward + autograd backward, timed on a channel slice and scaled."""
+    from mamba_amd.configs import C2, ScanConfig, make_scan_inputs
+    from oracle.mamba1_torch import complex_s6_scan
+
+    cfg = C2
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+
+    def run(dslice):
+        sub = ScanConfig("slice", cfg.batch, dslice, cfg.length, cfg.dstate, cfg.dtype)
+        x = make_scan_inputs(sub, seed=0, with_z=True, with_dout=True)
+        tr = lambda a: torch.from_numpy(np.ascontiguousarray(np.swapaxes(a, 1, 2))).requires_grad_(True)
+        u, dr, z, Bs, Cs = (tr(x[k]) for k in ("u", "delta", "z", "B", "C"))
+        dout = torch.from_numpy(np.ascontiguousarray(np.swapaxes(x["dout"], 1, 2)))
+        A = complex_a(torch, dslice, cfg.dstate, "cpu").requires_grad_(True)
+        bias = torch.from_numpy(x["delta_bias"]).requires_grad_(True)
+        D = torch.from_numpy(x["D"]).requires_grad_(True)
+        t0 = time.perf_counter()
+        deltas = torch.nn.functional.softplus(dr + bias)
+        y, _ = complex_s6_scan(A, deltas, Bs, Cs, u)
+        out = (y.real + D * u) * torch.nn.functional.silu(z)
+        (out * dout).sum().backward()
+        return time.perf_counter() - t0
+
+    run(d0)
+    t_probe = run(d0)
+    dslice = max(8, int(np.clip(d0 * (target_s / 4.0) / max(t_probe, 1e-3), d0, cfg.dim)) // 8 * 8)
+    if dslice != d0:
+        run(dslice)
+    times = [run(dslice) for _ in range(3)]
+    t_med = float(np.median(times))
+    t_full = t_med * cfg.dim / dslice
+    log(f"[bench] complex c2 cpu baseline: D={dslice} median {t_med:.2f} s")
+    return {"value": cfg.batch * cfg.length / t_full, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"complex c2: B={cfg.batch} L={cfg.length} N={cfg.dstate} complex64 states, {dslice} of "
+                       f"{cfg.dim} channels, fwd+bwd (autograd) median of 3 = {t_med:.3f} s, scaled "
+                       f"x{cfg.dim / dslice:.1f} ({t_full:.2f} s per step)")}
 
 
 C5_MODEL = dict(vocab=50280, d_model=768, n_layers=24, expand=2, d_state=16, dt_rank=48, d_conv=4)
@@ -390,6 +502,8 @@ def main():
     ap.add_argument("--train-warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=50,
                     help="timed single-token decode steps of the config-5 model (0 skips them)")
+    ap.add_argument("--complex-steps", type=int, default=10,
+                    help="timed steps of the complex-A scan at the config-2 shape (0 skips them)")
     ap.add_argument("--train-eager", action="store_true",
                     help="time the config-5 step eagerly only (no HIP graph capture)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -444,6 +558,9 @@ def main():
     decode = None
     if args.decode_steps > 0:
         decode = run_decode_c5(torch, args.decode_steps, graph=not args.train_eager)
+    cplx = None
+    if args.complex_steps > 0:
+        cplx = run_complex_c2(torch, args.complex_steps, max(1, args.complex_steps // 4))
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, cfg, args.cpu_seconds)
@@ -451,6 +568,8 @@ def main():
         for name in others:
             per_config[name]["cpu_baseline"] = cpu_baseline(torch, CONFIGS[name], args.cpu_seconds / 2,
                                                             results[name]["lens"], d0=8)
+        if cplx is not None:
+            cplx["cpu_baseline"] = cpu_baseline_complex(torch, args.cpu_seconds / 2)
     step_bytes = fwd_bytes + bwd_bytes
     result = {
         "metric": METRIC,
@@ -475,6 +594,7 @@ def main():
         "configs": per_config,
         "train_c5": train,
         "decode_c5": decode,
+        "complex_c2": cplx,
     }
     print(json.dumps(result), flush=True)
 
