@@ -15,7 +15,7 @@
 // segment, a wave pass covers a 512-step chunk, and segments are joined by a 64-lane
 // inclusive scan of complex affine maps on DPP lane shifts. exp(delta*A) is
 // exp2(delta*Re(A)*log2(e)) * (cos, sin)(delta*Im(A)), the angle taken in turns
-// (delta*Im(A)/2pi) and reduced exactly to a quarter turn before the polynomials.
+// (delta*Im(A)/2pi) for the hardware sine and cosine.
 #include "mss_common.h"
 
 namespace mss {
@@ -23,11 +23,11 @@ namespace mss {
 constexpr int kCT = kSegSteps;     // steps per lane: one carry segment
 constexpr int kCChunk = 64 * kCT;  // steps per wave pass
 constexpr int kCFwdW = 4;          // waves (channels) per forward workgroup
-constexpr int kCBwdW = 8;          // waves per backward workgroup
-constexpr int kCMaxChan = 32;      // channels one backward workgroup walks, at most
+constexpr int kCBwdW = 12;         // waves per backward workgroup (3 per SIMD, one per CU)
+constexpr int kCMaxChan = 48;      // channels one backward workgroup walks, at most
 // dB/dC accumulator rows of the backward: ceil(kCBwdW/N) copies of each state's row, so
-// waves never share a row within one state iteration (at most 16 for every N <= 16).
-constexpr int kCAccRows = 16;
+// waves never share a row within one state iteration; the most over N <= 16 is 22 (N = 11).
+constexpr int kCAccRows = 22;
 constexpr float kInv2Pi = 0.15915494309189535f;
 
 // Constants of exp(t * A) for one (channel, state).
@@ -48,41 +48,20 @@ __device__ __forceinline__ CoefA load_coef(const float* __restrict__ A, size_t i
   return c;
 }
 
-// sin and cos of 2*pi*r. r is reduced to the nearest quarter turn, k = rint(4r), with
-// f = r - k/4 exact (|f| <= 1/8, a multiple of r's ulp), so only the rounding of r itself
-// and of x = 2*pi*f reach the angle. On |x| <= pi/4 the Taylor polynomials of sin
-// (through x^9) and cos (through x^10) are within 3e-9 of the functions; the quadrant
-// k mod 4 then swaps and negates them.
-__device__ __forceinline__ void sincos_rev(float r, float& sn, float& cs) {
-  const float k = __builtin_rintf(4.f * r);
-  const float f = __builtin_fmaf(-0.25f, k, r);
-  const float x = f * 6.28318530717958648f;
-  const float x2 = x * x;
-  float sp = __builtin_fmaf(x2, 1.f / 362880.f, -1.f / 5040.f);
-  sp = __builtin_fmaf(sp, x2, 1.f / 120.f);
-  sp = __builtin_fmaf(sp, x2, -1.f / 6.f);
-  const float s = __builtin_fmaf(sp * x2, x, x);
-  float cp = __builtin_fmaf(x2, -1.f / 3628800.f, 1.f / 40320.f);
-  cp = __builtin_fmaf(cp, x2, -1.f / 720.f);
-  cp = __builtin_fmaf(cp, x2, 1.f / 24.f);
-  cp = __builtin_fmaf(cp, x2, -0.5f);
-  const float c = __builtin_fmaf(cp, x2, 1.f);
-  const int q = static_cast<int>(k) & 3;
-  const float s1 = (q & 1) ? c : s;
-  const float c1 = (q & 1) ? s : c;
-  sn = (q & 2) ? -s1 : s1;
-  cs = ((q + 1) & 2) ? -c1 : c1;
-}
-
 // exp(t * A) = m * (cy + i sy), m = exp(t Re A).
 struct CExp {
   float m, cy, sy;
 };
 
+// The angle t Im(A) in turns, reduced to [0, 1) by fract (exact), feeds the hardware
+// sine and cosine (which take turns): measured on MI355X against float64 over [-8, 8]
+// turns, their absolute error is at most 1.2e-7 (about one ulp of 1).
 __device__ __forceinline__ CExp cexp_t(float t, const CoefA& c) {
   CExp e;
   e.m = fast_exp2(t * c.ar2);
-  sincos_rev(t * c.airev, e.sy, e.cy);
+  const float rev = __builtin_amdgcn_fractf(t * c.airev);
+  e.cy = __builtin_amdgcn_cosf(rev);
+  e.sy = __builtin_amdgcn_sinf(rev);
   return e;
 }
 
@@ -185,13 +164,25 @@ __global__ __launch_bounds__(kCFwdW * 64) void cfwd_kernel(FwdParams p) {
       y[j] = Dv * uu[j];
       ssum += dlt[j];
     }
+    // B and C rows of the next state are loaded one state ahead.
+    float bnx[kCT], cnx[kCT];
+    load_seg<kCT>(Bb, tl, L, fast_bc, bnx);
+    load_seg<kCT>(Cb, tl, L, fast_bc, cnx);
     for (int n = 0; n < N; ++n) {
       const CoefA cf = load_coef(p.A, static_cast<size_t>(d) * N + n);
       float ar[kCT], ai[kCT], br[kCT], bi[kCT];
+      float bv[kCT], cv[kCT];
+#pragma unroll
+      for (int j = 0; j < kCT; ++j) {
+        bv[j] = bnx[j];
+        cv[j] = cnx[j];
+      }
+      if (n + 1 < N) {
+        load_seg<kCT>(Bb + (n + 1) * p.bc_sn, tl, L, fast_bc, bnx);
+        load_seg<kCT>(Cb + (n + 1) * p.bc_sn, tl, L, fast_bc, cnx);
+      }
       float hr = 0.f, hi = 0.f;
       {
-        float bv[kCT];
-        load_seg<kCT>(Bb + n * p.bc_sn, tl, L, fast_bc, bv);
 #pragma unroll
         for (int j = 0; j < kCT; ++j) {
           const CExp e = cexp_t(dlt[j], cf);
@@ -233,8 +224,6 @@ __global__ __launch_bounds__(kCFwdW * 64) void cfwd_kernel(FwdParams p) {
         *cp = make_float2(xr, xi);
       }
       {
-        float cv[kCT];
-        load_seg<kCT>(Cb + n * p.bc_sn, tl, L, fast_bc, cv);
 #pragma unroll
         for (int j = 0; j < kCT; ++j) {
           const float nr = __builtin_fmaf(ar[j], xr, __builtin_fmaf(-ai[j], xi, br[j]));
@@ -389,17 +378,45 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
         ddl[j] = 0.f;
       }
 
+      // B, C rows and the segment-entry state of the next state are loaded one state
+      // ahead, so their latency overlaps a state's arithmetic (Euler; ZOH keeps E_t per
+      // step in registers and has no room for them, so it loads each state's rows in place).
+      constexpr bool kAhead = !kZOH;
+      const float2* __restrict__ carry_seg = reinterpret_cast<const float2*>(p.carries) +
+                                             chan * N * p.n_seg + ts / kCT;
+      float bnx[kCT], cnx[kCT];
+      float2 hnx = make_float2(0.f, 0.f);
+      if (kAhead && active) {
+        const int n0 = w % N;
+        load_seg<kCT>(Bb + n0 * p.bc_sn, ts, L, fast_bc, bnx);
+        load_seg<kCT>(Cb + n0 * p.bc_sn, ts, L, fast_bc, cnx);
+        if (ts < L) hnx = carry_seg[static_cast<size_t>(n0) * p.n_seg];
+      }
       for (int it = 0; it < N; ++it) {
         const int n = (it + w) % N;
         const int arow = (w / N) * N + n;
         if (active) {
           const CoefA cf = load_coef(p.A, static_cast<size_t>(dd) * N + n);
           float bv[kCT], cv[kCT];
-          load_seg<kCT>(Bb + n * p.bc_sn, ts, L, fast_bc, bv);
-          load_seg<kCT>(Cb + n * p.bc_sn, ts, L, fast_bc, cv);
-          float hinr = 0.f, hini = 0.f;
-          if (ts < L) {
-            const float2 h0 = reinterpret_cast<const float2*>(p.carries)[(chan * N + n) * p.n_seg + ts / kCT];
+          float hinr, hini;
+          if constexpr (kAhead) {
+#pragma unroll
+            for (int j = 0; j < kCT; ++j) {
+              bv[j] = bnx[j];
+              cv[j] = cnx[j];
+            }
+            hinr = hnx.x;
+            hini = hnx.y;
+            if (it + 1 < N) {
+              const int nn = (it + 1 + w) % N;
+              load_seg<kCT>(Bb + nn * p.bc_sn, ts, L, fast_bc, bnx);
+              load_seg<kCT>(Cb + nn * p.bc_sn, ts, L, fast_bc, cnx);
+              if (ts < L) hnx = carry_seg[static_cast<size_t>(nn) * p.n_seg];
+            }
+          } else {
+            load_seg<kCT>(Bb + n * p.bc_sn, ts, L, fast_bc, bv);
+            load_seg<kCT>(Cb + n * p.bc_sn, ts, L, fast_bc, cv);
+            const float2 h0 = ts < L ? carry_seg[static_cast<size_t>(n) * p.n_seg] : make_float2(0.f, 0.f);
             hinr = h0.x;
             hini = h0.y;
           }
@@ -677,12 +694,12 @@ hipError_t launch_cfwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hi
 }
 
 int cbwd_chan_per_block(int batch, int dim) {
-  // Two workgroups fit a CU (LDS); take the fewest channel rounds K with
-  // batch * ceil(dim / (kW*K)) <= 2 * 256, at most kCMaxChan channels.
+  // One workgroup per CU (registers: 3 waves per SIMD); take the fewest channel rounds K
+  // with batch * ceil(dim / (kW*K)) <= 256, at most kCMaxChan channels.
   const long long per_row = (dim + kCBwdW - 1) / kCBwdW;
   long long k = 1;
   while (k < per_row && k * kCBwdW < kCMaxChan &&
-         static_cast<long long>(batch) * ((per_row + k - 1) / k) > 512)
+         static_cast<long long>(batch) * ((per_row + k - 1) / k) > 256)
     ++k;
   return static_cast<int>(k) * kCBwdW;
 }

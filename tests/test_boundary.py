@@ -305,10 +305,11 @@ def test_complex_workspace_bytes(lib):
     assert lib.mss_cbwd_workspace_bytes(bwd_args(dstate=17)) == 0
     real = lib.mss_bwd_workspace_bytes(bwd_args(batch=4, dim=1100, seqlen=64, dstate=4))
     cplx = lib.mss_cbwd_workspace_bytes(bwd_args(batch=4, dim=1100, seqlen=64, dstate=4))
-    # dB/dC partial rows of every channel block (complex blocks hold 16 channels here) plus
-    # complex dA partials [B][D][N][2] and dD / dbias partials [B][D], each 256-byte padded.
+    # dB/dC partial rows of every channel block (complex blocks hold 2 rounds of 12 channels
+    # here: 4 * ceil(1100 / 12) > 256 workgroups for one round) plus complex dA partials
+    # [B][D][N][2] and dD / dbias partials [B][D], each 256-byte padded.
     up = lambda x: (x + 255) // 256 * 256
-    blocks = (1100 + 15) // 16
+    blocks = (1100 + 23) // 24
     part = (4 * 2 * 4 * 64 + 63) // 64 * 64
     want = up(blocks * part * 4) + up(4 * 1100 * 4 * 2 * 4) + 2 * up(4 * 1100 * 4)
     assert cplx == want

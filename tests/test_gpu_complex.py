@@ -188,8 +188,8 @@ def test_complex_bf16():
 
 
 def test_complex_channel_rounds():
-    # batch * ceil(dim / 8) > 512 makes each backward workgroup walk two rounds of 8
-    # channels; 1100 = 68 * 16 + 12 leaves the last workgroup with a partial second round.
+    # batch * ceil(dim / 12) > 256 makes each backward workgroup walk two rounds of 12
+    # channels; 1100 = 45 * 24 + 20 leaves the last workgroup with a partial second round.
     log("case complex channel rounds B=4 D=1100 L=64 N=4")
     x, dout, dlast = complex_case(440, 4, 1100, 64, 4)
     check(x, dout, dlast, True)
