@@ -34,6 +34,7 @@ def test_norm_fwd_validation(lib, kw):
 def test_norm_bwd_validation(lib):
     base = dict(features=8, tokens=10, eps=1e-5, h=1, weight=1, rstd=1, dx=1, dhn=1)
     assert lib.mss_norm_bwd(_lib.NormArgs(**base), None) == _lib.MSS_ERR_INVALID_ARGUMENT  # no dweight
+    # dw partial rows: one per 64-token workgroup of the backward
     assert lib.mss_norm_bwd_workspace_bytes(_lib.NormArgs(features=768, tokens=16384)) == 256 * 768 * 4
 
 
@@ -67,7 +68,9 @@ def _bound_check(name, got, want, rtol, atol, normwise=False):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("with_delta", [False, True])
-@pytest.mark.parametrize("shape", [(96, 300), (768, 1024)])
+# (96, 300), (768, 1024): register-resident kernels (features a multiple of 32, <= 768;
+# 300 tokens leave a partial workgroup); (100, 333) and (1024, 320): the two-pass kernels.
+@pytest.mark.parametrize("shape", [(96, 300), (768, 1024), (100, 333), (1024, 320)])
 def test_add_rmsnorm(dtype, with_delta, shape):
     print(f"case add_rmsnorm {dtype} delta={with_delta} shape={shape}", flush=True)
     f, t = shape
