@@ -28,10 +28,10 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .conv1d_hip import causal_conv1d_fn
+from . import _lib
 from .decode import causal_conv1d_update, selective_state_update
 from .lm_ops import add_rmsnorm
-from .selective_scan_hip import selective_scan_fn
+from .selective_scan_hip import _io_tag, _ptr, _stream, selective_scan_fn
 
 __all__ = ["S6", "MambaBlock", "MambaLM", "RMSNormCM", "ShadowWeights", "GraphedTrainStep"]
 
@@ -89,19 +89,46 @@ class _TiedHeadMM(torch.autograd.Function):
 
 class ShadowWeights:
     """Low-precision copies of float32 weights, refreshed together in one multi-tensor
-    copy per step (instead of one cast per weight per use, plus one per gradient)."""
+    copy per step (instead of one cast per weight per use, plus one per gradient). The
+    copies are views of one buffer in the order given (offsets padded to 64 elements), so
+    consecutive weights with the same column count can be used as one stacked matrix."""
 
     def __init__(self, params):
         self.params = list(params)
         self.bufs = None
+        self.flat = None
+        self.offsets = {}
         self.by_id = {}
 
     def refresh(self, dtype):
-        if self.bufs is None or self.bufs[0].dtype != dtype:
-            self.bufs = [torch.empty_like(p, dtype=dtype) for p in self.params]
+        if self.bufs is None or self.flat.dtype != dtype:
+            offs, off = [], 0
+            for p in self.params:
+                offs.append(off)
+                off += (p.numel() + 63) // 64 * 64
+            self.flat = torch.empty(off, dtype=dtype, device=self.params[0].device)
+            self.bufs = [self.flat[o:o + p.numel()].view(p.shape) for o, p in zip(offs, self.params)]
             self.by_id = {id(p): b for p, b in zip(self.params, self.bufs)}
+            self.offsets = {id(p): o for p, o in zip(self.params, offs)}
         with torch.no_grad():
             torch._foreach_copy_(self.bufs, [p.detach() for p in self.params])
+
+    def stacked(self, *ws):
+        """The shadows of ws as one (sum of rows, cols) matrix when they lie back to back,
+        else None."""
+        if not self.by_id or any(id(w) not in self.by_id for w in ws):
+            return None
+        o, rows = self.offsets[id(ws[0])], 0
+        for w in ws:
+            if self.offsets[id(w)] != o + rows * w.shape[1] or w.shape[1] != ws[0].shape[1]:
+                return None
+            rows += w.shape[0]
+        return self.flat[o:o + rows * ws[0].shape[1]].view(rows, ws[0].shape[1])
+
+    def act(self, w, dtype):
+        """The weight in the activation dtype: its shadow, or a cast of the master."""
+        b = self.by_id.get(id(w))
+        return b if b is not None and b.dtype == dtype else w.to(dtype)
 
     def mm(self, w, x):
         """w @ x: plain autograd in float32, else through the shadow of w."""
@@ -225,6 +252,119 @@ class S6(nn.Module):
 _PLAIN = ShadowWeights([])  # no shadows: weights cast per use
 
 
+def _rows_strides(batch, tokens):
+    """mss_strides of (R, B*L) matrices read as (B, R, L) rows: b -> L, r -> B*L."""
+    l = tokens // batch
+    return _lib.Strides(io_batch=l, io_dim=tokens, bc_batch=l, bc_state=tokens)
+
+
+class _MambaMixer(torch.autograd.Function):
+    """The block between its norm and its out-projection, as one autograd node over the HIP
+    kernels (``mamba/mamba1.py:300-332`` with S6 ``:160-198``): [xin; z] = [W_in; W_z] x (one
+    GEMM when the two weights lie back to back), u = silu(conv(xin)), x_dbl = W_x u,
+    dt = W_dt x_dbl[:R], y = scan(u, dt, A, B = x_dbl[R:R+N], C = x_dbl[R+N:], D, z, dt_bias)
+    gated by silu(z). All activations are (features, B*L) matrices; the scan and conv read
+    their rows in place through row strides. The backward writes the scan's dB/dC straight
+    into the x_dbl gradient, the scan's dz and the conv's dxin into one [dxin; dz] buffer,
+    adds W_x^T dx_dbl to du in place, and takes dx and d[W_in; W_z] as one GEMM each:
+    no gradient sums or copies between the kernels. Weight gradients are float32."""
+
+    @staticmethod
+    def forward(ctx, x, w_in, w_z, conv_w, conv_b, w_x, w_dt, A, D, dt_bias, w_xz_act, w_x_act, w_dt_act,
+                batch, seq_lens, zoh):
+        lib = _lib.register_hip_kernel()
+        di, T = w_in.shape[0], x.shape[1]
+        r = w_dt.shape[1]
+        n = (w_x.shape[0] - r) // 2
+        L = T // batch
+        dev, act = x.device, x.dtype
+        cplx = A.is_complex()
+        io = _io_tag(act, "x")
+        st = _rows_strides(batch, T)
+        stream = _stream(x)
+        xz = torch.mm(w_xz_act, x)                       # (2 di, T): [xin; z]
+        xin, z = xz[:di], xz[di:]
+        u = torch.empty(di, T, dtype=act, device=dev)
+        ca = _lib.ConvArgs(batch=batch, dim=di, seqlen=L, width=conv_w.shape[1], io_dtype=io, activation=1,
+                           x=xin.data_ptr(), weight=conv_w.data_ptr(), bias=_ptr(conv_b),
+                           seq_lens=_ptr(seq_lens), y=u.data_ptr(), strides=st)
+        _lib.check(lib.mss_conv_fwd(ca, stream), "mss_conv_fwd")
+        x_dbl = torch.mm(w_x_act, u)                     # (R + 2N, T)
+        dt = torch.mm(w_dt_act, x_dbl[:r])               # (di, T), bias fused in the scan
+        n_seg = (L + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
+        sdt = torch.complex64 if cplx else torch.float32
+        rv = (lambda t: torch.view_as_real(t).data_ptr()) if cplx else (lambda t: t.data_ptr())
+        y = torch.empty(di, T, dtype=act, device=dev)
+        y_pre = torch.empty(di, T, dtype=act, device=dev)
+        last = torch.empty(batch, di, n, dtype=sdt, device=dev)
+        carries = torch.empty(batch, di, n, n_seg, dtype=sdt, device=dev)
+        fa = _lib.FwdArgs(batch=batch, dim=di, seqlen=L, dstate=n,
+                          discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER, delta_softplus=1,
+                          io_dtype=io, bc_dtype=io, u=u.data_ptr(), delta=dt.data_ptr(), A=rv(A),
+                          B=x_dbl[r].data_ptr(), C=x_dbl[r + n].data_ptr(), D=_ptr(D), z=z.data_ptr(),
+                          delta_bias=dt_bias.data_ptr(), seq_lens=_ptr(seq_lens), out=y.data_ptr(),
+                          last_state=rv(last), carries=rv(carries), y_pre=y_pre.data_ptr(), strides=st)
+        _lib.check((lib.mss_cfwd if cplx else lib.mss_fwd)(fa, stream), "scan forward")
+        ctx.save_for_backward(x, xz, u, x_dbl, dt, carries, y_pre, A, D, dt_bias, conv_w, conv_b,
+                              w_xz_act, w_x_act, w_dt_act, seq_lens)
+        ctx.batch, ctx.zoh, ctx.dims = batch, zoh, (di, r, n, L)
+        ctx.mark_non_differentiable(last, xz)
+        return y, last, xz
+
+    @staticmethod
+    def backward(ctx, dy, _dlast, _dxz):
+        lib = _lib.register_hip_kernel()
+        (x, xz, u, x_dbl, dt, carries, y_pre, A, D, dt_bias, conv_w, conv_b, w_xz_act, w_x_act, w_dt_act,
+         seq_lens) = ctx.saved_tensors
+        di, r, n, L = ctx.dims
+        batch = ctx.batch
+        T = x.shape[1]
+        dev, act = x.device, x.dtype
+        cplx = A.is_complex()
+        io = _io_tag(act, "x")
+        st = _rows_strides(batch, T)
+        stream = _stream(x)
+        rv = (lambda t: torch.view_as_real(t).data_ptr()) if cplx else (lambda t: t.data_ptr())
+        dy = dy.to(act).contiguous()
+        dxz = torch.empty(2 * di, T, dtype=act, device=dev)   # [dxin; dz]
+        dx_dbl = torch.empty(r + 2 * n, T, dtype=act, device=dev)
+        du = torch.empty(di, T, dtype=act, device=dev)
+        ddt = torch.empty(di, T, dtype=act, device=dev)
+        dA = torch.empty_like(A)
+        dD = None if D is None else torch.empty_like(D)
+        dbias = torch.empty_like(dt_bias)
+        ba = _lib.BwdArgs(batch=batch, dim=di, seqlen=L, dstate=n,
+                          discretization=_lib.MSS_ZOH if ctx.zoh else _lib.MSS_EULER, delta_softplus=1,
+                          io_dtype=io, bc_dtype=io, u=u.data_ptr(), delta=dt.data_ptr(), A=rv(A),
+                          B=x_dbl[r].data_ptr(), C=x_dbl[r + n].data_ptr(), D=_ptr(D), z=xz[di].data_ptr(),
+                          delta_bias=dt_bias.data_ptr(), seq_lens=_ptr(seq_lens), carries=rv(carries),
+                          y_pre=y_pre.data_ptr(), dout=dy.data_ptr(), du=du.data_ptr(), ddelta=ddt.data_ptr(),
+                          dA=rv(dA), dB=dx_dbl[r].data_ptr(), dC=dx_dbl[r + n].data_ptr(), dD=_ptr(dD),
+                          dz=dxz[di].data_ptr(), ddelta_bias=dbias.data_ptr(), strides=st)
+        ws_bytes = int((lib.mss_cbwd_workspace_bytes if cplx else lib.mss_bwd_workspace_bytes)(ba))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        ba.workspace, ba.workspace_bytes = ws.data_ptr(), ws_bytes
+        _lib.check((lib.mss_cbwd if cplx else lib.mss_bwd)(ba, stream), "scan backward")
+        dw_dt = _mm_fp32(ddt, x_dbl[:r].t())
+        torch.mm(w_dt_act.t(), ddt, out=dx_dbl[:r])
+        dw_x = _mm_fp32(dx_dbl, u.t())
+        du.addmm_(w_x_act.t(), dx_dbl)                    # du += W_x^T dx_dbl
+        dconv_w = torch.empty_like(conv_w)
+        dconv_b = None if conv_b is None else torch.empty_like(conv_b)
+        ca = _lib.ConvArgs(batch=batch, dim=di, seqlen=L, width=conv_w.shape[1], io_dtype=io, activation=1,
+                           x=xz.data_ptr(), weight=conv_w.data_ptr(), bias=_ptr(conv_b),
+                           seq_lens=_ptr(seq_lens), dy=du.data_ptr(), dx=dxz.data_ptr(),
+                           dweight=dconv_w.data_ptr(), dbias=_ptr(dconv_b), strides=st)
+        cws_bytes = int(lib.mss_conv_bwd_workspace_bytes(ca))
+        cws = torch.empty(cws_bytes, dtype=torch.uint8, device=dev)
+        ca.workspace, ca.workspace_bytes = cws.data_ptr(), cws_bytes
+        _lib.check(lib.mss_conv_bwd(ca, stream), "mss_conv_bwd")
+        dw_xz = _mm_fp32(dxz, x.t())
+        dx = torch.mm(w_xz_act.t(), dxz)
+        return (dx, dw_xz[:di], dw_xz[di:], dconv_w, dconv_b, dw_x, dw_dt, dA, dD, dbias,
+                None, None, None, None, None, None)
+
+
 class MambaBlock(nn.Module):
     """Mamba-1 block (``mamba/mamba1.py:216-337``): norm -> in-projections -> causal conv
     + silu -> S6 with D skip -> * silu(z) -> out-projection -> + residual."""
@@ -252,21 +392,28 @@ class MambaBlock(nn.Module):
     def forward(self, h, delta, batch, seq_lens=None, act_dtype=torch.bfloat16, weights=None):
         """h: (d_model, B*L) fp32 residual stream before the previous block's output `delta`
         (act_dtype, or None for the first block) is added. Returns (h + delta, this block's
-        output): the residual add is fused into the next norm."""
+        output): the residual add is fused into the next norm. The mixer between the norm and
+        the out-projection is one autograd node (_MambaMixer)."""
         weights = weights or _PLAIN
         h, x = self.norm(h, delta, act_dtype)
-        xin = weights.mm(self.in_proj, x)
-        z = weights.mm(self.z_proj, x)
-        # causal depthwise conv + silu (HIP kernel), masked past each row's length
-        u = _matrix(causal_conv1d_fn(_rows(xin, batch), self.conv_weight, self.conv_bias, seq_lens))
-        y = self.s6(u, batch, z=z, seq_lens=seq_lens, weights=weights)
+        s6 = self.s6
+        w_xz = weights.stacked(self.in_proj, self.z_proj)
+        if w_xz is None or w_xz.dtype != act_dtype:
+            w_xz = torch.cat([self.in_proj.detach(), self.z_proj.detach()]).to(act_dtype)
+        A = s6.a_matrix()
+        y, last, xz = _MambaMixer.apply(
+            x, self.in_proj, self.z_proj, self.conv_weight, self.conv_bias, s6.x_proj, s6.dt_proj, A,
+            None if s6.D is None else s6.D.float(), s6.dt_bias.float(), w_xz,
+            weights.act(s6.x_proj, act_dtype), weights.act(s6.dt_proj, act_dtype), batch, seq_lens,
+            s6.discretization == "zoh")
         if not torch.is_grad_enabled():  # inference: keep the decode caches of this prompt
+            xin = xz[:self.in_proj.shape[0]]
             k = self.conv_weight.shape[1]
             tail = _rows(xin, batch)[:, :, max(0, xin.shape[1] // batch - (k - 1)):]
             conv = torch.zeros(batch, xin.shape[0], k - 1, dtype=xin.dtype, device=xin.device)
             if k > 1:
                 conv[:, :, conv.shape[2] - tail.shape[2]:] = tail
-            self.cache = {"conv": conv, "ssm": self.s6.last_state, "A": self.s6.a_matrix()}
+            self.cache = {"conv": conv, "ssm": last, "A": A.detach()}
         return h, weights.mm(self.out_proj, y)
 
     def step(self, h, delta, cache, act_dtype=torch.bfloat16, weights=None):
