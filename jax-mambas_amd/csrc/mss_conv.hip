@@ -9,8 +9,8 @@
 //   y[t]   = act(pre[t]),  y[t] = 0 for t >= seq_lens[b]
 //
 // Mapping: one thread = kE consecutive steps of one row (a 16-byte vector when rows are
-// aligned, else kE = 1); grid (step tiles, channels, batch). The K-1 halo steps before a
-// thread's vector are re-read (they are the previous thread's, so they come from cache).
+// aligned, else kE = 1); grid (step tiles, channels, batch). On the vector path the K-1
+// halo steps around a thread's vector come from its neighbours through LDS.
 // Backward recomputes pre from x (no residual), forms g = dy * act'(pre), and writes
 //   dx[t] = sum_k w[k] * g[t + (K-1) - k],   and per-block partials of
 //   dw[k] = sum_t g[t] * x[t - (K-1) + k],   dbias = sum_t g[t]
@@ -71,13 +71,28 @@ __device__ __forceinline__ float at(const io_t* __restrict__ row, int t, int L) 
   return (t >= 0 && t < L) ? to_f32(row[t]) : 0.f;
 }
 
+// Vector path (kE >= K-1): the K-1 steps before a thread's vector are the previous
+// thread's last ones and, in the backward, the K-1 gradient terms after it are the next
+// thread's first ones; they are exchanged through LDS, so only the first (last) thread of a
+// workgroup reads its halo from global memory. Scalar path (kE = 1): halos are read.
+template <int kK, int kE>
+struct ConvShare {
+  static constexpr bool kOn = kE > 1 && kK > 1;
+  static constexpr int kRows = kOn ? kConvThreads : 1;
+  static constexpr int kH = kK > 1 ? kK - 1 : 1;
+};
+
 template <int kK, int kE, bool kSilu, typename io_t>
 __global__ __launch_bounds__(kConvThreads) void conv_fwd_kernel(ConvParams p) {
+  using Sh = ConvShare<kK, kE>;
+  __shared__ float s_tail[Sh::kRows][Sh::kH];
   const int L = p.seqlen;
   const int d = blockIdx.y;
   const int b = blockIdx.z;
-  const int t0 = (blockIdx.x * kConvThreads + threadIdx.x) * kE;
-  if (t0 >= L) return;
+  const int tid = threadIdx.x;
+  const int t0 = (blockIdx.x * kConvThreads + tid) * kE;
+  const bool live = t0 < L;
+  if (!Sh::kOn && !live) return;  // no barrier on the scalar path
   const long long row = b * p.sb + d * p.sd;
   const io_t* __restrict__ xr = static_cast<const io_t*>(p.x) + row;
   io_t* __restrict__ yr = static_cast<io_t*>(p.y) + row;
@@ -88,14 +103,25 @@ __global__ __launch_bounds__(kConvThreads) void conv_fwd_kernel(ConvParams p) {
   const float bias = p.bias ? p.bias[d] : 0.f;
 
   float xe[kE + kK - 1];  // x[t0 - (K-1) .. t0 + kE)
-#pragma unroll
-  for (int k = 0; k < kK - 1; ++k) xe[k] = at(xr, t0 - (kK - 1) + k, L);
   float v[kE];
-  if (kE > 1 && t0 + kE <= L) {
+  const bool full = kE > 1 && t0 + kE <= L;
+  if (full) {
     load_vec<kE>(xr + t0, v);
   } else {
 #pragma unroll
     for (int j = 0; j < kE; ++j) v[j] = at(xr, t0 + j, L);
+  }
+  if constexpr (Sh::kOn) {
+#pragma unroll
+    for (int k = 0; k < kK - 1; ++k) s_tail[tid][k] = v[kE - (kK - 1) + k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kK - 1; ++k)
+      xe[k] = tid > 0 ? s_tail[tid - 1][k] : at(xr, t0 - (kK - 1) + k, L);
+    if (!live) return;
+  } else {
+#pragma unroll
+    for (int k = 0; k < kK - 1; ++k) xe[k] = at(xr, t0 - (kK - 1) + k, L);
   }
 #pragma unroll
   for (int j = 0; j < kE; ++j) xe[kK - 1 + j] = v[j];
@@ -107,7 +133,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_fwd_kernel(ConvParams p) {
     for (int k = 0; k < kK; ++k) pre = __builtin_fmaf(w[k], xe[j + k], pre);
     out[j] = (t0 + j < len) ? (kSilu ? pre * sigmoid(pre) : pre) : 0.f;
   }
-  if (kE > 1 && t0 + kE <= L) {
+  if (full) {
     store_vec<kE>(yr + t0, out);
   } else {
 #pragma unroll
@@ -118,11 +144,15 @@ __global__ __launch_bounds__(kConvThreads) void conv_fwd_kernel(ConvParams p) {
 
 template <int kK, int kE, bool kSilu, typename io_t>
 __global__ __launch_bounds__(kConvThreads) void conv_bwd_kernel(ConvParams p) {
+  using Sh = ConvShare<kK, kE>;
   __shared__ float s_red[kConvThreads / 64][kK + 1];
+  __shared__ float s_xt[Sh::kRows][Sh::kH];  // last K-1 x of each thread's vector
+  __shared__ float s_gh[Sh::kRows][Sh::kH];  // first K-1 gradient terms g of each thread
   const int L = p.seqlen;
   const int d = blockIdx.y;
   const int b = blockIdx.z;
-  const int t0 = (blockIdx.x * kConvThreads + threadIdx.x) * kE;
+  const int tid = threadIdx.x;
+  const int t0 = (blockIdx.x * kConvThreads + tid) * kE;
   const long long row = b * p.sb + d * p.sd;
   const io_t* __restrict__ xr = static_cast<const io_t*>(p.x) + row;
   const io_t* __restrict__ gr = static_cast<const io_t*>(p.dy) + row;
@@ -137,45 +167,69 @@ __global__ __launch_bounds__(kConvThreads) void conv_bwd_kernel(ConvParams p) {
 #pragma unroll
   for (int k = 0; k <= kK; ++k) dw[k] = 0.f;
 
-  if (t0 < L) {
-    // x[t0 - (K-1) .. t0 + kE + K - 1) and g[t0 .. t0 + kE + K - 1)
-    constexpr int kX = kE + 2 * (kK - 1);
-    constexpr int kG = kE + kK - 1;
-    float xe[kX];
-    float ge[kG];
-    const bool full = kE > 1 && t0 + kE <= L;
-#pragma unroll
-    for (int k = 0; k < kK - 1; ++k) xe[k] = at(xr, t0 - (kK - 1) + k, L);
-    float v[kE], dv[kE];
-    if (full) {
-      load_vec<kE>(xr + t0, v);
-      load_vec<kE>(gr + t0, dv);
-    } else {
-#pragma unroll
-      for (int j = 0; j < kE; ++j) {
-        v[j] = at(xr, t0 + j, L);
-        dv[j] = at(gr, t0 + j, L);
-      }
-    }
+  // Threads past the row's end (t0 >= L) hold zeros and take part in the barriers.
+  // x[t0 - (K-1) .. t0 + kE + K - 1) and g[t0 .. t0 + kE + K - 1)
+  constexpr int kX = kE + 2 * (kK - 1);
+  constexpr int kG = kE + kK - 1;
+  float xe[kX];
+  float ge[kG];
+  const bool full = kE > 1 && t0 + kE <= L;
+  float v[kE], dv[kE];
+  if (full) {
+    load_vec<kE>(xr + t0, v);
+    load_vec<kE>(gr + t0, dv);
+  } else {
 #pragma unroll
     for (int j = 0; j < kE; ++j) {
-      xe[kK - 1 + j] = v[j];
-      ge[j] = dv[j];
+      v[j] = at(xr, t0 + j, L);
+      dv[j] = at(gr, t0 + j, L);
     }
+  }
 #pragma unroll
-    for (int k = 0; k < kK - 1; ++k) {
-      xe[kK - 1 + kE + k] = at(xr, t0 + kE + k, L);
-      ge[kE + k] = at(gr, t0 + kE + k, L);
+  for (int j = 0; j < kE; ++j) {
+    xe[kK - 1 + j] = v[j];
+    ge[j] = dv[j];
+  }
+  // The last thread of the workgroup (or every thread on the scalar path) reads the halo
+  // after its vector; the others take the next thread's gradient terms below.
+  const bool own_after = !Sh::kOn || tid == kConvThreads - 1;
+  if constexpr (Sh::kOn) {
+#pragma unroll
+    for (int k = 0; k < kK - 1; ++k) s_xt[tid][k] = v[kE - (kK - 1) + k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kK - 1; ++k)
+      xe[k] = tid > 0 ? s_xt[tid - 1][k] : at(xr, t0 - (kK - 1) + k, L);
+  } else {
+#pragma unroll
+    for (int k = 0; k < kK - 1; ++k) xe[k] = at(xr, t0 - (kK - 1) + k, L);
+  }
+#pragma unroll
+  for (int k = 0; k < kK - 1; ++k) {
+    xe[kK - 1 + kE + k] = own_after ? at(xr, t0 + kE + k, L) : 0.f;
+    ge[kE + k] = own_after ? at(gr, t0 + kE + k, L) : 0.f;
+  }
+  // g[t] = dy[t] * act'(pre[t]) for own steps (and the after-halo when read here); 0 past
+  // the length.
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    if (j >= kE && !own_after) continue;
+    float pre = bias;
+#pragma unroll
+    for (int k = 0; k < kK; ++k) pre = __builtin_fmaf(w[k], xe[j + k], pre);
+    const float gj = kSilu ? ge[j] * silu_grad(pre) : ge[j];
+    ge[j] = (t0 + j < len) ? gj : 0.f;
+  }
+  if constexpr (Sh::kOn) {
+#pragma unroll
+    for (int k = 0; k < kK - 1; ++k) s_gh[tid][k] = ge[k];
+    __syncthreads();
+    if (!own_after) {
+#pragma unroll
+      for (int k = 0; k < kK - 1; ++k) ge[kE + k] = s_gh[tid + 1][k];
     }
-    // g[t] = dy[t] * act'(pre[t]) for t in [t0, t0 + kE + K - 1); 0 past the length.
-#pragma unroll
-    for (int j = 0; j < kG; ++j) {
-      float pre = bias;
-#pragma unroll
-      for (int k = 0; k < kK; ++k) pre = __builtin_fmaf(w[k], xe[j + k], pre);
-      const float gj = kSilu ? ge[j] * silu_grad(pre) : ge[j];
-      ge[j] = (t0 + j < len) ? gj : 0.f;
-    }
+  }
+  if (t0 < L) {
     float dx[kE];
 #pragma unroll
     for (int j = 0; j < kE; ++j) {
