@@ -6,7 +6,10 @@ fused scan over the config-2 batch (fp32, B=4, D=1536, L=2048, N=16; softplus(de
 bias), D skip, silu(z) gate, last state), inputs resident in HBM, seeded synthetic data.
 Timing: HIP events recorded on the stream the kernels run on (torch's current stream,
 which the C ABI launches on), W untimed warmup steps, then exactly K timed steps
-bracketed by device synchronisation. Prints ONE JSON line on stdout; progress to stderr.
+bracketed by device synchronisation: replays of one captured HIP graph of the step's three
+launches (the eager rate is reported beside it); per-kernel means come from a separate
+eager run with events between the launches. Prints ONE JSON line on stdout; progress to
+stderr.
 
 Fields beyond the driver contract:
   roofline      dominant kernel: algorithmic bytes / its average event-timed duration
@@ -117,15 +120,16 @@ def gpu_step_setup(torch, cfg):
     return lib, t, fa, ba, lens
 
 
-def run_gpu(torch, cfg, steps, warmup):
-    """Times `steps` fwd+bwd steps of the scan at `cfg`; returns per-kernel means (ms)."""
+def run_gpu(torch, cfg, steps, warmup, graph=True):
+    """Times `steps` fwd+bwd steps of the scan at `cfg`. The step rate comes from a timed
+    region holding only the steps (replays of one captured HIP graph of the step's three
+    launches when `graph`, else eager launches); per-kernel means come from a second,
+    eager run with events between the launches (ms)."""
     from mamba_amd import _lib
 
     lib, t, fa, ba, lens = gpu_step_setup(torch, cfg)
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
 
-    def step(evs=None):
+    def step(sp, stream=None, evs=None):
         if evs:
             evs[0].record(stream)
         _lib.check(lib.mss_fwd(fa, sp), "mss_fwd")
@@ -138,28 +142,46 @@ def run_gpu(torch, cfg, steps, warmup):
         if evs:
             evs[3].record(stream)
 
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
     for _ in range(warmup):
-        step()
+        step(sp)
     torch.cuda.synchronize()
     log(f"[bench] {cfg.name}: warmup done ({warmup} steps)")
+
+    def timed(fn):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    eager_ms = timed(lambda: step(sp))
+    ms = eager_ms
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(torch.cuda.current_stream().cuda_stream)
+        g.replay()
+        torch.cuda.synchronize()
+        ms = timed(g.replay)
+        del g
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
     for i in range(steps):
-        step(evs[i])
-    end.record(stream)
+        step(sp, stream, evs[i])
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
     fwd = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     bws = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
     red = float(np.mean([e[2].elapsed_time(e[3]) for e in evs]))
-    log(f"[bench] {cfg.name}: timed {steps} steps: {total_ms / steps:.4f} ms/step "
-        f"(fwd {fwd:.4f}, bwd_scan {bws:.4f}, bwd_reduce {red:.4f} ms)")
+    log(f"[bench] {cfg.name}: timed {steps} steps: {ms:.4f} ms/step ({'hip graph' if graph else 'eager'}; eager "
+        f"{eager_ms:.4f}); kernels fwd {fwd:.4f}, bwd_scan {bws:.4f}, bwd_reduce {red:.4f} ms")
     del t
     torch.cuda.empty_cache()
-    return dict(ms=total_ms / steps, fwd=fwd, bwd_scan=bws, bwd_reduce=red, lens=lens)
+    return dict(ms=ms, eager_ms=eager_ms, graph=graph, fwd=fwd, bwd_scan=bws, bwd_reduce=red, lens=lens)
 
 
 def scan_report(cfg, r):
@@ -174,6 +196,7 @@ def scan_report(cfg, r):
         "workload": cfg.description, "dtype": cfg.dtype,
         "ms_fwd": round(r["fwd"], 5), "ms_bwd": round(r["bwd_scan"] + r["bwd_reduce"], 5),
         "ms_fwd_bwd": round(r["ms"], 5), "tokens_per_s": round(tokens / (r["ms"] * 1e-3), 1),
+        "launch": "hip graph" if r["graph"] else "eager", "ms_fwd_bwd_eager": round(r["eager_ms"], 5),
         "algorithmic_mb": {"fwd": round(fwd_b / 1e6, 1), "bwd": round(bwd_b / 1e6, 1)},
         "hbm_frac": {"fwd": frac(fwd_b, r["fwd"]), "bwd": frac(bwd_b, r["bwd_scan"] + r["bwd_reduce"]),
                      "fwd_bwd": frac(fwd_b + bwd_b, r["ms"])},
@@ -579,6 +602,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "ms_per_step_eager": round(r2["eager_ms"], 5),
+        "launch": "hip graph replay of the step's three launches" if r2["graph"] else "eager",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
