@@ -16,10 +16,15 @@ Two entry points, one pair of kernels:
   delta_bias and states. Softplus(delta + bias), the D skip, the silu(z) gate, the
   initial/last state and per-row lengths run inside the kernels.
 
-Both are differentiable (torch autograd); gradients come from the HIP backward kernel.
-There is no CPU path: inputs must live on a ROCm GPU and the library must be built.
+Both run through two torch.library custom ops, ``torch.ops.mamba_amd.selective_scan_fwd``
+and ``selective_scan_bwd`` (the C ABI's mss_fwd/mss_bwd, or mss_cfwd/mss_cbwd for a complex
+A), with fake implementations (shapes, dtypes and row layouts) and registered autograd, so
+they are differentiable and traceable by torch.compile; gradients come from the HIP backward
+kernel. There is no CPU path: inputs must live on a ROCm GPU and the library must be built.
 """
 from __future__ import annotations
+
+from typing import Optional, Tuple
 
 import torch
 
@@ -157,151 +162,157 @@ def _row_strides(t, layout):
     return s[0], s[1]
 
 
-class _SelectiveScan(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh,
-                io_layout, bc_layout):
-        lib = register_hip_kernel()
-        batch, dim, length = u.shape
-        n = A.shape[1]
-        n_seg = (length + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
-        out = _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        last = torch.empty(batch, dim, n, device=u.device, dtype=torch.float32)
-        # Residual: the state entering every 8-step segment, [B][D][N][ceil(L/8)].
-        carries = torch.empty(batch, dim, n, n_seg, device=u.device, dtype=torch.float32)
-        # Pre-gate output: the backward's dz needs it (kept only when z is given).
-        y_pre = _empty_rows(u.shape, io_layout, u.dtype, u.device) if z is not None else None
-        args = _lib.FwdArgs(
-            batch=batch, dim=dim, seqlen=length, dstate=n,
-            discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER,
-            delta_softplus=int(bool(delta_softplus)),
-            io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
-            u=_ptr(u), delta=_ptr(delta), A=_ptr(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
-            delta_bias=_ptr(delta_bias), initial_state=_ptr(initial_state), seq_lens=_ptr(seq_lens),
-            out=_ptr(out), last_state=_ptr(last), carries=_ptr(carries), y_pre=_ptr(y_pre),
-            strides=_strides(u, io_layout, B, bc_layout),
-        )
-        _lib.check(lib.mss_fwd(args, _stream(u)), "mss_fwd")
-        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre)
-        ctx.delta_softplus = bool(delta_softplus)
-        ctx.zoh = bool(zoh)
-        ctx.layouts = (io_layout, bc_layout)
-        return out, last
+# ---- torch.library custom ops over the C ABI (real and complex A). Optional results are
+# returned as empty tensors (custom ops return tensors only). The fake implementations give
+# the real ones' shapes, dtypes and row layouts, so torch.compile can trace the scan.
 
-    @staticmethod
-    def backward(ctx, dout, dlast):
-        lib = register_hip_kernel()
-        u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre = ctx.saved_tensors
-        batch, dim, length = u.shape
-        n = A.shape[1]
-        io_layout, bc_layout = ctx.layouts
-        if dout is None:
-            dout = torch.zeros_like(u)
-        dout = _conform(dout.to(u.dtype), io_layout)
-        dlast = None if dlast is None else dlast.float().contiguous()
-        du = _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        ddelta = _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        dA = torch.empty_like(A)
-        dB = _empty_rows(B.shape, bc_layout, B.dtype, B.device)
-        dC = _empty_rows(C.shape, bc_layout, C.dtype, C.device)
-        dD = None if D is None else torch.empty_like(D)
-        dz = None if z is None else _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        dbias = None if delta_bias is None else torch.empty_like(delta_bias)
-        dinit = None if initial_state is None else torch.empty_like(initial_state)
-        args = _lib.BwdArgs(
-            batch=batch, dim=dim, seqlen=length, dstate=n,
-            discretization=_lib.MSS_ZOH if ctx.zoh else _lib.MSS_EULER,
-            delta_softplus=int(ctx.delta_softplus),
-            io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
-            u=_ptr(u), delta=_ptr(delta), A=_ptr(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
-            delta_bias=_ptr(delta_bias), initial_state=_ptr(initial_state), seq_lens=_ptr(seq_lens),
-            carries=_ptr(carries), y_pre=_ptr(y_pre), dout=_ptr(dout), dlast_state=_ptr(dlast),
-            du=_ptr(du), ddelta=_ptr(ddelta), dA=_ptr(dA), dB=_ptr(dB), dC=_ptr(dC), dD=_ptr(dD),
-            dz=_ptr(dz), ddelta_bias=_ptr(dbias), dinitial_state=_ptr(dinit),
-            strides=_strides(u, io_layout, B, bc_layout),
-        )
-        ws_bytes = int(lib.mss_bwd_workspace_bytes(args))
-        ws = torch.empty(ws_bytes, device=u.device, dtype=torch.uint8)
-        args.workspace = ws.data_ptr()
-        args.workspace_bytes = ws_bytes
-        _lib.check(lib.mss_bwd(args, _stream(u)), "mss_bwd")
-        return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit, None, None, None, None, None
+_EMPTY = 0  # numel of an absent optional result
 
 
-class _ComplexSelectiveScan(torch.autograd.Function):
-    """Complex A (mss_cfwd / mss_cbwd): A (D, N), initial and last state (B, D, N) complex64,
-    passed to the kernels as interleaved float32 pairs (torch.view_as_real, no copy)."""
+def _layouts(u, B):
+    return _layout_of(u) or "brl", _layout_of(B) or "brl"
 
-    @staticmethod
-    def forward(ctx, u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh,
-                io_layout, bc_layout):
-        lib = register_hip_kernel()
-        batch, dim, length = u.shape
-        n = A.shape[1]
-        n_seg = (length + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
-        out = _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        last = torch.empty(batch, dim, n, device=u.device, dtype=torch.complex64)
-        carries = torch.empty(batch, dim, n, n_seg, device=u.device, dtype=torch.complex64)
-        y_pre = _empty_rows(u.shape, io_layout, u.dtype, u.device) if z is not None else None
-        rv = lambda t: None if t is None else torch.view_as_real(t).data_ptr()
-        args = _lib.FwdArgs(
-            batch=batch, dim=dim, seqlen=length, dstate=n,
-            discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER,
-            delta_softplus=int(bool(delta_softplus)),
-            io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
-            u=_ptr(u), delta=_ptr(delta), A=rv(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
-            delta_bias=_ptr(delta_bias), initial_state=rv(initial_state), seq_lens=_ptr(seq_lens),
-            out=_ptr(out), last_state=rv(last), carries=rv(carries), y_pre=_ptr(y_pre),
-            strides=_strides(u, io_layout, B, bc_layout),
-        )
-        _lib.check(lib.mss_cfwd(args, _stream(u)), "mss_cfwd")
-        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre)
-        ctx.delta_softplus = bool(delta_softplus)
-        ctx.zoh = bool(zoh)
-        ctx.layouts = (io_layout, bc_layout)
-        return out, last
 
-    @staticmethod
-    def backward(ctx, dout, dlast):
-        lib = register_hip_kernel()
-        u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre = ctx.saved_tensors
-        batch, dim, length = u.shape
-        n = A.shape[1]
-        io_layout, bc_layout = ctx.layouts
-        if dout is None:
-            dout = torch.zeros_like(u)
-        dout = _conform(dout.to(u.dtype), io_layout)
-        # Torch's gradient of a complex tensor for a real loss is dL/dRe + i dL/dIm: the
-        # convention of the C ABI's complex cotangents and gradients.
-        dlast = None if dlast is None else dlast.to(torch.complex64).contiguous()
-        rv = lambda t: None if t is None else torch.view_as_real(t).data_ptr()
-        du = _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        ddelta = _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        dA = torch.empty_like(A)
-        dB = _empty_rows(B.shape, bc_layout, B.dtype, B.device)
-        dC = _empty_rows(C.shape, bc_layout, C.dtype, C.device)
-        dD = None if D is None else torch.empty_like(D)
-        dz = None if z is None else _empty_rows(u.shape, io_layout, u.dtype, u.device)
-        dbias = None if delta_bias is None else torch.empty_like(delta_bias)
-        dinit = None if initial_state is None else torch.empty_like(initial_state)
-        args = _lib.BwdArgs(
-            batch=batch, dim=dim, seqlen=length, dstate=n,
-            discretization=_lib.MSS_ZOH if ctx.zoh else _lib.MSS_EULER,
-            delta_softplus=int(ctx.delta_softplus),
-            io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
-            u=_ptr(u), delta=_ptr(delta), A=rv(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
-            delta_bias=_ptr(delta_bias), initial_state=rv(initial_state), seq_lens=_ptr(seq_lens),
-            carries=rv(carries), y_pre=_ptr(y_pre), dout=_ptr(dout), dlast_state=rv(dlast),
-            du=_ptr(du), ddelta=_ptr(ddelta), dA=rv(dA), dB=_ptr(dB), dC=_ptr(dC), dD=_ptr(dD),
-            dz=_ptr(dz), ddelta_bias=_ptr(dbias), dinitial_state=rv(dinit),
-            strides=_strides(u, io_layout, B, bc_layout),
-        )
-        ws_bytes = int(lib.mss_cbwd_workspace_bytes(args))
-        ws = torch.empty(ws_bytes, device=u.device, dtype=torch.uint8)
-        args.workspace = ws.data_ptr()
-        args.workspace_bytes = ws_bytes
-        _lib.check(lib.mss_cbwd(args, _stream(u)), "mss_cbwd")
-        return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit, None, None, None, None, None
+def _state_dtype(A):
+    return torch.complex64 if A.is_complex() else torch.float32
+
+
+def _fwd_outputs(u, A, B, z):
+    """(out, last, carries, y_pre) allocated in the layouts the kernels write."""
+    batch, dim, length = u.shape
+    n = A.shape[1]
+    io_layout, _ = _layouts(u, B)
+    n_seg = (length + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
+    sdt = _state_dtype(A)
+    out = _empty_rows(u.shape, io_layout, u.dtype, u.device)
+    last = torch.empty(batch, dim, n, device=u.device, dtype=sdt)
+    # Residual: the state entering every 8-step segment, [B][D][N][ceil(L/8)].
+    carries = torch.empty(batch, dim, n, n_seg, device=u.device, dtype=sdt)
+    # Pre-gate output: the backward's dz needs it (kept only when z is given).
+    y_pre = (_empty_rows(u.shape, io_layout, u.dtype, u.device) if z is not None
+             else torch.empty(_EMPTY, device=u.device, dtype=u.dtype))
+    return out, last, carries, y_pre
+
+
+def _rv(t):
+    """Device pointer; complex tensors as interleaved (real, imaginary) float32 pairs."""
+    if t is None:
+        return None
+    return torch.view_as_real(t).data_ptr() if t.is_complex() else t.data_ptr()
+
+
+@torch.library.custom_op("mamba_amd::selective_scan_fwd", mutates_args=(), device_types="cuda")
+def _scan_fwd_op(u: torch.Tensor, delta: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                 D: Optional[torch.Tensor], z: Optional[torch.Tensor], delta_bias: Optional[torch.Tensor],
+                 initial_state: Optional[torch.Tensor], seq_lens: Optional[torch.Tensor],
+                 delta_softplus: bool, zoh: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """mss_fwd (mss_cfwd for a complex A): returns (out, last_state, carries, y_pre)."""
+    lib = register_hip_kernel()
+    io_layout, bc_layout = _layouts(u, B)
+    delta, z = _conform(delta, io_layout), _conform(z, io_layout)
+    C = _conform(C, bc_layout)
+    batch, dim, length = u.shape
+    out, last, carries, y_pre = _fwd_outputs(u, A, B, z)
+    args = _lib.FwdArgs(
+        batch=batch, dim=dim, seqlen=length, dstate=A.shape[1],
+        discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER, delta_softplus=int(bool(delta_softplus)),
+        io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
+        u=_ptr(u), delta=_ptr(delta), A=_rv(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
+        delta_bias=_ptr(delta_bias), initial_state=_rv(initial_state), seq_lens=_ptr(seq_lens),
+        out=_ptr(out), last_state=_rv(last), carries=_rv(carries), y_pre=_ptr(y_pre) if z is not None else None,
+        strides=_strides(u, io_layout, B, bc_layout),
+    )
+    fn, name = (lib.mss_cfwd, "mss_cfwd") if A.is_complex() else (lib.mss_fwd, "mss_fwd")
+    _lib.check(fn(args, _stream(u)), name)
+    return out, last, carries, y_pre
+
+
+@_scan_fwd_op.register_fake
+def _(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh):
+    return _fwd_outputs(u, A, B, z)
+
+
+def _bwd_outputs(u, A, B, D, z, delta_bias, initial_state):
+    io_layout, bc_layout = _layouts(u, B)
+    empty = lambda dt: torch.empty(_EMPTY, device=u.device, dtype=dt)
+    du = _empty_rows(u.shape, io_layout, u.dtype, u.device)
+    ddelta = _empty_rows(u.shape, io_layout, u.dtype, u.device)
+    dA = torch.empty_like(A)
+    dB = _empty_rows(B.shape, bc_layout, B.dtype, B.device)
+    dC = _empty_rows(B.shape, bc_layout, B.dtype, B.device)
+    dD = empty(torch.float32) if D is None else torch.empty_like(D)
+    dz = empty(u.dtype) if z is None else _empty_rows(u.shape, io_layout, u.dtype, u.device)
+    dbias = empty(torch.float32) if delta_bias is None else torch.empty_like(delta_bias)
+    dinit = empty(_state_dtype(A)) if initial_state is None else torch.empty_like(initial_state)
+    return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit
+
+
+@torch.library.custom_op("mamba_amd::selective_scan_bwd", mutates_args=(), device_types="cuda")
+def _scan_bwd_op(u: torch.Tensor, delta: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
+                 D: Optional[torch.Tensor], z: Optional[torch.Tensor], delta_bias: Optional[torch.Tensor],
+                 initial_state: Optional[torch.Tensor], seq_lens: Optional[torch.Tensor],
+                 carries: torch.Tensor, y_pre: torch.Tensor, dout: torch.Tensor, dlast: Optional[torch.Tensor],
+                 delta_softplus: bool, zoh: bool
+                 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                            torch.Tensor, torch.Tensor, torch.Tensor]:
+    """mss_bwd (mss_cbwd for a complex A): returns (du, ddelta, dA, dB, dC, dD, dz,
+    ddelta_bias, dinitial_state), empty where the input is absent."""
+    lib = register_hip_kernel()
+    io_layout, bc_layout = _layouts(u, B)
+    delta, z, dout = _conform(delta, io_layout), _conform(z, io_layout), _conform(dout.to(u.dtype), io_layout)
+    C = _conform(C, bc_layout)
+    y_pre = _conform(y_pre, io_layout) if z is not None else None
+    dlast = None if dlast is None else dlast.to(_state_dtype(A)).contiguous()
+    batch, dim, length = u.shape
+    du, ddelta, dA, dB, dC, dD, dz, dbias, dinit = _bwd_outputs(u, A, B, D, z, delta_bias, initial_state)
+    opt = lambda t, given: _rv(t) if given is not None else None
+    args = _lib.BwdArgs(
+        batch=batch, dim=dim, seqlen=length, dstate=A.shape[1],
+        discretization=_lib.MSS_ZOH if zoh else _lib.MSS_EULER, delta_softplus=int(bool(delta_softplus)),
+        io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
+        u=_ptr(u), delta=_ptr(delta), A=_rv(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
+        delta_bias=_ptr(delta_bias), initial_state=_rv(initial_state), seq_lens=_ptr(seq_lens),
+        carries=_rv(carries), y_pre=_ptr(y_pre), dout=_ptr(dout), dlast_state=_rv(dlast),
+        du=_ptr(du), ddelta=_ptr(ddelta), dA=_rv(dA), dB=_ptr(dB), dC=_ptr(dC), dD=opt(dD, D),
+        dz=opt(dz, z), ddelta_bias=opt(dbias, delta_bias), dinitial_state=opt(dinit, initial_state),
+        strides=_strides(u, io_layout, B, bc_layout),
+    )
+    cplx = A.is_complex()
+    ws_bytes = int((lib.mss_cbwd_workspace_bytes if cplx else lib.mss_bwd_workspace_bytes)(args))
+    ws = torch.empty(ws_bytes, device=u.device, dtype=torch.uint8)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = ws_bytes
+    fn, name = (lib.mss_cbwd, "mss_cbwd") if cplx else (lib.mss_bwd, "mss_bwd")
+    _lib.check(fn(args, _stream(u)), name)
+    return du, ddelta, dA, dB, dC, dD, dz, dbias, dinit
+
+
+@_scan_bwd_op.register_fake
+def _(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre, dout, dlast,
+      delta_softplus, zoh):
+    return _bwd_outputs(u, A, B, D, z, delta_bias, initial_state)
+
+
+def _scan_setup_context(ctx, inputs, output):
+    u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh = inputs
+    _, _, carries, y_pre = output
+    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre)
+    ctx.delta_softplus, ctx.zoh = delta_softplus, zoh
+
+
+def _scan_backward(ctx, dout, dlast, _dcarries, _dy_pre):
+    u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre = ctx.saved_tensors
+    if dout is None:
+        dout = torch.zeros_like(u)
+    g = torch.ops.mamba_amd.selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens,
+                                               carries, y_pre, dout, dlast, ctx.delta_softplus, ctx.zoh)
+    du, ddelta, dA, dB, dC, dD, dz, dbias, dinit = g
+    pick = lambda t, given: t if given is not None else None
+    return (du, ddelta, dA, dB, dC, pick(dD, D), pick(dz, z), pick(dbias, delta_bias),
+            pick(dinit, initial_state), None, None, None)
+
+
+torch.library.register_autograd("mamba_amd::selective_scan_fwd", _scan_backward, setup_context=_scan_setup_context)
 
 
 def _validate_complex(A, initial_state):
@@ -326,17 +337,17 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
                         seq_lens, discretization)
     else:
         _validate_fused(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, discretization)
-    register_hip_kernel()
+    if not torch.compiler.is_compiling():
+        register_hip_kernel()  # fail early when the library is missing (the op loads it too)
     # Rows of u/delta/z (and B/C) may be batch-outer or channel-outer; the others follow
     # u's (B's) layout, copied only when they differ.
     io_layout = _layout_of(u) or "brl"
     bc_layout = _layout_of(B) or "brl"
-    fn = _ComplexSelectiveScan if cplx else _SelectiveScan
-    out, last = fn.apply(
+    out, last, _, _ = torch.ops.mamba_amd.selective_scan_fwd(
         _conform(u, io_layout), _conform(delta, io_layout), A.contiguous(),
         _conform(B, bc_layout), _conform(C, bc_layout),
         _contig(D), _conform(z, io_layout), _contig(delta_bias), _contig(initial_state),
-        _contig(seq_lens), bool(delta_softplus), discretization == "zoh", io_layout, bc_layout)
+        _contig(seq_lens), bool(delta_softplus), discretization == "zoh")
     return (out, last) if return_last_state else out
 
 
@@ -379,7 +390,7 @@ def selective_scan(A, deltas, Bs, Cs, u, initial_x=None, *, use_euler_barB_appro
     # Channel-major physical layout at the kernel boundary (the reference gets the same
     # layout from XLA input_layouts=(0,2,1), mamba/selective_scan_cuda.py:135-147).
     t = lambda x: x.transpose(1, 2).contiguous()
-    out, last = _SelectiveScan.apply(t(u), t(deltas), A.contiguous(), t(Bs), t(Cs), None, None,
-                                     None, initial_x.contiguous(), None, False,
-                                     not use_euler_barB_approx, "brl", "brl")
+    out, last, _, _ = torch.ops.mamba_amd.selective_scan_fwd(
+        t(u), t(deltas), A.contiguous(), t(Bs), t(Cs), None, None, None, initial_x.contiguous(), None,
+        False, not use_euler_barB_approx)
     return out.transpose(1, 2), last

@@ -314,3 +314,45 @@ def test_complex_workspace_bytes(lib):
     want = up(blocks * part * 4) + up(4 * 1100 * 4 * 2 * 4) + 2 * up(4 * 1100 * 4)
     assert cplx == want
     assert real > 0
+
+
+# torch.library registration of the scan: fake implementations (no GPU needed) give the
+# real ones' shapes, dtypes and row layouts; absent optional results are empty tensors.
+def _fake_scan(cplx, layout, with_extras):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    b, d, l, n = 2, 3, 40, 4
+    with FakeTensorMode():
+        if layout == "rbl":
+            u = torch.empty(d, b, l, device="cuda").permute(1, 0, 2)
+            B = torch.empty(n, b, l, device="cuda").permute(1, 0, 2)
+        else:
+            u = torch.empty(b, d, l, device="cuda")
+            B = torch.empty(b, n, l, device="cuda")
+        A = torch.empty(d, n, device="cuda", dtype=torch.complex64 if cplx else torch.float32)
+        D = torch.empty(d, device="cuda") if with_extras else None
+        z = u if with_extras else None
+        x0 = torch.empty(b, d, n, device="cuda", dtype=A.dtype) if with_extras else None
+        fw = torch.ops.mamba_amd.selective_scan_fwd(u, u, A, B, B, D, z, D, x0, None, True, False)
+        bw = torch.ops.mamba_amd.selective_scan_bwd(u, u, A, B, B, D, z, D, x0, None, fw[2], fw[3], fw[0],
+                                                    fw[1], True, False)
+        return u, B, A, fw, bw
+
+
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("layout", ["brl", "rbl"])
+@pytest.mark.parametrize("with_extras", [False, True])
+def test_custom_op_fake_shapes(cplx, layout, with_extras):
+    u, B, A, (out, last, carries, y_pre), bw = _fake_scan(cplx, layout, with_extras)
+    sdt = torch.complex64 if cplx else torch.float32
+    assert out.shape == u.shape and out.stride() == u.stride() and out.dtype == u.dtype
+    assert last.shape == (2, 3, 4) and last.dtype == sdt
+    assert carries.shape == (2, 3, 4, 5) and carries.dtype == sdt
+    assert (y_pre.numel() > 0) == with_extras
+    du, ddelta, dA, dB, dC, dD, dz, dbias, dinit = bw
+    assert du.stride() == u.stride() and ddelta.stride() == u.stride()
+    assert dA.shape == A.shape and dA.dtype == A.dtype
+    assert dB.shape == B.shape and dB.stride() == B.stride() and dC.stride() == B.stride()
+    for t in (dD, dz, dbias, dinit):
+        assert (t.numel() > 0) == with_extras
+    if with_extras:
+        assert dz.stride() == u.stride() and dinit.dtype == sdt
