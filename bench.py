@@ -50,6 +50,17 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def read_traffic(kernel_tag):
     """HBM bytes per launch from profiles/<kernel_tag>_traffic.txt (key=value lines)."""
     path = os.path.join(ROOT, "profiles", f"{kernel_tag}_traffic.txt")
@@ -310,7 +321,8 @@ def cpu_baseline_complex(torch, target_s, d0=8):
     t_med = float(np.median(times))
     t_full = t_med * cfg.dim / dslice
     log(f"[bench] complex c2 cpu baseline: D={dslice} median {t_med:.2f} s")
-    return {"value": cfg.batch * cfg.length / t_full, "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": cfg.batch * cfg.length / t_full, "unit": "tokens/s", "cores": threads,
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": (f"complex c2: B={cfg.batch} L={cfg.length} N={cfg.dstate} complex64 states, {dslice} of "
                        f"{cfg.dim} channels, fwd+bwd (autograd) median of 3 = {t_med:.3f} s, scaled "
                        f"x{cfg.dim / dslice:.1f} ({t_full:.2f} s per step)")}
@@ -503,6 +515,7 @@ def cpu_baseline(torch, cfg, target_s, lens=None, d0=32):
         "value": tokens / t_full,
         "unit": "tokens/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": (f"{cfg.name}: B={cfg.batch} L={cfg.length} N={cfg.dstate} ({cfg.dtype} inputs, fp32 math), "
                    f"{dslice} of {cfg.dim} channels, fwd+bwd (autograd) median of 3 = {t_med:.3f} s, "
