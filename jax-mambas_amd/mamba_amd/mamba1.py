@@ -309,6 +309,7 @@ class _MambaMixer(torch.autograd.Function):
                               w_xz_act, w_x_act, w_dt_act, seq_lens)
         ctx.batch, ctx.zoh, ctx.dims = batch, zoh, (di, r, n, L)
         ctx.mark_non_differentiable(last, xz)
+        ctx.set_materialize_grads(False)  # no zero-filled gradients for last / xz
         return y, last, xz
 
     @staticmethod
@@ -325,7 +326,7 @@ class _MambaMixer(torch.autograd.Function):
         st = _rows_strides(batch, T)
         stream = _stream(x)
         rv = (lambda t: torch.view_as_real(t).data_ptr()) if cplx else (lambda t: t.data_ptr())
-        dy = dy.to(act).contiguous()
+        dy = torch.zeros(di, T, dtype=act, device=dev) if dy is None else dy.to(act).contiguous()
         dxz = torch.empty(2 * di, T, dtype=act, device=dev)   # [dxin; dz]
         dx_dbl = torch.empty(r + 2 * n, T, dtype=act, device=dev)
         du = torch.empty(di, T, dtype=act, device=dev)
