@@ -28,18 +28,25 @@
 namespace mss {
 
 constexpr int kBwdT = kSegSteps;  // steps per lane: the granularity of the forward's carries
-constexpr int kBwdW = 12;         // waves per workgroup (3 per SIMD, one workgroup per CU)
 constexpr int kBwdChunk = 64 * kBwdT;
-constexpr int kMaxChanPerBlock = 96;  // 8 rounds of 12 waves
+constexpr int kMaxChanPerBlock = 96;  // channels one workgroup walks, at most
 constexpr int kCUs = 256;             // MI355X compute units
+
+// Waves per workgroup, one workgroup per CU: 12 (3 per SIMD, 168 VGPRs) for every state
+// count, or 16 (4 per SIMD, 128 VGPRs) when 16 waves own exactly 16 accumulator rows
+// (N divides 16), which keeps the LDS within 160 KB. 16 waves walk a round of channels
+// ~1.2x slower than 12 but 16/12 as many channels per round (measured on MI355X).
+constexpr bool bwd_waves_fit(int waves, int n) { return waves == 12 || (waves == 16 && 16 % n == 0); }
 
 // Floats of LDS holding the dB/dC accumulator (ceil(kW/N) copies of 2N rows of a chunk,
 // see the kernel) followed by the B/C stage (2N rows of the chunk in bc_t), maximised over
-// N in [1, kMaxN]: N = 11 needs two accumulator copies (22 rows) and is the largest.
-constexpr int bwd_lds_floats(int bc_bytes) {
+// the N the wave count serves: with 12 waves N = 11 needs two accumulator copies (22 rows)
+// and is the largest.
+constexpr int bwd_lds_floats(int waves, int bc_bytes) {
   int m = 0;
   for (int n = 1; n <= kMaxN; ++n) {
-    const int v = ((kBwdW + n - 1) / n) * n * 2 * kBwdChunk + n * 2 * kBwdChunk * bc_bytes / 4;
+    if (!bwd_waves_fit(waves, n)) continue;
+    const int v = ((waves + n - 1) / n) * n * 2 * kBwdChunk + n * 2 * kBwdChunk * bc_bytes / 4;
     m = v > m ? v : m;
   }
   return m;
@@ -131,10 +138,9 @@ __device__ __forceinline__ void stage_chunk(const bc_t* __restrict__ Bb, const b
   }
 }
 
-template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
-__global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
+template <int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
+__global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   constexpr int kT = kBwdT;
-  constexpr int kW = kBwdW;
   constexpr int kChunk = kBwdChunk;
   constexpr int kRowSlots = kChunk * static_cast<int>(sizeof(bc_t)) / 16;
   // One LDS buffer: first the dB/dC partial sums of the workgroup's channels for one
@@ -143,7 +149,7 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
   // w / N, so rows are updated with plain read-add-write in a fixed order (LDS float
   // atomics are avoided: far slower than a read, an add and a write on gfx950). Then the
   // B/C rows of the current chunk, all states: stage[n][B|C][slot].
-  __shared__ __attribute__((aligned(16))) float lds[bwd_lds_floats(sizeof(bc_t))];
+  __shared__ __attribute__((aligned(16))) float lds[bwd_lds_floats(kW, sizeof(bc_t))];
   __shared__ float s_mu[kMaxChanPerBlock][kMaxN];  // adjoint message entering the chunk
   __shared__ float s_dA[kMaxChanPerBlock][kMaxN];
   __shared__ float s_dD[kMaxChanPerBlock];
@@ -249,8 +255,10 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
       float dlt[kT], dlu[kT], uu[kT], g[kT], s1[kT], s2[kT];
       float ssum = 0.f;
       float hin_next = 0.f;
-      if (active) {
-        if (seg_ok) hin_next = (carry_chunk + static_cast<size_t>(wmod) * p.n_seg)[seg];
+      if (active && seg_ok) hin_next = (carry_chunk + static_cast<size_t>(wmod) * p.n_seg)[seg];
+      {
+        // Unconditional, so no per-step value needs a copy for the inactive path: a wave past
+        // the last channel reads the clamped channel's row and never stores or accumulates.
         load_seg<kT>(static_cast<const io_t*>(p.delta) + row, tl, L, fast, dlt);
         load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
         load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, fast, g);
@@ -267,7 +275,7 @@ __global__ __launch_bounds__(kBwdW * 64) void bwd_kernel(BwdParams p) {
             yp[j] = go * yp[j] * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
             g[j] = go * zr[j] * sz;
           }
-          store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);
+          if (active) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);
         }
 #pragma unroll
         for (int j = 0; j < kT; ++j) {
@@ -550,7 +558,13 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
 template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
 static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
   dim3 grid(p.n_blocks_d, p.batch);
-  hipLaunchKernelGGL((bwd_kernel<kZOH, kHasZ, io_t, bc_t>), grid, dim3(kBwdW * 64), 0, stream, p);
+  if (p.waves == 16) {
+    if (!bwd_waves_fit(16, p.dstate) || p.chan_per_block % 16 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((bwd_kernel<16, kZOH, kHasZ, io_t, bc_t>), grid, dim3(16 * 64), 0, stream, p);
+  } else {
+    if (p.waves != 12 || p.chan_per_block % 12 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((bwd_kernel<12, kZOH, kHasZ, io_t, bc_t>), grid, dim3(12 * 64), 0, stream, p);
+  }
   return hipGetLastError();
 }
 
@@ -563,21 +577,39 @@ static hipError_t launch_bwd_io(const BwdParams& p, int zoh, hipStream_t stream)
             : launch_bwd_t<false, false, io_t, bc_t>(p, stream);
 }
 
-int bwd_chan_per_block(int batch, int dim, int varlen) {
-  // One workgroup per CU holds the B/C stage and the dB/dC accumulator (LDS), so the grid
-  // should fit one pass over the 256 CUs: the fewest channel rounds K with
-  // batch * ceil(dim / (kW*K)) <= 256 (more rounds also mean fewer dB/dC partials to
-  // reduce). With variable lengths rows finish at different times, so workgroups stay ~4x
-  // smaller and the hardware balances them. Bounded by the LDS bookkeeping size; depends
-  // on shapes only.
-  const long long per_row = (dim + kBwdW - 1) / kBwdW;  // rounds needed for a whole row
-  const long long target = varlen ? 4 * kCUs : kCUs;
+// Channels one workgroup of `waves` waves walks: the fewest channel rounds K with
+// batch * ceil(dim / (waves*K)) <= target workgroups (more rounds also mean fewer dB/dC
+// partials to reduce), bounded by the LDS bookkeeping size.
+static int chan_per_block_for(int waves, int batch, int dim, long long target) {
+  const long long per_row = (dim + waves - 1) / waves;  // rounds needed for a whole row
   long long k = (static_cast<long long>(batch) * per_row + target - 1) / target;
   if (k < 1) k = 1;
   while (k < per_row && static_cast<long long>(batch) * ((per_row + k - 1) / k) > target) ++k;
-  if (k > kMaxChanPerBlock / kBwdW) k = kMaxChanPerBlock / kBwdW;
+  if (k > kMaxChanPerBlock / waves) k = kMaxChanPerBlock / waves;
   if (k > per_row) k = per_row;
-  return static_cast<int>(k) * kBwdW;
+  return static_cast<int>(k) * waves;
+}
+
+BwdPlan bwd_plan(int batch, int dim, int dstate, int varlen) {
+  // One workgroup per CU holds the B/C stage and the dB/dC accumulator (LDS), so the grid
+  // should fit one pass over the 256 CUs. With variable lengths rows finish at different
+  // times, so workgroups stay ~4x smaller and the hardware balances them. Of 12 and 16
+  // waves the plan takes the one with the smaller modelled time: workgroup passes x rounds
+  // x time of a round (16 waves: 1.2x that of 12). Depends on shapes only.
+  const long long target = varlen ? 4 * kCUs : kCUs;
+  auto cost = [&](int waves, int cpb) {
+    const long long grid = static_cast<long long>(batch) * ((dim + cpb - 1) / cpb);
+    const double rounds = static_cast<double>(cpb / waves) * (waves == 16 ? 1.2 : 1.0);
+    const double passes = varlen ? static_cast<double>(grid) / kCUs
+                                 : static_cast<double>((grid + kCUs - 1) / kCUs);
+    return passes * rounds;
+  };
+  BwdPlan plan{12, chan_per_block_for(12, batch, dim, target)};
+  if (bwd_waves_fit(16, dstate)) {
+    const int cpb16 = chan_per_block_for(16, batch, dim, target);
+    if (cost(16, cpb16) < cost(12, plan.chan_per_block)) plan = BwdPlan{16, cpb16};
+  }
+  return plan;
 }
 
 hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16,

@@ -22,7 +22,7 @@ hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16
                            hipStream_t stream);
 hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, void* dA, void* dB,
                              void* dC, float* dD, float* dbias, hipStream_t stream);
-int bwd_chan_per_block(int batch, int dim, int varlen);
+BwdPlan bwd_plan(int batch, int dim, int dstate, int varlen);
 hipError_t launch_cfwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
 hipError_t launch_cbwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
 int cbwd_chan_per_block(int batch, int dim);
@@ -112,7 +112,7 @@ bool strides_aligned(long long s0, long long s1, size_t esz) {
 int n_seg_of(int32_t seqlen) { return (seqlen + MSS_SEG_STEPS - 1) / MSS_SEG_STEPS; }
 
 struct BwdLayout {
-  int chan_per_block = 0, n_blocks_d = 0;
+  int waves = 12, chan_per_block = 0, n_blocks_d = 0;
   size_t part_stride = 0;  // floats per channel block of dB/dC partials (multiple of 64)
   size_t off_dA = 0, off_dD = 0, off_db = 0, total = 0;
 };
@@ -121,8 +121,13 @@ struct BwdLayout {
 BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate, bool varlen,
                      bool cplx = false) {
   BwdLayout l;
-  l.chan_per_block = cplx ? mss::cbwd_chan_per_block(batch, dim)
-                          : mss::bwd_chan_per_block(batch, dim, varlen ? 1 : 0);
+  if (cplx) {
+    l.chan_per_block = mss::cbwd_chan_per_block(batch, dim);
+  } else {
+    const mss::BwdPlan plan = mss::bwd_plan(batch, dim, dstate, varlen ? 1 : 0);
+    l.waves = plan.waves;
+    l.chan_per_block = plan.chan_per_block;
+  }
   l.n_blocks_d = (dim + l.chan_per_block - 1) / l.chan_per_block;
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   l.part_stride = (static_cast<size_t>(batch) * 2 * dstate * seqlen + 63) / 64 * 64;
@@ -227,6 +232,7 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   p.vec_bc = (bc_row % 16 == 0) && strides_aligned(st.bc_sb, st.bc_sn, bc_e) && aligned16(a->B) &&
              aligned16(a->C);
   p.n_seg = n_seg_of(a->seqlen);
+  p.waves = l.waves;
   p.chan_per_block = l.chan_per_block;
   p.n_blocks_d = l.n_blocks_d;
   p.u = a->u;

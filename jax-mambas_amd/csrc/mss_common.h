@@ -377,11 +377,17 @@ struct FwdParams {
   void* y_pre;
 };
 
+// Backward launch shape: waves per workgroup and channels per workgroup.
+struct BwdPlan {
+  int waves, chan_per_block;
+};
+
 struct BwdParams {
   int batch, dim, seqlen, dstate;
   int delta_softplus;
   int vec_io, vec_bc;
   int n_seg;
+  int waves;           // waves per backward workgroup (12 or 16)
   int chan_per_block;  // channels one workgroup walks (multiple of the wave count)
   int n_blocks_d;      // ceil(dim / chan_per_block)
   long long io_sb, io_sd;  // row strides of u/delta/z/y_pre/dout/du/ddelta/dz

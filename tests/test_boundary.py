@@ -181,6 +181,39 @@ def test_workspace_size_depends_on_shapes_only(lib):
     assert n1 >= 4 * 2 * 16 * 2048 * 4
 
 
+def _bwd_blocks(lib, batch, dim, seqlen, dstate):
+    """Channel blocks of the backward plan, read back from the workspace size: dB/dC partials
+    (blocks x [batch][2][N][L] floats, padded to 64) then dA, dD and dbias partials, each
+    rounded up to 256 bytes."""
+    a = bwd_args(batch=batch, dim=dim, seqlen=seqlen, dstate=dstate)
+    up = lambda x: (x + 255) // 256 * 256
+    stride = (batch * 2 * dstate * seqlen + 63) // 64 * 64
+    rest = up(batch * dim * dstate * 4) + 2 * up(batch * dim * 4)
+    total = lib.mss_bwd_workspace_bytes(a)
+    assert (total - rest) % (stride * 4) == 0
+    return (total - rest) // (stride * 4)
+
+
+@pytest.mark.parametrize("shape,waves", [
+    ((4, 1536, 2048, 16), 12),   # config 2: 24 channels per CU, 12 waves x 2 rounds
+    ((8, 2048, 4096, 16), 16),   # config 3: 16 waves x 4 rounds beat 12 x 6 (232 workgroups)
+    ((1, 4096, 600, 8), 16),     # one pass of 16-channel workgroups
+    ((1, 4096, 600, 11), 12),    # 16 waves need N to divide 16
+    ((2, 24, 64, 16), 12),       # small grids: 12 waves, one round
+])
+def test_backward_plan(lib, shape, waves):
+    """The backward takes 12 or 16 waves per workgroup by a modelled time: workgroup passes
+    over 256 CUs x channel rounds x the time of a round (1.2x for 16 waves); the channel
+    count per workgroup is the fewest rounds whose grid fits one pass."""
+    b, d, l, n = shape
+    per_row = -(-d // waves)
+    k = max(1, -(-b * per_row // 256))
+    while k < per_row and b * (-(-per_row // k)) > 256:
+        k += 1
+    cpb = min(k, 96 // waves, per_row) * waves
+    assert _bwd_blocks(lib, b, d, l, n) == -(-d // cpb)
+
+
 def test_reference_entry_points_validate(lib):
     p = ctypes.c_void_p(1)
     assert lib.mss_scan_fwd(None, 0, 0, 10, 3, 4, *[p] * 9) == _lib.MSS_ERR_INVALID_ARGUMENT

@@ -184,6 +184,29 @@ def test_fused_wide_grid(zoh):
     check_fused(ts, out, last, fw, g)
 
 
+@pytest.mark.parametrize("zoh", [False, True])
+@pytest.mark.parametrize("n", [8, 4, 1])
+def test_sixteen_wave_state_counts(n, zoh):
+    """1 x 4096 channels: the backward runs 16 waves per workgroup (its plan for this grid,
+    checked on the host in test_boundary), where N < 16 states give each wave a copy of the
+    rotated dB/dC accumulator rows (16 / N copies)."""
+    log(f"case sixteen waves N={n} zoh={zoh}")
+    x, dout, dlast = fused_case(960 + n + zoh, 1, 4096, 600, n, zoh=zoh)
+    ts, out, last = run_fused(x, dout, dlast, "f32", zoh)
+    fw, g = oracle_fused(x, dout, dlast, zoh)
+    check_fused(ts, out, last, fw, g)
+
+
+def test_sixteen_wave_varlen():
+    """Variable lengths on a grid whose backward plan is 16 waves per workgroup: whole chunks
+    past a row's length (zero gradients, the adjoint passing through) and an empty row."""
+    log("case sixteen waves varlen")
+    x, dout, dlast = fused_case(970, 4, 2048, 1100, 16, lens=[1100, 530, 0, 1])
+    ts, out, last = run_fused(x, dout, dlast, "f32", False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    check_fused(ts, out, last, fw, g)
+
+
 @pytest.mark.parametrize("l", [5, 300, 2100])
 def test_fused_zoh(l):
     log(f"case fused zoh L={l}")
