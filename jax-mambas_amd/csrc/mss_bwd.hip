@@ -52,31 +52,30 @@ constexpr int bwd_lds_floats(int waves, int bc_bytes) {
   return m;
 }
 
-// Upward (lane i takes lane i - 2^k) scan step of two chains at once: an affine map (P, H)
-// and a plain sum S. Each of the three DPP reads comes two VALU instructions after the
-// write of its source, which is the wait a DPP read needs; the caller pads the first and
-// last step (MSS_DPP_PAD).
-#define MSS_DPP_AFFINE_SUM_STEP(CTRL, RM, H, P, S)                                     \
-  asm volatile("v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
-               "v_add_f32_dpp %2, %2, %2 " CTRL " row_mask:" RM " bank_mask:0xf\n\t"  \
-               "v_mul_f32_dpp %1, %1, %1 " CTRL " row_mask:" RM " bank_mask:0xf"      \
-               : "+v"(H), "+v"(P), "+v"(S))
-#define MSS_DPP_PAD() asm volatile("s_nop 1")
-
 // Inclusive upward scan over the 64 lanes of maps m -> P*m + H (lower lanes applied
 // first: (Pl, Hl) then (Pr, Hr) gives (Pl*Pr, Pr*Hl + Hr), the operator of reference
 // native/selective_scan_cuda.cu:58-63) and of plain sums S. Lane 63 ends with the
-// whole wave's map and sum.
+// whole wave's map and sum. Each step (lane i takes lane i - 2^k) advances the three
+// chains; each DPP read comes two VALU instructions after the write of its source, the
+// wait a DPP read needs, and `s_nop 1` pads the first and last step. One asm statement,
+// so the compiler neither places a write between a pad and the read it guards nor pads
+// between steps itself.
+#define MSS_BWD_SCAN_STEP(CTRL, RM)                                \
+  "v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
+  "v_add_f32_dpp %2, %2, %2 " CTRL " row_mask:" RM " bank_mask:0xf\n\t"  \
+  "v_mul_f32_dpp %1, %1, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t"
 __device__ __forceinline__ void wave_scan_affine_sum(float& P, float& H, float& S) {
-  MSS_DPP_PAD();
-  MSS_DPP_AFFINE_SUM_STEP("row_shr:1", "0xf", H, P, S);
-  MSS_DPP_AFFINE_SUM_STEP("row_shr:2", "0xf", H, P, S);
-  MSS_DPP_AFFINE_SUM_STEP("row_shr:4", "0xf", H, P, S);
-  MSS_DPP_AFFINE_SUM_STEP("row_shr:8", "0xf", H, P, S);
-  MSS_DPP_AFFINE_SUM_STEP("row_bcast:15", "0xa", H, P, S);
-  MSS_DPP_AFFINE_SUM_STEP("row_bcast:31", "0xc", H, P, S);
-  MSS_DPP_PAD();
+  asm volatile("s_nop 1\n\t"                                   //
+               MSS_BWD_SCAN_STEP("row_shr:1", "0xf")            //
+               MSS_BWD_SCAN_STEP("row_shr:2", "0xf")            //
+               MSS_BWD_SCAN_STEP("row_shr:4", "0xf")            //
+               MSS_BWD_SCAN_STEP("row_shr:8", "0xf")            //
+               MSS_BWD_SCAN_STEP("row_bcast:15", "0xa")         //
+               MSS_BWD_SCAN_STEP("row_bcast:31", "0xc")         //
+               "s_nop 1"
+               : "+v"(H), "+v"(P), "+v"(S));
 }
+#undef MSS_BWD_SCAN_STEP
 
 // Sum over the 64 lanes, complete in lane 63 (other lanes hold prefix sums).
 __device__ __forceinline__ float wave_sum_to_last(float v) {

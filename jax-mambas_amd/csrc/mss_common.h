@@ -62,51 +62,32 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-// One Hillis-Steele step of an affine scan with the lane shift fused into the ALU ops:
-//   H = P * H[src] + H ;  P = P[src] * P      (lanes without a source keep their values)
-// `s_nop 1` supplies the two wait states a DPP read needs after a VALU write of its
-// source register (also covering writes just before/after the asm block).
-#define MSS_DPP_AFFINE_STEP(CTRL, RM, H, P)                                            \
-  asm volatile("s_nop 1\n\t"                                                          \
-               "v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
-               "s_nop 1\n\t"                                                          \
-               "v_mul_f32_dpp %1, %1, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
-               "s_nop 1"                                                              \
-               : "+v"(H), "+v"(P))
-
 // Inclusive scan over the 64 lanes (lane order = time order) of affine maps
 // h -> P*h + H. Combining an earlier element (Pl, Hl) with a later one (Pr, Hr) gives
 // (Pl*Pr, Pr*Hl + Hr): the operator of reference native/selective_scan_cuda.cu:58-63.
+// Each Hillis-Steele step fuses the lane shift into the ALU ops:
+//   H = P * H[src] + H ;  P = P[src] * P      (lanes without a source keep their values)
+// A DPP read needs two wait states after a VALU write of its source: each step's reads
+// come after the previous step's write of that register, one VALU instruction and an
+// `s_nop 0`; `s_nop 1` pads the first and the last step. One asm statement, so the
+// compiler neither places a write between a pad and the read it guards nor pads between
+// steps itself.
+#define MSS_FWD_SCAN_STEP(CTRL, RM)                               \
+  "v_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t" \
+  "v_mul_f32_dpp %1, %1, %1 " CTRL " row_mask:" RM " bank_mask:0xf\n\t"  \
+  "s_nop 0\n\t"
 __device__ __forceinline__ void wave_scan_affine_fwd(float& P, float& H) {
-  MSS_DPP_AFFINE_STEP("row_shr:1", "0xf", H, P);
-  MSS_DPP_AFFINE_STEP("row_shr:2", "0xf", H, P);
-  MSS_DPP_AFFINE_STEP("row_shr:4", "0xf", H, P);
-  MSS_DPP_AFFINE_STEP("row_shr:8", "0xf", H, P);
-  MSS_DPP_AFFINE_STEP("row_bcast:15", "0xa", H, P);
-  MSS_DPP_AFFINE_STEP("row_bcast:31", "0xc", H, P);
+  asm volatile("s_nop 1\n\t"                                   //
+               MSS_FWD_SCAN_STEP("row_shr:1", "0xf")            //
+               MSS_FWD_SCAN_STEP("row_shr:2", "0xf")            //
+               MSS_FWD_SCAN_STEP("row_shr:4", "0xf")            //
+               MSS_FWD_SCAN_STEP("row_shr:8", "0xf")            //
+               MSS_FWD_SCAN_STEP("row_bcast:15", "0xa")         //
+               MSS_FWD_SCAN_STEP("row_bcast:31", "0xc")         //
+               "s_nop 1"
+               : "+v"(H), "+v"(P));
 }
-
-// Inclusive reverse scan (lane 63 is applied first) of affine maps m -> a*m + b:
-// lane i ends with R_i = f_i o f_{i+1} o ... o f_63.
-__device__ __forceinline__ void wave_scan_affine_rev(float& a, float& b, int lane) {
-  MSS_DPP_AFFINE_STEP("row_shl:1", "0xf", b, a);
-  MSS_DPP_AFFINE_STEP("row_shl:2", "0xf", b, a);
-  MSS_DPP_AFFINE_STEP("row_shl:4", "0xf", b, a);
-  MSS_DPP_AFFINE_STEP("row_shl:8", "0xf", b, a);
-  // Row r (lanes 16r..16r+15) now holds suffixes within the row; lane 16r holds the
-  // whole row's map. Compose with the rows to the right.
-  const float a1 = readlane(a, 16), b1 = readlane(b, 16);
-  const float a2 = readlane(a, 32), b2 = readlane(b, 32);
-  const float a3 = readlane(a, 48), b3 = readlane(b, 48);
-  // S2 = R2 o R3, S1 = R1 o S2 (uniform values).
-  const float s2a = a2 * a3, s2b = __builtin_fmaf(a2, b3, b2);
-  const float s1a = a1 * s2a, s1b = __builtin_fmaf(a1, s2b, b1);
-  const int row = lane >> 4;
-  const float sa = row == 0 ? s1a : (row == 1 ? s2a : (row == 2 ? a3 : 1.f));
-  const float sb = row == 0 ? s1b : (row == 1 ? s2b : (row == 2 ? b3 : 0.f));
-  b = __builtin_fmaf(a, sb, b);
-  a = a * sa;
-}
+#undef MSS_FWD_SCAN_STEP
 
 // Sum over the 64 lanes; the result is returned uniform.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -216,6 +216,7 @@ void fwd_kernel(FwdParams p) {
       for (int k = 0; k < nb; ++k) {
         const int n = n0 + k;
         const float a2 = s_a2[w][n];
+        const float run = s_run[w][n];  // read early: its wait would otherwise follow the scan
         float a[kT], bu[kT];
         float H = 0.f;
         {
@@ -235,7 +236,6 @@ void fwd_kernel(FwdParams p) {
         }
         float P = fast_exp2(a2 * ssum);
         wave_scan_affine_fwd(P, H);
-        const float run = s_run[w][n];
         const float hend = __builtin_fmaf(P, run, H);  // true state at the lane's last step
         float h = dpp_mov<kWaveShr1, 0xF>(run, hend);   // carry-in (lane 0: running state)
         {
