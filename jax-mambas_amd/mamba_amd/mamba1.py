@@ -422,8 +422,14 @@ class MambaBlock(nn.Module):
         "ssm": (B, d_inner, N)} updated in place (Mamba.step, mamba/mamba1.py:339-363)."""
         weights = weights or _PLAIN
         h, x = self.norm(h, delta, act_dtype)
-        xin = weights.mm(self.in_proj, x)
-        z = weights.mm(self.z_proj, x)
+        w_xz = weights.stacked(self.in_proj, self.z_proj)
+        if w_xz is not None and w_xz.dtype == x.dtype:
+            xz = torch.mm(w_xz, x)  # (2 d_inner, B): [xin; z] in one GEMM
+            di = self.in_proj.shape[0]
+            xin, z = xz[:di], xz[di:]
+        else:
+            xin = weights.mm(self.in_proj, x)
+            z = weights.mm(self.z_proj, x)
         u = causal_conv1d_update(cache["conv"], xin.t(), self.conv_weight, self.conv_bias).t()
         y = self.s6.step(u, z, cache["ssm"], weights, cache.get("A"))
         return h, weights.mm(self.out_proj, y)

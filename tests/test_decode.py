@@ -145,3 +145,27 @@ def test_prefill_and_steps_match_full_forward(euler, complex_ssm):
     for t in range(steps):
         logits = model.step(tokens[:, prompt + t], caches, act_dtype=torch.float32)
         torch.testing.assert_close(logits, full[:, prompt + t], rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.gpu
+def test_prefill_and_steps_bf16_match_full_forward():
+    """The bf16 decode path (shadow weights; in_proj and z_proj as one GEMM) against the
+    bf16 full forward: the same bf16 GEMMs and activations, the scan run chunked in one and
+    one token at a time in the other (float32 states in both), so logits agree to a few
+    bf16 roundings of their scale."""
+    print("case prefill + steps bf16", flush=True)
+    torch.manual_seed(5)
+    model = MambaLM(16, 64, 2, 2, 16, None, 4, device="cuda")
+    g = torch.Generator().manual_seed(7)
+    b, prompt, steps = 3, 37, 6
+    tokens = torch.randint(0, 16, (b, prompt + steps), generator=g).cuda()
+    with torch.no_grad():
+        full = model(tokens, act_dtype=torch.bfloat16).view(b, prompt + steps, -1).float()
+    last, caches = model.prefill(tokens[:, :prompt], act_dtype=torch.bfloat16)
+    scale = full.abs().max().item()
+    assert (last.float() - full[:, prompt - 1]).abs().max().item() <= 3e-2 * scale
+    for t in range(steps):
+        logits = model.step(tokens[:, prompt + t], caches, act_dtype=torch.bfloat16).float()
+        err = (logits - full[:, prompt + t]).abs().max().item()
+        print(f"  step {t}: max abs err {err:.3e} (logit scale {scale:.3e})", flush=True)
+        assert err <= 3e-2 * scale
