@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 4
+#define MSS_ABI_VERSION 5
 #define MSS_MAX_DSTATE 16
 #define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
@@ -249,6 +249,23 @@ typedef struct mss_conv_step_args {
 } mss_conv_step_args;
 
 int mss_conv_step(const mss_conv_step_args* args, void* stream);
+
+/* --- Decode-shaped GEMM: Y = W X. -------------------------------------------------------
+ * No counterpart symbol in the reference (its decode step, mamba/mamba1.py:200-214,
+ * 339-363, runs the block's projections as XLA dot products). W [M][K] bf16 with row
+ * stride ldw (16-byte aligned, ldw >= K, ldw % 8 == 0); X [K][N] bf16 (16-byte aligned)
+ * and Y [M][N] bf16 with rows of N contiguous values; K % 8 == 0; N in {1, 2, 4, 8} and
+ * 2*K*N <= 65536 bytes (X is staged in LDS; MSS_ERR_UNSUPPORTED otherwise). Float32
+ * accumulation, Y rounded to bf16 once. */
+typedef struct mss_gemv_args {
+  int32_t M, K, N;
+  int64_t ldw;
+  const void* W;
+  const void* X;
+  void* Y;
+} mss_gemv_args;
+
+int mss_gemv(const mss_gemv_args* args, void* stream);
 
 /* --- Residual add + RMSNorm over the features of a channel-major stream. ----------
  * No counterpart symbol in the reference (mamba/mamba1.py:300-337 applies

@@ -38,6 +38,7 @@ int norm_blocks(int tokens);
 hipError_t launch_xent(const XentParams& p, bool bwd, bool vec, hipStream_t stream);
 hipError_t launch_ssm_step(const StepParams& p, bool zoh, bool io_bf16, bool bc_bf16, hipStream_t stream);
 hipError_t launch_conv_step(const ConvStepParams& p, bool io_bf16, hipStream_t stream);
+hipError_t launch_gemv(const GemvParams& p, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -621,6 +622,25 @@ int mss_conv_step(const mss_conv_step_args* a, void* stream) {
   p.y = a->y;
   const hipError_t e = mss::launch_conv_step(p, a->io_dtype == MSS_BF16, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching conv step");
+}
+
+int mss_gemv(const mss_gemv_args* a, void* stream) {
+  if (a == nullptr || a->M <= 0 || a->K <= 0 || a->K % 8 != 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->N != 1 && a->N != 2 && a->N != 4 && a->N != 8) return MSS_ERR_UNSUPPORTED;
+  if (a->ldw < a->K || a->ldw % 8 != 0 || !a->W || !a->X || !a->Y) return MSS_ERR_INVALID_ARGUMENT;
+  if (!aligned16(a->W) || !aligned16(a->X) || reinterpret_cast<uintptr_t>(a->Y) % 2 != 0)
+    return MSS_ERR_INVALID_ARGUMENT;
+  if (static_cast<long long>(a->K) * a->N * 2 > 65536) return MSS_ERR_UNSUPPORTED;  // X staged in LDS
+  mss::GemvParams p{};
+  p.M = a->M;
+  p.K = a->K;
+  p.N = a->N;
+  p.ldw = a->ldw;
+  p.W = a->W;
+  p.X = a->X;
+  p.Y = a->Y;
+  const hipError_t e = mss::launch_gemv(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching gemv");
 }
 
 int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,

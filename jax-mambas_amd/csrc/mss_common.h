@@ -309,6 +309,14 @@ struct StepParams {
   void* out;
 };
 
+struct GemvParams {
+  int M, K, N;      // Y [M][N] = W [M][K] X [K][N]
+  long long ldw;    // W row stride (elements)
+  const void* W;    // bf16
+  const void* X;    // bf16, rows of N contiguous values
+  void* Y;          // bf16, rows of N contiguous values
+};
+
 struct ConvStepParams {
   int batch, dim, width, act;
   long long sb, sd;  // strides of x and y

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 4
+MSS_ABI_VERSION = 5
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "mss_scan_step",
     "mss_cscan_step",
     "mss_conv_step",
+    "mss_gemv",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -126,6 +127,10 @@ class StepArgs(ctypes.Structure):
     ]
 
 
+class GemvArgs(ctypes.Structure):
+    _fields_ = [("M", _i32), ("K", _i32), ("N", _i32), ("ldw", ctypes.c_int64), ("W", _p), ("X", _p), ("Y", _p)]
+
+
 class ConvStepArgs(ctypes.Structure):
     _fields_ = [
         ("batch", _i32), ("dim", _i32), ("width", _i32), ("io_dtype", _i32), ("activation", _i32),
@@ -193,6 +198,8 @@ def register_hip_kernel(library_path=None):
         getattr(lib, name).restype = ctypes.c_int
     lib.mss_conv_step.argtypes = [ctypes.POINTER(ConvStepArgs), _p]
     lib.mss_conv_step.restype = ctypes.c_int
+    lib.mss_gemv.argtypes = [ctypes.POINTER(GemvArgs), _p]
+    lib.mss_gemv.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

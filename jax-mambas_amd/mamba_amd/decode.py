@@ -13,6 +13,11 @@ state; output sum_n C Re(state) + D u).
 conv window step of Mamba.step (:339-363): y = act(bias + sum_k weight[:, k] * window[k])
 for window = [conv_state, x]; ``conv_state`` (B, D, K-1) shifts in place.
 
+``gemv(w, x) -> y`` — ``w @ x`` for decode shapes (the block's projections over a few
+tokens): w (M, K) bf16 with 16-byte aligned rows, x (K, N) bf16 contiguous and 16-byte
+aligned with N in {1, 2, 4, 8}, K % 8 == 0, 2*K*N <= 64 KiB; y (M, N) bf16, float32
+accumulation. Other shapes and dtypes go through ``torch.mm``.
+
 Inference only (no autograd); there is no CPU path.
 """
 from __future__ import annotations
@@ -22,7 +27,7 @@ import torch
 from . import _lib
 from .selective_scan_hip import _io_tag, _ptr, _require_gpu, _stream
 
-__all__ = ["selective_state_update", "causal_conv1d_update"]
+__all__ = ["selective_state_update", "causal_conv1d_update", "gemv"]
 
 
 def _strides2(t):
@@ -90,4 +95,19 @@ def causal_conv1d_update(conv_state, x, weight, bias=None, activation="silu"):
                           bias=_ptr(None if bias is None else bias.contiguous()), y=y.data_ptr(),
                           strides=_lib.Strides(io_batch=sb, io_dim=sd))
     _lib.check(lib.mss_conv_step(a, _stream(x)), "mss_conv_step")
+    return y
+
+
+def gemv(w, x):
+    m, k = w.shape
+    if (w.dtype != torch.bfloat16 or x.dtype != torch.bfloat16 or not w.is_cuda or x.device != w.device
+            or x.ndim != 2 or x.shape[0] != k or x.shape[1] not in (1, 2, 4, 8) or k % 8 != 0
+            or not x.is_contiguous() or x.data_ptr() % 16 != 0 or 2 * k * x.shape[1] > 65536
+            or w.stride(1) != 1 or w.stride(0) % 8 != 0 or w.data_ptr() % 16 != 0):
+        return torch.mm(w, x)
+    lib = _lib.register_hip_kernel()
+    n = x.shape[1]
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+    a = _lib.GemvArgs(M=m, K=k, N=n, ldw=w.stride(0), W=w.data_ptr(), X=x.data_ptr(), Y=y.data_ptr())
+    _lib.check(lib.mss_gemv(a, _stream(x)), "mss_gemv")
     return y

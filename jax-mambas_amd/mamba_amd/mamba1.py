@@ -29,7 +29,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from .decode import causal_conv1d_update, selective_state_update
+from .decode import causal_conv1d_update, gemv, selective_state_update
 from .lm_ops import add_rmsnorm
 from .selective_scan_hip import _io_tag, _ptr, _stream, selective_scan_fn
 
@@ -129,6 +129,14 @@ class ShadowWeights:
         """The weight in the activation dtype: its shadow, or a cast of the master."""
         b = self.by_id.get(id(w))
         return b if b is not None and b.dtype == dtype else w.to(dtype)
+
+    def mv(self, w, x):
+        """w @ x for a decode step (no autograd): the decode-shaped HIP GEMM on the shadow of
+        w when x is a few bf16 token columns, else mm."""
+        b = self.by_id.get(id(w))
+        if b is not None and b.dtype == x.dtype and not torch.is_grad_enabled():
+            return gemv(b, x)
+        return self.mm(w, x)
 
     def mm(self, w, x):
         """w @ x: plain autograd in float32, else through the shadow of w."""
@@ -239,8 +247,8 @@ class S6(nn.Module):
         A: the state matrix computed once per generation (recomputed when None)."""
         r, n = self.dt_rank, self.d_state
         weights = weights or _PLAIN
-        x_dbl = weights.mm(self.x_proj, u)
-        dt = weights.mm(self.dt_proj, x_dbl[:r])
+        x_dbl = weights.mv(self.x_proj, u)
+        dt = weights.mv(self.dt_proj, x_dbl[:r])
         A = self.a_matrix() if A is None else A
         y = selective_state_update(
             state, u.t(), dt.t(), A, x_dbl[r:r + n].t(), x_dbl[r + n:].t(),
@@ -424,7 +432,7 @@ class MambaBlock(nn.Module):
         h, x = self.norm(h, delta, act_dtype)
         w_xz = weights.stacked(self.in_proj, self.z_proj)
         if w_xz is not None and w_xz.dtype == x.dtype:
-            xz = torch.mm(w_xz, x)  # (2 d_inner, B): [xin; z] in one GEMM
+            xz = gemv(w_xz, x)  # (2 d_inner, B): [xin; z] in one GEMM
             di = self.in_proj.shape[0]
             xin, z = xz[:di], xz[di:]
         else:
@@ -432,7 +440,7 @@ class MambaBlock(nn.Module):
             z = weights.mm(self.z_proj, x)
         u = causal_conv1d_update(cache["conv"], xin.t(), self.conv_weight, self.conv_bias).t()
         y = self.s6.step(u, z, cache["ssm"], weights, cache.get("A"))
-        return h, weights.mm(self.out_proj, y)
+        return h, weights.mv(self.out_proj, y)
 
 
 class MambaLM(nn.Module):
@@ -494,7 +502,7 @@ class MambaLM(nn.Module):
         for blk, cache in zip(self.blocks, caches):
             h, delta = blk.step(h, delta, cache, act_dtype, weights)
         _, hn = self.final_norm(h, delta, act_dtype)
-        return weights.head(hn, self.embedding)
+        return weights.mv(self.embedding, hn).t()  # (B, vocab) logits of the tied head
 
 
 class GraphedTrainStep:

@@ -6,13 +6,15 @@ float64 oracle scan over the same T steps from the same initial state (fp32 with
 1e-4 / atol 1e-5), causal_conv1d_update against the oracle conv of [prefix, x], and
 MambaLM.prefill + step logits against MambaLM.forward logits on the whole sequence.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
 
 from mamba_amd import _lib
-from mamba_amd.decode import causal_conv1d_update, selective_state_update
+from mamba_amd.decode import causal_conv1d_update, gemv, selective_state_update
 from mamba_amd.mamba1 import MambaLM
 from oracle import mamba1_torch as ref
 from oracle import cscan64, scan64
@@ -169,3 +171,34 @@ def test_prefill_and_steps_bf16_match_full_forward():
         err = (logits - full[:, prompt + t]).abs().max().item()
         print(f"  step {t}: max abs err {err:.3e} (logit scale {scale:.3e})", flush=True)
         assert err <= 3e-2 * scale
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,k,n", [(3072, 768, 8), (768, 1536, 8), (80, 1536, 8), (1536, 48, 8),
+                                   (4099, 768, 4), (5, 8, 1), (257, 136, 2)])
+def test_gemv_matches_float32_product(m, k, n):
+    """The decode-shaped GEMM against the float32 product of the same bf16 operands: each
+    output is one float32 sum over K rounded to bf16 once, so it sits within a bf16
+    rounding (plus float32 reordering) of the reference."""
+    print(f"case gemv M={m} K={k} N={n}", flush=True)
+    g = torch.Generator().manual_seed(m + k + n)
+    w = torch.randn(m, k, generator=g).to(torch.bfloat16).cuda()
+    x = torch.randn(k, n, generator=g).to(torch.bfloat16).cuda()
+    y = gemv(w, x)
+    torch.cuda.synchronize()
+    ref = w.float() @ x.float()
+    assert y.dtype == torch.bfloat16 and y.shape == (m, n)
+    err = (y.float() - ref).abs()
+    bound = 2.0 ** -8 * ref.abs() + 1e-3 * (k ** 0.5)
+    assert bool((err <= bound).all()), f"max err {err.max().item():.3e}"
+
+
+def test_gemv_validation(lib):
+    ok = dict(M=4, K=8, N=8, ldw=8, W=16, X=16, Y=16)
+    assert lib.mss_gemv(None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    for kw, status in ((dict(K=12), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(N=3), _lib.MSS_ERR_UNSUPPORTED),
+                       (dict(K=8192, ldw=8192), _lib.MSS_ERR_UNSUPPORTED), (dict(X=8), _lib.MSS_ERR_INVALID_ARGUMENT),
+                       (dict(ldw=4), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(W=8), _lib.MSS_ERR_INVALID_ARGUMENT),
+                       (dict(M=0), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(Y=None), _lib.MSS_ERR_INVALID_ARGUMENT)):
+        a = dict(ok, **kw)
+        assert lib.mss_gemv(_lib.GemvArgs(**a), None) == status, kw
