@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 5
+#define MSS_ABI_VERSION 6
 #define MSS_MAX_DSTATE 16
 #define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
@@ -266,6 +266,23 @@ typedef struct mss_gemv_args {
 } mss_gemv_args;
 
 int mss_gemv(const mss_gemv_args* args, void* stream);
+
+/* mss_gemv with the next decode step fused behind it (no counterpart symbol in the
+ * reference: Mamba.step, mamba/mamba1.py:339-363, applies the conv window and S6.step,
+ * :200-214, to the projections' outputs). Each entry computes the products exactly as
+ * mss_gemv (rounded to bf16), then, instead of storing some rows of Y, applies the step to
+ * them; the results equal mss_gemv followed by the separate step call, bit for bit.
+ *
+ * mss_gemv_conv_step: rows [0, conv->dim) of W X are conv->x (ignored, may be null) of
+ * mss_conv_step: conv_state and conv->y are updated as that call would, and those rows of
+ * Y are not written (Y may be null when conv->dim == M). conv->batch == N, conv->dim <= M,
+ * io_dtype MSS_BF16.
+ *
+ * mss_gemv_scan_step: W X is step->delta (ignored, may be null) of mss_scan_step (real A):
+ * state and step->out are updated as that call would; Y is not written (may be null).
+ * step->batch == N, step->dim == M, io_dtype and bc_dtype MSS_BF16. */
+int mss_gemv_conv_step(const mss_gemv_args* gemv, const mss_conv_step_args* conv, void* stream);
+int mss_gemv_scan_step(const mss_gemv_args* gemv, const mss_step_args* step, void* stream);
 
 /* --- Residual add + RMSNorm over the features of a channel-major stream. ----------
  * No counterpart symbol in the reference (mamba/mamba1.py:300-337 applies

@@ -555,43 +555,99 @@ int mss_xent_bwd(const mss_xent_args* args, void* stream) {
 }
 
 namespace {
-int run_scan_step(const mss_step_args* a, void* stream, bool cplx) {
+// Validated StepParams of a scan-step call; need_delta false when delta comes from elsewhere.
+int step_params(const mss_step_args* a, bool cplx, bool need_delta, mss::StepParams* p) {
   if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
   int s = check_dims(a->batch, a->dim, 1, a->dstate);
   if (s != MSS_OK) return s;
   s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
   if (s != MSS_OK) return s;
-  if (!a->state || !a->u || !a->delta || !a->A || !a->B || !a->C || !a->out) return MSS_ERR_INVALID_ARGUMENT;
+  if (!a->state || !a->u || (need_delta && !a->delta) || !a->A || !a->B || !a->C || !a->out)
+    return MSS_ERR_INVALID_ARGUMENT;
   if (cplx && (!aligned8(a->state) || !aligned8(a->A))) return MSS_ERR_INVALID_ARGUMENT;
   Strides st;
   // Rows of one step: the per-row "length" is 1.
   s = resolve_strides(a->strides, a->batch, a->dim, 1, a->dstate, &st);
   if (s != MSS_OK) return s;
+  p->batch = a->batch;
+  p->dim = a->dim;
+  p->dstate = a->dstate;
+  p->delta_softplus = a->delta_softplus;
+  p->io_sb = st.io_sb;
+  p->io_sd = st.io_sd;
+  p->bc_sb = st.bc_sb;
+  p->bc_sn = st.bc_sn;
+  p->state = a->state;
+  p->u = a->u;
+  p->delta = a->delta;
+  p->z = a->z;
+  p->B = a->B;
+  p->C = a->C;
+  p->A = a->A;
+  p->D = a->D;
+  p->delta_bias = a->delta_bias;
+  p->out = a->out;
+  return MSS_OK;
+}
+
+int run_scan_step(const mss_step_args* a, void* stream, bool cplx) {
   mss::StepParams p{};
-  p.batch = a->batch;
-  p.dim = a->dim;
-  p.dstate = a->dstate;
-  p.delta_softplus = a->delta_softplus;
-  p.io_sb = st.io_sb;
-  p.io_sd = st.io_sd;
-  p.bc_sb = st.bc_sb;
-  p.bc_sn = st.bc_sn;
-  p.state = a->state;
-  p.u = a->u;
-  p.delta = a->delta;
-  p.z = a->z;
-  p.B = a->B;
-  p.C = a->C;
-  p.A = a->A;
-  p.D = a->D;
-  p.delta_bias = a->delta_bias;
-  p.out = a->out;
+  const int s = step_params(a, cplx, true, &p);
+  if (s != MSS_OK) return s;
   const bool zoh = a->discretization == MSS_ZOH;
   const bool io_bf16 = a->io_dtype == MSS_BF16, bc_bf16 = a->bc_dtype == MSS_BF16;
   const hipStream_t st_ = static_cast<hipStream_t>(stream);
   const hipError_t e = cplx ? mss::launch_cssm_step(p, zoh, io_bf16, bc_bf16, st_)
                             : mss::launch_ssm_step(p, zoh, io_bf16, bc_bf16, st_);
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching scan step");
+}
+
+// Validated ConvStepParams; need_x false when x comes from elsewhere.
+int conv_step_params(const mss_conv_step_args* a, bool need_x, mss::ConvStepParams* p) {
+  if (a == nullptr || a->batch <= 0 || a->dim <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->width < 1 || a->width > 4) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->io_dtype != MSS_F32 && a->io_dtype != MSS_BF16) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->activation != 0 && a->activation != 1) return MSS_ERR_INVALID_ARGUMENT;
+  if ((need_x && !a->x) || !a->weight || !a->y || (a->width > 1 && !a->conv_state))
+    return MSS_ERR_INVALID_ARGUMENT;
+  Strides st;
+  const int s = resolve_strides(a->strides, a->batch, a->dim, 1, 1, &st);
+  if (s != MSS_OK) return s;
+  p->batch = a->batch;
+  p->dim = a->dim;
+  p->width = a->width;
+  p->act = a->activation;
+  p->sb = st.io_sb;
+  p->sd = st.io_sd;
+  p->state = a->conv_state;
+  p->x = a->x;
+  p->w = a->weight;
+  p->bias = a->bias;
+  p->y = a->y;
+  return MSS_OK;
+}
+
+// Validated GemvParams; need_y false when an epilogue replaces every store to Y.
+int gemv_params(const mss_gemv_args* a, bool need_y, mss::GemvParams* p) {
+  if (a == nullptr || a->M <= 0 || a->K <= 0 || a->K % 8 != 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->N != 1 && a->N != 2 && a->N != 4 && a->N != 8) return MSS_ERR_UNSUPPORTED;
+  if (a->ldw < a->K || a->ldw % 8 != 0 || !a->W || !a->X || (need_y && !a->Y)) return MSS_ERR_INVALID_ARGUMENT;
+  if (!aligned16(a->W) || !aligned16(a->X) || reinterpret_cast<uintptr_t>(a->Y) % 2 != 0)
+    return MSS_ERR_INVALID_ARGUMENT;
+  if (static_cast<long long>(a->K) * a->N * 2 > 65536) return MSS_ERR_UNSUPPORTED;  // X staged in LDS
+  p->M = a->M;
+  p->K = a->K;
+  p->N = a->N;
+  p->ldw = a->ldw;
+  p->W = a->W;
+  p->X = a->X;
+  p->Y = a->Y;
+  return MSS_OK;
+}
+
+int run_gemv(const mss::GemvParams& p, void* stream) {
+  const hipError_t e = mss::launch_gemv(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching gemv");
 }
 }  // namespace
 
@@ -600,47 +656,52 @@ int mss_scan_step(const mss_step_args* a, void* stream) { return run_scan_step(a
 int mss_cscan_step(const mss_step_args* a, void* stream) { return run_scan_step(a, stream, true); }
 
 int mss_conv_step(const mss_conv_step_args* a, void* stream) {
-  if (a == nullptr || a->batch <= 0 || a->dim <= 0) return MSS_ERR_INVALID_ARGUMENT;
-  if (a->width < 1 || a->width > 4) return MSS_ERR_INVALID_ARGUMENT;
-  if (a->io_dtype != MSS_F32 && a->io_dtype != MSS_BF16) return MSS_ERR_INVALID_ARGUMENT;
-  if (a->activation != 0 && a->activation != 1) return MSS_ERR_INVALID_ARGUMENT;
-  if (!a->x || !a->weight || !a->y || (a->width > 1 && !a->conv_state)) return MSS_ERR_INVALID_ARGUMENT;
-  Strides st;
-  const int s = resolve_strides(a->strides, a->batch, a->dim, 1, 1, &st);
-  if (s != MSS_OK) return s;
   mss::ConvStepParams p{};
-  p.batch = a->batch;
-  p.dim = a->dim;
-  p.width = a->width;
-  p.act = a->activation;
-  p.sb = st.io_sb;
-  p.sd = st.io_sd;
-  p.state = a->conv_state;
-  p.x = a->x;
-  p.w = a->weight;
-  p.bias = a->bias;
-  p.y = a->y;
+  const int s = conv_step_params(a, true, &p);
+  if (s != MSS_OK) return s;
   const hipError_t e = mss::launch_conv_step(p, a->io_dtype == MSS_BF16, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching conv step");
 }
 
 int mss_gemv(const mss_gemv_args* a, void* stream) {
-  if (a == nullptr || a->M <= 0 || a->K <= 0 || a->K % 8 != 0) return MSS_ERR_INVALID_ARGUMENT;
-  if (a->N != 1 && a->N != 2 && a->N != 4 && a->N != 8) return MSS_ERR_UNSUPPORTED;
-  if (a->ldw < a->K || a->ldw % 8 != 0 || !a->W || !a->X || !a->Y) return MSS_ERR_INVALID_ARGUMENT;
-  if (!aligned16(a->W) || !aligned16(a->X) || reinterpret_cast<uintptr_t>(a->Y) % 2 != 0)
-    return MSS_ERR_INVALID_ARGUMENT;
-  if (static_cast<long long>(a->K) * a->N * 2 > 65536) return MSS_ERR_UNSUPPORTED;  // X staged in LDS
   mss::GemvParams p{};
-  p.M = a->M;
-  p.K = a->K;
-  p.N = a->N;
-  p.ldw = a->ldw;
-  p.W = a->W;
-  p.X = a->X;
-  p.Y = a->Y;
-  const hipError_t e = mss::launch_gemv(p, static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching gemv");
+  const int s = gemv_params(a, true, &p);
+  return s != MSS_OK ? s : run_gemv(p, stream);
+}
+
+int mss_gemv_conv_step(const mss_gemv_args* g, const mss_conv_step_args* c, void* stream) {
+  if (g == nullptr || c == nullptr) return MSS_ERR_INVALID_ARGUMENT;
+  mss::GemvParams p{};
+  int s = gemv_params(g, c->dim < g->M, &p);
+  if (s == MSS_OK) s = conv_step_params(c, false, &p.cs);
+  if (s != MSS_OK) return s;
+  if (c->io_dtype != MSS_BF16 || c->batch != g->N || c->dim > g->M) return MSS_ERR_INVALID_ARGUMENT;
+  // the fused kernel indexes the step's operands with int offsets
+  const long long span = (c->batch - 1LL) * p.cs.sb + (c->dim - 1LL) * p.cs.sd;
+  if (span >= (1LL << 31) || static_cast<long long>(c->batch) * c->dim * c->width >= (1LL << 31))
+    return MSS_ERR_UNSUPPORTED;
+  p.epi = 1;
+  return run_gemv(p, stream);
+}
+
+int mss_gemv_scan_step(const mss_gemv_args* g, const mss_step_args* a, void* stream) {
+  if (g == nullptr || a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
+  mss::GemvParams p{};
+  int s = gemv_params(g, false, &p);
+  if (s == MSS_OK) s = step_params(a, false, false, &p.ss);
+  if (s != MSS_OK) return s;
+  if (a->io_dtype != MSS_BF16 || a->bc_dtype != MSS_BF16 || a->batch != g->N || a->dim != g->M)
+    return MSS_ERR_INVALID_ARGUMENT;
+  // the fused kernel indexes the step's operands with int offsets
+  const mss::StepParams& q = p.ss;
+  const long long io_span = (q.batch - 1LL) * q.io_sb + (q.dim - 1LL) * q.io_sd;
+  const long long bc_span = (q.batch - 1LL) * q.bc_sb + (q.dstate - 1LL) * q.bc_sn;
+  if (io_span >= (1LL << 31) || bc_span >= (1LL << 31) ||
+      static_cast<long long>(q.batch) * q.dim * q.dstate >= (1LL << 31))
+    return MSS_ERR_UNSUPPORTED;
+  p.epi = 2;
+  p.zoh = a->discretization == MSS_ZOH;
+  return run_gemv(p, stream);
 }
 
 int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, int32_t batch,

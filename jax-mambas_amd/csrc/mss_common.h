@@ -309,13 +309,6 @@ struct StepParams {
   void* out;
 };
 
-struct GemvParams {
-  int M, K, N;      // Y [M][N] = W [M][K] X [K][N]
-  long long ldw;    // W row stride (elements)
-  const void* W;    // bf16
-  const void* X;    // bf16, rows of N contiguous values
-  void* Y;          // bf16, rows of N contiguous values
-};
 
 struct ConvStepParams {
   int batch, dim, width, act;
@@ -325,6 +318,21 @@ struct ConvStepParams {
   const float* w;
   const float* bias;  // optional
   void* y;
+};
+
+struct GemvParams {
+  int M, K, N;      // Y [M][N] = W [M][K] X [K][N]
+  long long ldw;    // W row stride (elements)
+  const void* W;    // bf16
+  const void* X;    // bf16, rows of N contiguous values
+  void* Y;          // bf16, rows of N contiguous values
+  // Epilogue over the N tokens of each row (a channel). 0: store Y. 1: rows [0, cs.dim) are
+  // the conv input x of their channel: the conv-window step (cs, x bf16) replaces the store.
+  // 2: row m is the raw delta of channel m: the selective-state step (ss, Euler or ZOH,
+  // bf16 io and B/C) replaces the store.
+  int epi, zoh;
+  ConvStepParams cs;
+  StepParams ss;
 };
 
 struct ConvParams {

@@ -39,35 +39,205 @@ __device__ __forceinline__ void load_xrow(const bf16_t* x, float (&v)[kN]) {
   }
 }
 
-// A workgroup of 4 waves stages X (K x N bf16, at most 64 KB) in LDS once; each
-// wave then produces kR consecutive rows of Y: lane l covers K elements 8l + 512 s
-// (s = 0, 1, ..), reading 16 bytes of each of its kR weight rows per step, and the wave
-// sums over its lanes. Rows past M are clamped to M - 1 for the reads and never stored.
-template <int kN, int kR>
+// s[i] of a register array as a chain of selects. Each candidate goes through an empty
+// asm so that the chain is not folded back into one indexed load, which the compiler
+// would serve from scratch memory.
+template <int kN>
+__device__ __forceinline__ float pick(const float (&s)[kN], int i) {
+  float v = s[0];
+#pragma unroll
+  for (int c = 1; c < kN; ++c) {
+    float sc = s[c];
+    asm("; pick %1" : "+v"(sc) : "n"(c));
+    v = i == c ? sc : v;
+  }
+  return v;
+}
+
+// Offsets into the step operands are int: the entry points reject calls whose operands
+// span 2^31 elements or more.
+//
+// Raw bits of the fused epilogues' operands, loaded before the products so their latency
+// overlaps the weight reads. The loads are unconditional (indexes clamped into range,
+// absent optional operands read from a present one) and the bf16 values stay as bits
+// until after the barrier, so no load waits on its own inside a branch: the vector
+// memory counter is in order, and any such wait would also wait for the weights.
+__device__ __forceinline__ float bits_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+// Conv-window step of channel m for token `lane` (lanes < kN): weights, bias, window.
+struct ConvOperands {
+  float w[4], bias;
+  uint32_t c[3];
+};
+
+__device__ __forceinline__ void load_conv(const ConvStepParams& p, int m, int lane, int n_tok, ConvOperands& o) {
+  const int K = p.width;
+  const int mm = m < p.dim ? m : 0;
+  const int b = lane < n_tok ? lane : 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o.w[k] = p.w[mm * K + min(k, K - 1)];
+  o.bias = p.bias ? p.bias[mm] : 0.f;
+  // width 1 has no window state (the pointer may be null): read the weights instead, unused
+  const uint16_t* cache = K > 1 ? static_cast<const uint16_t*>(p.state) + (b * p.dim + mm) * (K - 1)
+                                : reinterpret_cast<const uint16_t*>(p.w);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) o.c[k] = cache[min(k, max(K - 2, 0))];
+}
+
+// Conv-window step of channel m for token `lane` on x (rounded to bf16): the arithmetic
+// of conv_step_kernel (mss_step.hip): pre = bias + sum_k w[k] window[k] over
+// window = [state, x], y = act(pre), the state shifts left and takes x.
+template <int kN>
+__device__ __forceinline__ void conv_epilogue(const ConvStepParams& p, int m, const float (&s)[kN], int lane,
+                                              const ConvOperands& o) {
+  if (lane >= kN) return;
+  const int K = p.width;
+  bf16_t* cache = static_cast<bf16_t*>(p.state) + (lane * p.dim + m) * (K - 1);
+  const float x = pick<kN>(s, lane);
+  float pre = o.bias;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    if (k < K - 1) {
+      pre = __builtin_fmaf(o.w[k], bits_f32(o.c[k]), pre);
+      if (k > 0) cache[k - 1].bits = static_cast<uint16_t>(o.c[k]);
+    }
+  }
+  pre = __builtin_fmaf(pick<4>(o.w, K - 1), x, pre);
+  if (K > 1) cache[K - 2] = f32_to_bf16(x);
+  const float y = p.act ? pre * sigmoid(pre) : pre;
+  static_cast<bf16_t*>(p.y)[lane * static_cast<int>(p.sb) + m * static_cast<int>(p.sd)] = f32_to_bf16(y);
+}
+
+// Selective-state step of channel d: lanes are (token, state) pairs, 16 lanes (one DPP
+// row) per token, four tokens per pass.
+template <int kP>
+struct SsmOperands {
+  float a[kP], h[kP];
+  uint32_t u[kP], b[kP], c[kP], z[kP];
+  float bias, D;
+};
+
+template <int kN>
+__device__ __forceinline__ void load_ssm(const StepParams& p, int d, int lane, SsmOperands<(kN + 3) / 4>& o) {
+  const int N = p.dstate;
+  const int n = min(lane & 15, N - 1);
+  const uint16_t* U = static_cast<const uint16_t*>(p.u);
+  const uint16_t* Z = static_cast<const uint16_t*>(p.z ? p.z : p.u);
+  const uint16_t* Bm = static_cast<const uint16_t*>(p.B);
+  const uint16_t* Cm = static_cast<const uint16_t*>(p.C);
+  o.bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+  o.D = p.D ? p.D[d] : 0.f;
+#pragma unroll
+  for (int pass = 0; pass < (kN + 3) / 4; ++pass) {
+    const int tok = pass * 4 + (lane >> 4);
+    const int b = tok < kN ? tok : 0;
+    const int io = b * static_cast<int>(p.io_sb) + d * static_cast<int>(p.io_sd);
+    const int bc = b * static_cast<int>(p.bc_sb) + n * static_cast<int>(p.bc_sn);
+    o.u[pass] = U[io];
+    o.z[pass] = Z[io];
+    o.a[pass] = p.A[d * N + n];
+    o.b[pass] = Bm[bc];
+    o.c[pass] = Cm[bc];
+    o.h[pass] = p.state[(b * p.dim + d) * N + n];
+  }
+}
+
+// Selective-state step of channel d on the raw delta (rounded to bf16): the arithmetic of
+// ssm_step_kernel (mss_step.hip): delta = softplus(raw + bias), h = exp(delta A) h +
+// b_bar u, y = sum_n C h + D u, out = y silu(z).
+template <int kN>
+__device__ __forceinline__ void ssm_epilogue(const StepParams& p, bool zoh, int d, const float (&s)[kN], int lane,
+                                             const SsmOperands<(kN + 3) / 4>& o) {
+  const int n = lane & 15;
+  const int N = p.dstate;
+#pragma unroll
+  for (int pass = 0; pass < (kN + 3) / 4; ++pass) {
+    const int tok = pass * 4 + (lane >> 4);
+    const bool ok = tok < kN;
+    const int b = ok ? tok : 0;
+    const float u = bits_f32(o.u[pass]);
+    float dt = pick<kN>(s, b) + o.bias;
+    if (p.delta_softplus) dt = softplus(dt);
+    float yv = 0.f;
+    if (ok && n < N) {
+      const float an = o.a[pass];
+      const float a = fast_exp2(dt * an * kLog2e);
+      const float bn = bits_f32(o.b[pass]);
+      const float bu = zoh ? (expm1f(dt * an) / an) * bn * u : dt * bn * u;
+      const float h = __builtin_fmaf(a, o.h[pass], bu);
+      p.state[(b * p.dim + d) * N + n] = h;
+      yv = bits_f32(o.c[pass]) * h;
+    }
+    yv += dpp_mov<kRowShr1, 0xF>(0.f, yv);
+    yv += dpp_mov<kRowShr2, 0xF>(0.f, yv);
+    yv += dpp_mov<kRowShr4, 0xF>(0.f, yv);
+    yv += dpp_mov<kRowShr8, 0xF>(0.f, yv);
+    if (ok && n == 15) {
+      float y = yv;
+      if (p.D) y = __builtin_fmaf(o.D, u, y);
+      if (p.z) {
+        const float z = bits_f32(o.z[pass]);
+        y *= z * sigmoid(z);
+      }
+      static_cast<bf16_t*>(p.out)[b * static_cast<int>(p.io_sb) + d * static_cast<int>(p.io_sd)] = f32_to_bf16(y);
+    }
+  }
+}
+
+// Weight steps held in registers from before the X barrier: K <= 512 kPre.
+constexpr int kPre = 4;
+
+// A workgroup of 4 waves stages X (K x N bf16, at most 64 KB) in LDS once; each wave
+// produces kR consecutive rows of Y: lane l covers K elements 8l + 512 s (s = 0, 1, ..),
+// reading 16 bytes of each of its kR weight rows per step, and the wave sums over its
+// lanes. The first kPre steps of weights, and a fused epilogue's operands, are loaded
+// before X is staged, so one memory latency covers them all. Rows past M are clamped to
+// M - 1 for the reads and never stored. The row's sums are rounded to bf16 before the
+// epilogue (kEpi, as GemvParams::epi), so a fused epilogue sees the values the separate
+// step kernel would read back from Y.
+template <int kN, int kR, int kEpi>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+  static_assert(kEpi == 0 || kR == 1, "fused epilogues take one row per wave");
   extern __shared__ u32x4 s_x[];
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // wave-uniform row index in a scalar register (the per-channel operands then come
+  // through scalar loads)
+  const int m0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (tid >> 6)) * kR);
+  const bool wave_on = m0 < p.M;
+  const int mc = min(m0, p.M - 1);  // rows past M read row M - 1 (no branch around loads)
+  const bf16_t* __restrict__ W = static_cast<const bf16_t*>(p.W);
+  u32x4 wq[kPre][kR];
+  ConvOperands co;
+  SsmOperands<(kN + 3) / 4> so;
+  if constexpr (kEpi == 1) load_conv(p.cs, mc, lane, kN, co);
+  if constexpr (kEpi == 2) load_ssm<kN>(p.ss, mc, lane, so);
+#pragma unroll
+  for (int st = 0; st < kPre; ++st) {
+    const int k0 = lane * 8 + 512 * st;
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const int m = min(mc + r, p.M - 1);
+      // steps past K re-read the row's first slice (unused)
+      wq[st][r] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + (k0 < p.K ? k0 : 0));
+    }
+  }
   const int n_q = p.K * kN / 8;  // 16-byte words of X (K % 8 == 0)
   const u32x4* __restrict__ xg = static_cast<const u32x4*>(p.X);
   for (int i = tid; i < n_q; i += 256) s_x[i] = xg[i];
   __syncthreads();
-  const int lane = tid & 63;
-  const int m0 = (blockIdx.x * 4 + (tid >> 6)) * kR;
-  if (m0 >= p.M) return;  // wave-uniform, after the only barrier
-  const bf16_t* __restrict__ W = static_cast<const bf16_t*>(p.W);
+  if (!wave_on) return;  // after the only barrier
   const bf16_t* X = reinterpret_cast<const bf16_t*>(s_x);
   float acc[kR][kN];
 #pragma unroll
   for (int r = 0; r < kR; ++r)
 #pragma unroll
     for (int c = 0; c < kN; ++c) acc[r][c] = 0.f;
-  for (int k0 = lane * 8; k0 < p.K; k0 += 512) {
+  auto step = [&](int k0, const u32x4 (&q)[kR]) {
     float w[kR][8];
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
-      const int m = min(m0 + r, p.M - 1);
-      const u32x4 q = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + k0);
-      const uint32_t a[4] = {q.x, q.y, q.z, q.w};
+      const uint32_t a[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         w[r][2 * i] = __uint_as_float(a[i] << 16);
@@ -83,37 +253,76 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll
         for (int c = 0; c < kN; ++c) acc[r][c] = __builtin_fmaf(w[r][e], x[c], acc[r][c]);
     }
+  };
+#pragma unroll
+  for (int st = 0; st < kPre; ++st) {
+    const int k0 = lane * 8 + 512 * st;
+    if (k0 < p.K) step(k0, wq[st]);
+  }
+  for (int k0 = lane * 8 + 512 * kPre; k0 < p.K; k0 += 512) {
+    u32x4 q[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const int m = min(m0 + r, p.M - 1);
+      q[r] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + k0);
+    }
+    step(k0, q);
   }
   bf16_t* __restrict__ Y = static_cast<bf16_t*>(p.Y);
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
+    const int m = m0 + r;
+    float s[kN];  // row m's value for each token, rounded to bf16 (uniform over the wave)
 #pragma unroll
-    for (int c = 0; c < kN; ++c) {
-      const float s = wave_sum(acc[r][c]);
-      if (lane == 0 && m0 + r < p.M) Y[static_cast<size_t>(m0 + r) * kN + c] = f32_to_bf16(s);
+    for (int c = 0; c < kN; ++c) s[c] = to_f32(f32_to_bf16(wave_sum(acc[r][c])));
+    if (m >= p.M) continue;
+    if constexpr (kEpi == 1) {
+      if (m < p.cs.dim) {
+        conv_epilogue<kN>(p.cs, m, s, lane, co);
+        continue;
+      }
     }
+    if constexpr (kEpi == 2) {
+      ssm_epilogue<kN>(p.ss, p.zoh, m, s, lane, so);
+      continue;
+    }
+    if (lane < kN) Y[static_cast<size_t>(m) * kN + lane] = f32_to_bf16(pick<kN>(s, lane));
   }
 }
 
-template <int kN>
+template <int kN, int kEpi>
 static hipError_t launch_gemv_n(const GemvParams& p, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(p.K) * kN * sizeof(bf16_t);
   // 4 rows per wave (X staged once per 16 rows) when that still gives >= 256 workgroups.
-  if (p.M >= 4096) {
-    const int waves = (p.M + 3) / 4;
-    hipLaunchKernelGGL((gemv_kernel<kN, 4>), dim3((waves + 3) / 4), dim3(256), lds, stream, p);
-  } else {
-    hipLaunchKernelGGL((gemv_kernel<kN, 1>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
+  if constexpr (kEpi == 0) {
+    if (p.M >= 4096) {
+      const int waves = (p.M + 3) / 4;
+      hipLaunchKernelGGL((gemv_kernel<kN, 4, kEpi>), dim3((waves + 3) / 4), dim3(256), lds, stream, p);
+      return hipGetLastError();
+    }
+  }
+  {
+    hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_gemv(const GemvParams& p, hipStream_t stream) {
+template <int kEpi>
+static hipError_t launch_gemv_e(const GemvParams& p, hipStream_t stream) {
   switch (p.N) {
-    case 1: return launch_gemv_n<1>(p, stream);
-    case 2: return launch_gemv_n<2>(p, stream);
-    case 4: return launch_gemv_n<4>(p, stream);
-    case 8: return launch_gemv_n<8>(p, stream);
+    case 1: return launch_gemv_n<1, kEpi>(p, stream);
+    case 2: return launch_gemv_n<2, kEpi>(p, stream);
+    case 4: return launch_gemv_n<4, kEpi>(p, stream);
+    case 8: return launch_gemv_n<8, kEpi>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv(const GemvParams& p, hipStream_t stream) {
+  switch (p.epi) {
+    case 0: return launch_gemv_e<0>(p, stream);
+    case 1: return launch_gemv_e<1>(p, stream);
+    case 2: return launch_gemv_e<2>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }

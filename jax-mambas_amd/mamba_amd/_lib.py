@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 5
+MSS_ABI_VERSION = 6
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -52,6 +52,8 @@ EXPORTED_SYMBOLS = (
     "mss_cscan_step",
     "mss_conv_step",
     "mss_gemv",
+    "mss_gemv_conv_step",
+    "mss_gemv_scan_step",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -200,6 +202,10 @@ def register_hip_kernel(library_path=None):
     lib.mss_conv_step.restype = ctypes.c_int
     lib.mss_gemv.argtypes = [ctypes.POINTER(GemvArgs), _p]
     lib.mss_gemv.restype = ctypes.c_int
+    lib.mss_gemv_conv_step.argtypes = [ctypes.POINTER(GemvArgs), ctypes.POINTER(ConvStepArgs), _p]
+    lib.mss_gemv_conv_step.restype = ctypes.c_int
+    lib.mss_gemv_scan_step.argtypes = [ctypes.POINTER(GemvArgs), ctypes.POINTER(StepArgs), _p]
+    lib.mss_gemv_scan_step.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

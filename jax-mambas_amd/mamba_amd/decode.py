@@ -18,6 +18,12 @@ tokens): w (M, K) bf16 with 16-byte aligned rows, x (K, N) bf16 contiguous and 1
 aligned with N in {1, 2, 4, 8}, K % 8 == 0, 2*K*N <= 64 KiB; y (M, N) bf16, float32
 accumulation. Other shapes and dtypes go through ``torch.mm``.
 
+``gemv_conv_update(w, x, conv_state, weight, bias=None) -> (u, rest)`` and
+``gemv_state_update(w, x, state, u, A, B, C, ...) -> out`` — a decode GEMM with the next
+step fused behind it (one kernel instead of two): the conv window step on the first D
+rows of ``w @ x`` (the in-projection), and the selective-state step with ``w @ x`` as the
+raw delta (the dt projection). Same results as ``gemv`` followed by the step call.
+
 Inference only (no autograd); there is no CPU path.
 """
 from __future__ import annotations
@@ -27,7 +33,7 @@ import torch
 from . import _lib
 from .selective_scan_hip import _io_tag, _ptr, _require_gpu, _stream
 
-__all__ = ["selective_state_update", "causal_conv1d_update", "gemv"]
+__all__ = ["selective_state_update", "causal_conv1d_update", "gemv", "gemv_conv_update", "gemv_state_update"]
 
 
 def _strides2(t):
@@ -38,8 +44,9 @@ def _strides2(t):
     return sb, sx
 
 
-def selective_state_update(state, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=True,
-                           discretization="euler"):
+def _step_args(state, u, delta, A, B, C, D, z, delta_bias, delta_softplus, discretization):
+    """Checked StepArgs, the output tensor and the tensors the call must keep alive;
+    delta None when the raw delta comes from a fused GEMM."""
     cplx = A.is_complex()
     sdt, adt = (torch.complex64, torch.complex64) if cplx else (torch.float32, torch.float32)
     if state.dtype != sdt or state.ndim != 3 or not state.is_contiguous():
@@ -58,27 +65,35 @@ def selective_state_update(state, u, delta, A, B, C, D=None, z=None, delta_bias=
     if A.dtype != adt or tuple(A.shape) != (dim, n):
         raise ValueError(f"A must be {adt} ({dim}, {n})")
     _require_gpu(state, u, delta, A, B, C, D, z, delta_bias)
-    lib = _lib.register_hip_kernel()
     out = torch.empty_strided(u.shape, u.stride(), dtype=u.dtype, device=u.device)
     io_b, io_d = _strides2(u)
     bc_b, bc_n = _strides2(B)
-    Ac = A.contiguous()  # complex A and state: interleaved (real, imaginary) float32 pairs
+    keep = (A.contiguous(),  # complex A and state: interleaved (real, imaginary) float32 pairs
+            None if D is None else D.contiguous(), None if delta_bias is None else delta_bias.contiguous())
     a = _lib.StepArgs(batch=batch, dim=dim, dstate=n,
                       discretization=_lib.MSS_ZOH if discretization == "zoh" else _lib.MSS_EULER,
                       delta_softplus=int(bool(delta_softplus)), io_dtype=_io_tag(u.dtype, "u"),
                       bc_dtype=_io_tag(B.dtype, "B"), state=state.data_ptr(), u=u.data_ptr(),
-                      delta=delta.data_ptr(), A=Ac.data_ptr(), B=B.data_ptr(), C=C.data_ptr(),
-                      D=_ptr(None if D is None else D.contiguous()), z=_ptr(z),
-                      delta_bias=_ptr(None if delta_bias is None else delta_bias.contiguous()), out=out.data_ptr(),
+                      delta=_ptr(delta), A=keep[0].data_ptr(), B=B.data_ptr(), C=C.data_ptr(),
+                      D=_ptr(keep[1]), z=_ptr(z), delta_bias=_ptr(keep[2]), out=out.data_ptr(),
                       strides=_lib.Strides(io_batch=io_b, io_dim=io_d, bc_batch=bc_b, bc_state=bc_n))
-    if cplx:
+    return a, out, keep
+
+
+def selective_state_update(state, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=True,
+                           discretization="euler"):
+    a, out, keep = _step_args(state, u, delta, A, B, C, D, z, delta_bias, delta_softplus, discretization)
+    lib = _lib.register_hip_kernel()
+    if A.is_complex():
         _lib.check(lib.mss_cscan_step(a, _stream(u)), "mss_cscan_step")
     else:
         _lib.check(lib.mss_scan_step(a, _stream(u)), "mss_scan_step")
     return out
 
 
-def causal_conv1d_update(conv_state, x, weight, bias=None, activation="silu"):
+def _conv_step_args(conv_state, x, weight, bias, activation, y):
+    """Checked ConvStepArgs writing y (x's shape and strides); x may be a shape-only
+    stand-in when the conv input comes from a fused GEMM."""
     batch, dim = x.shape
     k = weight.shape[1]
     if tuple(conv_state.shape) != (batch, dim, k - 1) or conv_state.dtype != x.dtype or not conv_state.is_contiguous():
@@ -86,28 +101,77 @@ def causal_conv1d_update(conv_state, x, weight, bias=None, activation="silu"):
     if weight.dtype != torch.float32 or not 1 <= k <= 4:
         raise ValueError("weight must be float32 (D, K) with K <= 4")
     _require_gpu(conv_state, x, weight, bias)
-    lib = _lib.register_hip_kernel()
-    y = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
     sb, sd = _strides2(x)
+    keep = (weight.contiguous(), None if bias is None else bias.contiguous())
     a = _lib.ConvStepArgs(batch=batch, dim=dim, width=k, io_dtype=_io_tag(x.dtype, "x"),
                           activation=1 if activation == "silu" else 0, conv_state=conv_state.data_ptr(),
-                          x=x.data_ptr(), weight=weight.contiguous().data_ptr(),
-                          bias=_ptr(None if bias is None else bias.contiguous()), y=y.data_ptr(),
+                          x=x.data_ptr(), weight=keep[0].data_ptr(), bias=_ptr(keep[1]), y=y.data_ptr(),
                           strides=_lib.Strides(io_batch=sb, io_dim=sd))
+    return a, keep
+
+
+def causal_conv1d_update(conv_state, x, weight, bias=None, activation="silu"):
+    y = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+    a, keep = _conv_step_args(conv_state, x, weight, bias, activation, y)
+    lib = _lib.register_hip_kernel()
     _lib.check(lib.mss_conv_step(a, _stream(x)), "mss_conv_step")
     return y
 
 
-def gemv(w, x):
+def _gemv_ok(w, x):
+    """Whether mss_gemv takes w @ x (bf16, a few token columns, aligned, X fits in LDS)."""
     m, k = w.shape
-    if (w.dtype != torch.bfloat16 or x.dtype != torch.bfloat16 or not w.is_cuda or x.device != w.device
-            or x.ndim != 2 or x.shape[0] != k or x.shape[1] not in (1, 2, 4, 8) or k % 8 != 0
-            or not x.is_contiguous() or x.data_ptr() % 16 != 0 or 2 * k * x.shape[1] > 65536
-            or w.stride(1) != 1 or w.stride(0) % 8 != 0 or w.data_ptr() % 16 != 0):
+    return not (w.dtype != torch.bfloat16 or x.dtype != torch.bfloat16 or not w.is_cuda or x.device != w.device
+                or x.ndim != 2 or x.shape[0] != k or x.shape[1] not in (1, 2, 4, 8) or k % 8 != 0
+                or not x.is_contiguous() or x.data_ptr() % 16 != 0 or 2 * k * x.shape[1] > 65536
+                or w.stride(1) != 1 or w.stride(0) % 8 != 0 or w.data_ptr() % 16 != 0)
+
+
+def _gemv_args(w, x, y):
+    m, k = w.shape
+    return _lib.GemvArgs(M=m, K=k, N=x.shape[1], ldw=w.stride(0), W=w.data_ptr(), X=x.data_ptr(),
+                         Y=_ptr(y))
+
+
+def gemv(w, x):
+    """w @ x for a decode step: the HIP decode GEMM (bf16 in and out, float32 sums) where it
+    applies, else torch.mm."""
+    if not _gemv_ok(w, x):
         return torch.mm(w, x)
     lib = _lib.register_hip_kernel()
-    n = x.shape[1]
-    y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
-    a = _lib.GemvArgs(M=m, K=k, N=n, ldw=w.stride(0), W=w.data_ptr(), X=x.data_ptr(), Y=y.data_ptr())
-    _lib.check(lib.mss_gemv(a, _stream(x)), "mss_gemv")
+    y = torch.empty(w.shape[0], x.shape[1], dtype=torch.bfloat16, device=x.device)
+    _lib.check(lib.mss_gemv(_gemv_args(w, x, y), _stream(x)), "mss_gemv")
     return y
+
+
+def gemv_conv_update(w, x, conv_state, weight, bias=None, activation="silu"):
+    """(u, rest) for v = w @ x (rows, tokens) whose first D rows are the conv input of a
+    decode step: u = causal_conv1d_update(conv_state, v[:D].t(), weight, bias).t() (D, B)
+    and rest = v[D:]. One fused HIP kernel where the GEMM applies, else the two calls."""
+    dim = weight.shape[0]
+    if not _gemv_ok(w, x) or conv_state.dtype != torch.bfloat16 or not dim <= w.shape[0]:
+        v = gemv(w, x)
+        return causal_conv1d_update(conv_state, v[:dim].t(), weight, bias, activation).t(), v[dim:]
+    n = x.shape[1]
+    u = torch.empty(dim, n, dtype=torch.bfloat16, device=x.device)
+    v = torch.empty(w.shape[0], n, dtype=torch.bfloat16, device=x.device)
+    a, keep = _conv_step_args(conv_state, u.t(), weight, bias, activation, u.t())
+    a.x = None
+    lib = _lib.register_hip_kernel()
+    _lib.check(lib.mss_gemv_conv_step(_gemv_args(w, x, v), a, _stream(x)), "mss_gemv_conv_step")
+    return u, v[dim:]
+
+
+def gemv_state_update(w, x, state, u, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=True,
+                      discretization="euler"):
+    """selective_state_update(state, u, (w @ x).t(), ...): the raw delta of a decode step
+    as a GEMM, fused with the state update in one HIP kernel where the GEMM applies (real
+    A, bf16 u and B), else the two calls."""
+    if (not _gemv_ok(w, x) or A.is_complex() or u.dtype != torch.bfloat16 or B.dtype != torch.bfloat16
+            or w.shape[0] != u.shape[1] or x.shape[1] != u.shape[0]):
+        return selective_state_update(state, u, gemv(w, x).t(), A, B, C, D, z, delta_bias, delta_softplus,
+                                      discretization)
+    a, out, keep = _step_args(state, u, None, A, B, C, D, z, delta_bias, delta_softplus, discretization)
+    lib = _lib.register_hip_kernel()
+    _lib.check(lib.mss_gemv_scan_step(_gemv_args(w, x, None), a, _stream(x)), "mss_gemv_scan_step")
+    return out

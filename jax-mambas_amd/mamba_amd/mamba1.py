@@ -29,7 +29,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from .decode import causal_conv1d_update, gemv, selective_state_update
+from .decode import causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update, selective_state_update
 from .lm_ops import add_rmsnorm
 from .selective_scan_hip import _io_tag, _ptr, _stream, selective_scan_fn
 
@@ -124,6 +124,10 @@ class ShadowWeights:
                 return None
             rows += w.shape[0]
         return self.flat[o:o + rows * ws[0].shape[1]].view(rows, ws[0].shape[1])
+
+    def shadow(self, w):
+        """The low-precision copy of w, or None."""
+        return self.by_id.get(id(w))
 
     def act(self, w, dtype):
         """The weight in the activation dtype: its shadow, or a cast of the master."""
@@ -248,12 +252,16 @@ class S6(nn.Module):
         r, n = self.dt_rank, self.d_state
         weights = weights or _PLAIN
         x_dbl = weights.mv(self.x_proj, u)
-        dt = weights.mv(self.dt_proj, x_dbl[:r])
         A = self.a_matrix() if A is None else A
-        y = selective_state_update(
-            state, u.t(), dt.t(), A, x_dbl[r:r + n].t(), x_dbl[r + n:].t(),
-            D=None if self.D is None else self.D.float(), z=None if z is None else z.t(),
-            delta_bias=self.dt_bias.float(), delta_softplus=True, discretization=self.discretization)
+        args = (A, x_dbl[r:r + n].t(), x_dbl[r + n:].t())
+        kw = dict(D=None if self.D is None else self.D.float(), z=None if z is None else z.t(),
+                  delta_bias=self.dt_bias.float(), delta_softplus=True, discretization=self.discretization)
+        w_dt = weights.shadow(self.dt_proj)
+        if w_dt is not None and w_dt.dtype == u.dtype and not torch.is_grad_enabled():
+            y = gemv_state_update(w_dt, x_dbl[:r], state, u.t(), *args, **kw)  # dt GEMM + state step
+        else:
+            dt = weights.mv(self.dt_proj, x_dbl[:r])
+            y = selective_state_update(state, u.t(), dt.t(), *args, **kw)
         return y.t()
 
 
@@ -432,13 +440,12 @@ class MambaBlock(nn.Module):
         h, x = self.norm(h, delta, act_dtype)
         w_xz = weights.stacked(self.in_proj, self.z_proj)
         if w_xz is not None and w_xz.dtype == x.dtype:
-            xz = gemv(w_xz, x)  # (2 d_inner, B): [xin; z] in one GEMM
-            di = self.in_proj.shape[0]
-            xin, z = xz[:di], xz[di:]
+            # [xin; z] in one GEMM, the conv window step fused on the xin rows
+            u, z = gemv_conv_update(w_xz, x, cache["conv"], self.conv_weight, self.conv_bias)
         else:
             xin = weights.mm(self.in_proj, x)
             z = weights.mm(self.z_proj, x)
-        u = causal_conv1d_update(cache["conv"], xin.t(), self.conv_weight, self.conv_bias).t()
+            u = causal_conv1d_update(cache["conv"], xin.t(), self.conv_weight, self.conv_bias).t()
         y = self.s6.step(u, z, cache["ssm"], weights, cache.get("A"))
         return h, weights.mv(self.out_proj, y)
 

@@ -14,7 +14,8 @@ import torch
 import torch.nn.functional as F
 
 from mamba_amd import _lib
-from mamba_amd.decode import causal_conv1d_update, gemv, selective_state_update
+from mamba_amd.decode import (causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update,
+                              selective_state_update)
 from mamba_amd.mamba1 import MambaLM
 from oracle import mamba1_torch as ref
 from oracle import cscan64, scan64
@@ -202,3 +203,90 @@ def test_gemv_validation(lib):
                        (dict(M=0), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(Y=None), _lib.MSS_ERR_INVALID_ARGUMENT)):
         a = dict(ok, **kw)
         assert lib.mss_gemv(_lib.GemvArgs(**a), None) == status, kw
+
+
+def test_fused_step_validation(lib):
+    """mss_gemv_conv_step / mss_gemv_scan_step check their shapes against each other (CPU,
+    invalid arguments only: nothing is launched)."""
+    g = _lib.GemvArgs(M=32, K=8, N=4, ldw=8, W=16, X=16, Y=16)
+    conv = dict(batch=4, dim=16, width=4, io_dtype=_lib.MSS_BF16, activation=1, conv_state=16, x=None,
+                weight=16, bias=None, y=16)
+    assert lib.mss_gemv_conv_step(None, _lib.ConvStepArgs(**conv), None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_gemv_conv_step(g, None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    for kw in (dict(batch=2), dict(dim=33), dict(io_dtype=_lib.MSS_F32), dict(y=None), dict(width=5)):
+        assert lib.mss_gemv_conv_step(g, _lib.ConvStepArgs(**dict(conv, **kw)), None) == \
+            _lib.MSS_ERR_INVALID_ARGUMENT, kw
+    # Y is needed for the rows past the conv's
+    g_noy = _lib.GemvArgs(M=32, K=8, N=4, ldw=8, W=16, X=16, Y=None)
+    assert lib.mss_gemv_conv_step(g_noy, _lib.ConvStepArgs(**conv), None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    step = dict(batch=4, dim=32, dstate=16, discretization=_lib.MSS_EULER, delta_softplus=1,
+                io_dtype=_lib.MSS_BF16, bc_dtype=_lib.MSS_BF16, state=16, u=16, delta=None, A=16, B=16, C=16,
+                out=16)
+    assert lib.mss_gemv_scan_step(g, None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    for kw in (dict(batch=8), dict(dim=16), dict(io_dtype=_lib.MSS_F32), dict(bc_dtype=_lib.MSS_F32),
+               dict(out=None), dict(discretization=7)):
+        assert lib.mss_gemv_scan_step(g, _lib.StepArgs(**dict(step, **kw)), None) == \
+            _lib.MSS_ERR_INVALID_ARGUMENT, kw
+    assert lib.mss_gemv_scan_step(g, _lib.StepArgs(**dict(step, dstate=17)), None) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_gemv_scan_step(_lib.GemvArgs(M=32, K=8, N=3, ldw=8, W=16, X=16), _lib.StepArgs(**step),
+                                  None) == _lib.MSS_ERR_UNSUPPORTED
+
+
+def _bf16(*shape, scale=1.0, device="cuda"):
+    return (torch.randn(*shape, device=device) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 2, 4, 8])
+@pytest.mark.parametrize("k,act,extra", [(4, "silu", 96), (2, None, 0), (1, "silu", 8), (3, "silu", 40)])
+def test_gemv_conv_update_matches_separate_calls(n, k, act, extra):
+    """GEMM + fused conv window step == gemv then causal_conv1d_update, bit for bit, over
+    three steps in a row (the window state carries between them)."""
+    torch.manual_seed(n * 10 + k)
+    dim, kin = 200, 136
+    w = _bf16(dim + extra, kin, scale=kin ** -0.5)
+    weight = torch.randn(dim, k, device="cuda") * 0.5
+    bias = torch.randn(dim, device="cuda") * 0.1 if act else None
+    s_fused = _bf16(n, dim, k - 1)
+    s_ref = s_fused.clone()
+    for _ in range(3):
+        x = _bf16(kin, n)
+        v = gemv(w, x)
+        u_ref = causal_conv1d_update(s_ref, v[:dim].t(), weight, bias, act or "none").t()
+        u, rest = gemv_conv_update(w, x, s_fused, weight, bias, act or "none")
+        assert tuple(u.shape) == (dim, n) and tuple(rest.shape) == (extra, n)
+        assert torch.equal(u, u_ref)
+        assert torch.equal(rest, v[dim:])
+        assert torch.equal(s_fused, s_ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 2, 4, 8])
+@pytest.mark.parametrize("zoh,with_dz,dstate", [(False, True, 16), (True, True, 16), (False, False, 5),
+                                                (True, False, 11)])
+def test_gemv_state_update_matches_separate_calls(n, zoh, with_dz, dstate):
+    """dt GEMM + fused selective-state step == gemv then selective_state_update, bit for
+    bit, over three steps in a row (the state carries between them), with the model's
+    (features, batch) activation layouts."""
+    torch.manual_seed(n * 100 + dstate)
+    dim, rank = 160, 48
+    disc = "zoh" if zoh else "euler"
+    w = _bf16(dim, rank, scale=rank ** -0.5)
+    A = -torch.rand(dim, dstate, device="cuda") * 4 - 0.1
+    D = torch.randn(dim, device="cuda") if with_dz else None
+    bias = torch.randn(dim, device="cuda") * 0.5 if with_dz else None
+    st_fused = torch.randn(n, dim, dstate, device="cuda")
+    st_ref = st_fused.clone()
+    for _ in range(3):
+        x = _bf16(rank, n)
+        u = _bf16(dim, n)
+        z = _bf16(dim, n) if with_dz else None
+        bc = _bf16(2 * dstate, n)
+        Bt, Ct = bc[:dstate].t(), bc[dstate:].t()
+        dt = gemv(w, x)
+        y_ref = selective_state_update(st_ref, u.t(), dt.t(), A, Bt, Ct, D, None if z is None else z.t(), bias,
+                                       True, disc)
+        y = gemv_state_update(w, x, st_fused, u.t(), A, Bt, Ct, D, None if z is None else z.t(), bias, True,
+                              disc)
+        assert torch.equal(y, y_ref)
+        assert torch.equal(st_fused, st_ref)
