@@ -184,8 +184,6 @@ __device__ __forceinline__ void ssm_epilogue(const StepParams& p, bool zoh, int 
   }
 }
 
-// Weight steps held in registers from before the X barrier: K <= 512 kPre.
-constexpr int kPre = 4;
 
 // A workgroup of 4 waves stages X (K x N bf16, at most 64 KB) in LDS once; each wave
 // produces kR consecutive rows of Y: lane l covers K elements 8l + 512 s (s = 0, 1, ..),
@@ -195,7 +193,7 @@ constexpr int kPre = 4;
 // M - 1 for the reads and never stored. The row's sums are rounded to bf16 before the
 // epilogue (kEpi, as GemvParams::epi), so a fused epilogue sees the values the separate
 // step kernel would read back from Y.
-template <int kN, int kR, int kEpi>
+template <int kN, int kR, int kEpi, int kPre>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   static_assert(kEpi == 0 || kR == 1, "fused epilogues take one row per wave");
   extern __shared__ u32x4 s_x[];
@@ -290,21 +288,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   }
 }
 
-template <int kN, int kEpi>
-static hipError_t launch_gemv_n(const GemvParams& p, hipStream_t stream) {
+template <int kN, int kEpi, int kPre>
+static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(p.K) * kN * sizeof(bf16_t);
   // 4 rows per wave (X staged once per 16 rows) when that still gives >= 256 workgroups.
   if constexpr (kEpi == 0) {
     if (p.M >= 4096) {
       const int waves = (p.M + 3) / 4;
-      hipLaunchKernelGGL((gemv_kernel<kN, 4, kEpi>), dim3((waves + 3) / 4), dim3(256), lds, stream, p);
+      hipLaunchKernelGGL((gemv_kernel<kN, 4, kEpi, kPre>), dim3((waves + 3) / 4), dim3(256), lds, stream, p);
       return hipGetLastError();
     }
   }
-  {
-    hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
-  }
+  hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi, kPre>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
   return hipGetLastError();
+}
+
+// Weight steps (512 elements of K each) loaded into registers before the X barrier: all
+// of them up to K = 2048, the rest streamed after it.
+template <int kN, int kEpi>
+static hipError_t launch_gemv_n(const GemvParams& p, hipStream_t stream) {
+  switch (min((p.K + 511) / 512, 4)) {
+    case 1: return launch_gemv_p<kN, kEpi, 1>(p, stream);
+    case 2: return launch_gemv_p<kN, kEpi, 2>(p, stream);
+    case 3: return launch_gemv_p<kN, kEpi, 3>(p, stream);
+    default: return launch_gemv_p<kN, kEpi, 4>(p, stream);
+  }
 }
 
 template <int kEpi>
