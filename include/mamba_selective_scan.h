@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 6
+#define MSS_ABI_VERSION 7
 #define MSS_MAX_DSTATE 16
 #define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
@@ -137,6 +137,14 @@ typedef struct mss_bwd_args {
 /* Size of the scratch mss_bwd needs for these shapes and for whether seq_lens is given
  * (0 on invalid arguments). */
 size_t mss_bwd_workspace_bytes(const mss_bwd_args* args);
+
+/* Launch plan of the backward scan kernel for these shapes (varlen: seq_lens given):
+ * waves per workgroup and channels one workgroup walks. The plan depends on the shapes
+ * only, so a caller (or a test) can tell which kernel variant a configuration runs. No
+ * counterpart in the reference, whose backward launch shape is fixed by its traits
+ * (native/upstream_mamba/selective_scan_bwd_kernel.cuh:499-535). */
+int mss_bwd_plan(int32_t batch, int32_t dim, int32_t dstate, int32_t varlen, int32_t* waves,
+                 int32_t* chan_per_block);
 
 int mss_fwd(const mss_fwd_args* args, void* stream);
 int mss_bwd(const mss_bwd_args* args, void* stream);

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 6
+MSS_ABI_VERSION = 7
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -30,6 +30,7 @@ MSS_REF_CHUNK = 2048
 # Every symbol include/mamba_selective_scan.h declares.
 EXPORTED_SYMBOLS = (
     "mss_bwd_workspace_bytes",
+    "mss_bwd_plan",
     "mss_fwd",
     "mss_bwd",
     "mss_bwd_scan",
@@ -176,6 +177,8 @@ def register_hip_kernel(library_path=None):
     for name in ("mss_bwd_workspace_bytes", "mss_cbwd_workspace_bytes"):
         getattr(lib, name).argtypes = [ctypes.POINTER(BwdArgs)]
         getattr(lib, name).restype = ctypes.c_size_t
+    lib.mss_bwd_plan.argtypes = [_i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
+    lib.mss_bwd_plan.restype = ctypes.c_int
     lib.mss_scan_fwd.argtypes = [_p, _i32, _i32, _i32, _i32, _i32] + [_p] * 9
     lib.mss_scan_fwd.restype = ctypes.c_int
     lib.mss_scan_fwd_repeat.argtypes = [_p, _i32, _i32, _i32, _i32, _i32, _i32] + [_p] * 9
@@ -232,6 +235,15 @@ class MSSError(RuntimeError):
             msg += ": " + lib.mss_last_hip_error().decode()
         super().__init__(f"{op} failed with status {status}: {msg}")
         self.status = status
+
+
+def bwd_plan(batch, dim, dstate, varlen=False):
+    """(waves per workgroup, channels per workgroup) of the backward scan for these shapes."""
+    lib = register_hip_kernel()
+    w, c = _i32(), _i32()
+    check(lib.mss_bwd_plan(batch, dim, dstate, int(bool(varlen)), ctypes.byref(w), ctypes.byref(c)),
+          "mss_bwd_plan")
+    return w.value, c.value
 
 
 def check(status, op):

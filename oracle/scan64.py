@@ -127,12 +127,16 @@ def forward(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=F
 
 def backward(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_softplus=False,
              initial_state=None, seq_lens=None, discretization="euler", dlast_state=None,
-             segment=64):
+             segment=64, abs_terms=False):
     """Gradients of out (and last_state) w.r.t. every input, float64.
 
     Returns dict(du, ddelta, dA, dB, dC, dD, dz, ddelta_bias, dinitial_state); entries for
     absent optional inputs are None. Forward states are recomputed from checkpoints every
     ``segment`` steps, so memory stays O(B*D*N*(L/segment + segment)).
+    With ``abs_terms`` the dict also holds, for each reduction gradient, the sum of the
+    absolute values of the terms it adds up (``dA_abs``, ``dB_abs``, ``dC_abs``,
+    ``dD_abs``, ``ddelta_bias_abs``): the scale that bounds the rounding error of any
+    order of summation of those terms.
     """
     zoh = discretization == "zoh"
     fw = forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, initial_state, seq_lens,
@@ -155,6 +159,10 @@ def backward(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_sof
     dA = np.zeros((dim, n))
     dB = np.zeros((bsz, n, L))
     dC = np.zeros((bsz, n, L))
+    ddl_a = np.zeros((bsz, dim, L))
+    dA_a = np.zeros((dim, n))
+    dB_a = np.zeros((bsz, n, L))
+    dC_a = np.zeros((bsz, n, L))
     ckpt = fw["checkpoints"]
     seg_starts = sorted(ckpt.keys())
     for s0 in reversed(seg_starts):
@@ -176,35 +184,63 @@ def backward(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_sof
             dl_t = dl[:, :, t]
             u_t = u[:, :, t]
             B_t = B[:, None, :, t]
+            q = lam * (A[None] * a_bar * h_prev)
             if zoh:
                 du[:, :, t] += np.sum(lam * B_t * E, axis=2)
-                ddl[:, :, t] += np.sum(lam * (A[None] * a_bar * h_prev + B_t * u_t[:, :, None] * a_bar), axis=2)
+                r = lam * B_t * u_t[:, :, None] * a_bar
+                ddl[:, :, t] += np.sum(q + r, axis=2)
                 dEdA = (dl_t[:, :, None] * A[None] * a_bar - np.expm1(dl_t[:, :, None] * A[None])) / (A[None] ** 2)
-                dA += np.sum(lam * (dl_t[:, :, None] * a_bar * h_prev + B_t * u_t[:, :, None] * dEdA), axis=0)
-                dB[:, :, t] += np.sum(lam * E * u_t[:, :, None], axis=1)
+                ta = lam * dl_t[:, :, None] * a_bar * h_prev
+                tb = lam * B_t * u_t[:, :, None] * dEdA
+                dA += np.sum(ta + tb, axis=0)
+                tB = lam * E * u_t[:, :, None]
+                dB[:, :, t] += np.sum(tB, axis=1)
+                if abs_terms:
+                    ddl_a[:, :, t] += np.sum(np.abs(q) + np.abs(r), axis=2)
+                    dA_a += np.sum(np.abs(ta) + np.abs(tb), axis=0)
+                    dB_a[:, :, t] += np.sum(np.abs(tB), axis=1)
             else:
-                du[:, :, t] += dl_t * np.sum(lam * B_t, axis=2)
-                ddl[:, :, t] += np.sum(lam * (A[None] * a_bar * h_prev), axis=2) + u_t * np.sum(lam * B_t, axis=2)
-                dA += np.sum(lam * dl_t[:, :, None] * a_bar * h_prev, axis=0)
-                dB[:, :, t] += np.sum(lam * (dl_t * u_t)[:, :, None], axis=1)
-            dC[:, :, t] += np.sum(g[:, :, t, None] * h_t, axis=1)
+                lb = lam * B_t
+                du[:, :, t] += dl_t * np.sum(lb, axis=2)
+                ddl[:, :, t] += np.sum(q, axis=2) + u_t * np.sum(lb, axis=2)
+                ta = lam * dl_t[:, :, None] * a_bar * h_prev
+                dA += np.sum(ta, axis=0)
+                tB = lam * (dl_t * u_t)[:, :, None]
+                dB[:, :, t] += np.sum(tB, axis=1)
+                if abs_terms:
+                    ddl_a[:, :, t] += np.sum(np.abs(q), axis=2) + np.abs(u_t) * np.sum(np.abs(lb), axis=2)
+                    dA_a += np.sum(np.abs(ta), axis=0)
+                    dB_a[:, :, t] += np.sum(np.abs(tB), axis=1)
+            tC = g[:, :, t, None] * h_t
+            dC[:, :, t] += np.sum(tC, axis=1)
+            if abs_terms:
+                dC_a[:, :, t] += np.sum(np.abs(tC), axis=1)
             mu = a_bar * lam
     dinit = mu  # a_bar_0 * lambda_0
-    dD = None
+    dD = dD_a = None
     if Dv is not None:
         du += Dv[None, :, None] * g
         dD = np.sum(g * u, axis=(0, 2))
+        dD_a = np.sum(np.abs(g * u), axis=(0, 2))
     if delta_softplus:
-        dx = np.where(x > SOFTPLUS_THRESHOLD, ddl, ddl * sigmoid64(x))
+        sp = np.where(x > SOFTPLUS_THRESHOLD, 1.0, sigmoid64(x))
+        dx = ddl * sp
+        dx_a = ddl_a * sp
     else:
         dx = ddl
+        dx_a = ddl_a
     dx = dx * mask[:, None, :]
+    dx_a = dx_a * mask[:, None, :]
     du = du * mask[:, None, :]
     if dz is not None:
         dz = dz * mask[:, None, :]
     ddelta_bias = None if delta_bias is None else np.sum(dx, axis=(0, 2))
-    return dict(du=du, ddelta=dx, dA=dA, dB=dB, dC=dC, dD=dD, dz=dz,
-                ddelta_bias=ddelta_bias, dinitial_state=dinit)
+    res = dict(du=du, ddelta=dx, dA=dA, dB=dB, dC=dC, dD=dD, dz=dz,
+               ddelta_bias=ddelta_bias, dinitial_state=dinit)
+    if abs_terms:
+        res.update(dA_abs=dA_a, dB_abs=dB_a, dC_abs=dC_a, dD_abs=dD_a,
+                   ddelta_bias_abs=None if delta_bias is None else np.sum(dx_a, axis=(0, 2)))
+    return res
 
 
 def reference_api_forward(A, deltas, Bs, Cs, u, initial_x=None, use_euler_barB_approx=True):
@@ -217,11 +253,17 @@ def reference_api_forward(A, deltas, Bs, Cs, u, initial_x=None, use_euler_barB_a
     return np.swapaxes(res["y"], 1, 2), res["last_state"], res["ref_chunk_states"]
 
 
-def reference_api_backward(A, deltas, Bs, Cs, u, initial_x, dy, dfinal_x, use_euler_barB_approx=True):
+def reference_api_backward(A, deltas, Bs, Cs, u, initial_x, dy, dfinal_x, use_euler_barB_approx=True,
+                           abs_terms=False):
     """Cotangents -> (dA, ddeltas, dBs, dCs, du, dinitial_x) in the reference's layout, as
-    ``_selective_scan_bwd_ffi`` returns them (``mamba/selective_scan_cuda.py:163-214``)."""
+    ``_selective_scan_bwd_ffi`` returns them (``mamba/selective_scan_cuda.py:163-214``).
+    With ``abs_terms`` also a dict of the |term| sums of dA, dBs and dCs (same layouts)."""
     tr = lambda a: np.ascontiguousarray(np.swapaxes(_f64(a), 1, 2))
     g = backward(tr(u), tr(deltas), A, tr(Bs), tr(Cs), tr(dy), initial_state=initial_x,
-                 dlast_state=dfinal_x, discretization="euler" if use_euler_barB_approx else "zoh")
+                 dlast_state=dfinal_x, discretization="euler" if use_euler_barB_approx else "zoh",
+                 abs_terms=abs_terms)
     sw = lambda a: np.swapaxes(a, 1, 2)
-    return g["dA"], sw(g["ddelta"]), sw(g["dB"]), sw(g["dC"]), sw(g["du"]), g["dinitial_state"]
+    grads = g["dA"], sw(g["ddelta"]), sw(g["dB"]), sw(g["dC"]), sw(g["du"]), g["dinitial_state"]
+    if not abs_terms:
+        return grads
+    return grads, dict(dA=g["dA_abs"], dBs=sw(g["dB_abs"]), dCs=sw(g["dC_abs"]))

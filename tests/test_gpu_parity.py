@@ -1,9 +1,13 @@
 """GPU parity: HIP kernels (through the C ABI) vs the float64 oracle on identical inputs.
 
 Bars (stated by the build target): float32 within rtol 1e-4 / atol 1e-5; bfloat16
-inputs with float32 accumulation within rtol 2e-2. Per-element outputs and gradients are
-checked elementwise; gradients that are sums over many terms (dA, dB, dC, dD, ddelta_bias)
-are checked on the scale of the tensor (rtol * max|ref|). Cases follow the reference tests
+inputs with float32 accumulation within rtol 2e-2. Every output and gradient is checked
+element by element: |got - ref| <= atol + rtol * s, where s = |ref| for per-step values and,
+for the gradients that are sums over channels, batch rows or steps (dA, dB, dC, dD,
+ddelta_bias), s = the sum of the absolute values of the terms summed into that element
+(returned by the oracle), the scale of the rounding error of any order of summation.
+The oracle is the float64 C restatement (oracle/scan64c.c, pinned against the numpy
+oracle on the CPU). Cases follow the reference tests
 (tests/test_selective_scan_cuda.py: lengths {1, 17, 128, 513} forward, {1, 31, 513, 2051}
 VJP, ZOH VJP at 31, reference input recipe) and extend them to the fused extras,
 multi-chunk lengths, ragged tails, variable lengths, bf16 and the full config-2 shape.
@@ -19,7 +23,7 @@ import torch
 from mamba_amd import _lib
 from mamba_amd.configs import C2, C3, C4, ScanConfig, make_scan_inputs
 from mamba_amd.selective_scan_hip import selective_scan, selective_scan_fn
-from oracle import scan64
+from oracle import scan64, scan64c
 
 pytestmark = pytest.mark.gpu
 
@@ -32,20 +36,23 @@ def log(msg):
     sys.stdout.flush()
 
 
-def close(name, got, ref, rtol=F32_RTOL, atol=F32_ATOL, normwise=False):
-    """Elementwise |got - ref| <= atol + rtol*|ref|; with normwise, rtol scales max|ref|
-    (sums over many terms that cancel, where an element's own size says nothing about
-    its rounding error)."""
+def close(name, got, ref, rtol=F32_RTOL, atol=F32_ATOL, scale=None):
+    """Elementwise |got - ref| <= atol + rtol * s with s = |ref|, or s = `scale` (same shape:
+    the oracle's sum of |terms| of a reduction gradient). Logs the worst err / bound."""
     got = got.detach().float().cpu().numpy() if torch.is_tensor(got) else np.asarray(got)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    s = np.abs(ref) if scale is None else np.asarray(scale, np.float64)
+    assert s.shape == ref.shape, (name, s.shape, ref.shape)
     err = np.abs(got - ref)
-    bound = atol + rtol * (np.abs(ref).max() if normwise else np.abs(ref))
-    worst = np.argmax(err - bound)
+    bound = atol + rtol * s
+    ratio = err / bound
+    worst = int(np.argmax(ratio))
     ok = bool(np.all(err <= bound))
-    log(f"  {name:16s} max_abs={err.max():.3e} max_rel={(err / np.maximum(np.abs(ref), 1e-30)).max():.3e} "
-        f"worst(got={got.flat[worst]:.6e}, ref={ref.flat[worst]:.6e}) ok={ok}")
+    log(f"  {name:16s} max_abs={err.max():.3e} worst err/bound={ratio.flat[worst]:.3f} "
+        f"(got={got.flat[worst]:.6e}, ref={ref.flat[worst]:.6e}, scale={s.flat[worst]:.3e}) ok={ok}")
     assert ok, f"{name}: {np.sum(err > bound)} of {err.size} elements outside rtol={rtol}, atol={atol}"
+    return float(ratio.flat[worst])
 
 
 dev = "cuda"
@@ -91,9 +98,9 @@ def test_reference_api_vjp(length, euler):
     ey, efin, _ = scan64.reference_api_forward(*args, use_euler_barB_approx=euler)
     dy = 2 * ey / ey.size
     dfin = 2 * efin / efin.size
-    grads = scan64.reference_api_backward(*args, dy, dfin, use_euler_barB_approx=euler)
+    grads, ab = scan64.reference_api_backward(*args, dy, dfin, use_euler_barB_approx=euler, abs_terms=True)
     for name, t, g in zip(["dA", "ddeltas", "dBs", "dCs", "du", "dinitial_x"], ts, grads):
-        close(name, t.grad, g, normwise=name in ("dA", "dBs", "dCs"))
+        close(name, t.grad, g, scale=ab.get(name))
 
 
 def fused_case(seed, b, d, l, n, dtype="f32", lens=None, zoh=False, extras=True):
@@ -141,8 +148,8 @@ def oracle_fused(x, dout, dlast, zoh, softplus=True):
     kw = dict(D=x.get("D"), z=x.get("z"), delta_bias=x.get("delta_bias"), delta_softplus=softplus,
               initial_state=x.get("initial_state"), seq_lens=x.get("seq_lens"),
               discretization="zoh" if zoh else "euler")
-    fw = scan64.forward(x["u"], x["delta"], x["A"], x["B"], x["C"], **kw)
-    g = scan64.backward(x["u"], x["delta"], x["A"], x["B"], x["C"], dout, dlast_state=dlast, **kw)
+    fw = scan64c.forward(x["u"], x["delta"], x["A"], x["B"], x["C"], **kw)
+    g = scan64c.backward(x["u"], x["delta"], x["A"], x["B"], x["C"], dout, dlast_state=dlast, abs_terms=True, **kw)
     return fw, g
 
 
@@ -155,11 +162,14 @@ REDUCTIONS = {"dA", "dB", "dC", "dD", "ddelta_bias"}
 
 
 def check_fused(ts, out, last, fw, g, rtol=F32_RTOL, atol=F32_ATOL):
-    close("out", out, fw["out"], rtol, atol)
-    close("last_state", last, fw["last_state"], rtol, atol)
+    """Every output and gradient against the oracle; returns {name: worst err / bound}."""
+    worst = {"out": close("out", out, fw["out"], rtol, atol),
+             "last_state": close("last_state", last, fw["last_state"], rtol, atol)}
     for k, gname in GRAD_OF.items():
         if k in ts:
-            close(gname, ts[k].grad, g[gname], rtol, atol, normwise=gname in REDUCTIONS)
+            scale = g[gname + "_abs"] if gname in REDUCTIONS else None
+            worst[gname] = close(gname, ts[k].grad, g[gname], rtol, atol, scale=scale)
+    return worst
 
 
 @pytest.mark.parametrize("l", [1, 7, 250, 1024, 1500, 3000])
@@ -184,27 +194,35 @@ def test_fused_wide_grid(zoh):
     check_fused(ts, out, last, fw, g)
 
 
+def tol(dtype):
+    return (BF16_RTOL, BF16_RTOL * 0.05) if dtype == "bf16" else (F32_RTOL, F32_ATOL)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("zoh", [False, True])
 @pytest.mark.parametrize("n", [8, 4, 1])
-def test_sixteen_wave_state_counts(n, zoh):
-    """1 x 4096 channels: the backward runs 16 waves per workgroup (its plan for this grid,
-    checked on the host in test_boundary), where N < 16 states give each wave a copy of the
-    rotated dB/dC accumulator rows (16 / N copies)."""
-    log(f"case sixteen waves N={n} zoh={zoh}")
-    x, dout, dlast = fused_case(960 + n + zoh, 1, 4096, 600, n, zoh=zoh)
-    ts, out, last = run_fused(x, dout, dlast, "f32", zoh)
+def test_sixteen_wave_state_counts(n, zoh, dtype):
+    """1 x 4096 channels: the backward runs 16 waves per workgroup (asserted from the
+    library's plan), where N < 16 states give each wave a copy of the rotated dB/dC
+    accumulator rows (16 / N copies)."""
+    log(f"case sixteen waves N={n} zoh={zoh} {dtype}")
+    assert _lib.bwd_plan(1, 4096, n)[0] == 16
+    x, dout, dlast = fused_case(960 + n + zoh, 1, 4096, 600, n, dtype=dtype, zoh=zoh)
+    ts, out, last = run_fused(x, dout, dlast, dtype, zoh)
     fw, g = oracle_fused(x, dout, dlast, zoh)
-    check_fused(ts, out, last, fw, g)
+    check_fused(ts, out, last, fw, g, *tol(dtype))
 
 
-def test_sixteen_wave_varlen():
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sixteen_wave_varlen(dtype):
     """Variable lengths on a grid whose backward plan is 16 waves per workgroup: whole chunks
     past a row's length (zero gradients, the adjoint passing through) and an empty row."""
-    log("case sixteen waves varlen")
-    x, dout, dlast = fused_case(970, 4, 2048, 1100, 16, lens=[1100, 530, 0, 1])
-    ts, out, last = run_fused(x, dout, dlast, "f32", False)
+    log(f"case sixteen waves varlen {dtype}")
+    assert _lib.bwd_plan(4, 2048, 16, varlen=True)[0] == 16
+    x, dout, dlast = fused_case(970, 4, 2048, 1100, 16, dtype=dtype, lens=[1100, 530, 0, 1])
+    ts, out, last = run_fused(x, dout, dlast, dtype, False)
     fw, g = oracle_fused(x, dout, dlast, False)
-    check_fused(ts, out, last, fw, g)
+    check_fused(ts, out, last, fw, g, *tol(dtype))
 
 
 @pytest.mark.parametrize("l", [5, 300, 2100])
@@ -324,11 +342,11 @@ def test_reference_c_entry_points():
     close("y", y.transpose(1, 2), ey)
     close("final_x", fin, efin)
     close("chunk_states", cs, ecs)
-    grads = scan64.reference_api_backward(A, deltas, Bs, Cs, u, x0, dy, dfin)
-    names = ["dA", "ddeltas", "dB", "dC", "du", "dinitial_x"]
+    grads, ab = scan64.reference_api_backward(A, deltas, Bs, Cs, u, x0, dy, dfin, abs_terms=True)
+    names = ["dA", "ddeltas", "dBs", "dCs", "du", "dinitial_x"]
     for name, o, g in zip(names, outs, grads):
         got = o if o.shape == g.shape else o.transpose(1, 2)
-        close(name, got, g, normwise=name in REDUCTIONS)
+        close(name, got, g, scale=ab.get(name))
 
 
 def config_tensors(cfg, x, dout):
@@ -351,13 +369,78 @@ def test_config2_full_size():
     dlast = np.random.default_rng(1).standard_normal((C2.batch, C2.dim, C2.dstate)).astype(np.float32)
     ts, out, last = run_fused(x, dout, dlast, "f32", False)
     fw, g = oracle_fused(x, dout, dlast, False)
-    check_fused(ts, out, last, fw, g)
+    worst = check_fused(ts, out, last, fw, g)
+    log("  c2 worst err/bound: " + ", ".join(f"{k}={v:.3f}" for k, v in worst.items()))
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("cfg", [C3, C4], ids=["c3", "c4"])
+def test_config3_full_size_bf16():
+    """Config 3 at its full shape (B=8, D=2048, L=4096, N=16; u/delta/B/C/z/dout in bf16,
+    fp32 accumulation): the 16-wave backward plan the config runs, every output and
+    gradient against the oracle on the same bf16-rounded inputs."""
+    log("case c3 full size")
+    assert _lib.bwd_plan(C3.batch, C3.dim, C3.dstate)[0] == 16
+    x = make_scan_inputs(C3, seed=0, with_z=True, with_dout=True)
+    dout = x.pop("dout")
+    dlast = np.zeros((C3.batch, C3.dim, C3.dstate), np.float32)
+    ts, out, last = run_fused(x, dout, dlast, "bf16", False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    worst = check_fused(ts, out, last, fw, g, *tol("bf16"))
+    log("  c3 worst err/bound: " + ", ".join(f"{k}={v:.3f}" for k, v in worst.items()))
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("zoh", [False, True])
+def test_c5_layer_scan_bf16(zoh):
+    """The scan of one layer of the config-5 model, as the model calls it: B=8, d_inner=1536,
+    L=2048, N=16, bf16, u/delta/z channel-outer ((d_inner, B*L) activation matrices) and B/C
+    row slices of the (dt_rank + 2N, B*L) x-projection output (dt_rank 48); the 16-wave
+    backward plan; every output and gradient against the oracle."""
+    log(f"case c5 layer scan zoh={zoh}")
+    b, d, l, n, r = 8, 1536, 2048, 16, 48
+    assert _lib.bwd_plan(b, d, n)[0] == 16
+    cfg = ScanConfig("c5_layer", b, d, l, n, "bf16", None)
+    x = make_scan_inputs(cfg, seed=5 + zoh, with_z=True, with_dout=True)
+    dout = x.pop("dout")
+    dlast = np.zeros((b, d, n), np.float32)
+    tdt = torch.bfloat16
+
+    def channel_outer(a):  # (b, d, l) -> leaf (d, b, l) and its (b, d, l) view
+        leaf = T(np.ascontiguousarray(np.swapaxes(a, 0, 1)), tdt).requires_grad_(True)
+        return leaf, leaf.permute(1, 0, 2)
+
+    leaves = {k: channel_outer(x[k]) for k in ("u", "delta", "z")}
+    junk = np.random.default_rng(9).standard_normal((r, b, l)).astype(np.float32)
+    proj = T(np.concatenate([junk, np.swapaxes(x["B"], 0, 1), np.swapaxes(x["C"], 0, 1)], axis=0),
+             tdt).requires_grad_(True)
+    Bv = proj[r:r + n].permute(1, 0, 2)
+    Cv = proj[r + n:].permute(1, 0, 2)
+    small = {k: T(x[k]).requires_grad_(True) for k in ("A", "D", "delta_bias")}
+    out, last = selective_scan_fn(leaves["u"][1], leaves["delta"][1], small["A"], Bv, Cv, D=small["D"],
+                                  z=leaves["z"][1], delta_bias=small["delta_bias"], delta_softplus=True,
+                                  return_last_state=True, discretization="zoh" if zoh else "euler")
+    (out.float() * T(dout)).sum().backward()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(proj.grad[:r]) == 0
+    ts = {k: leaves[k][0] for k in leaves}
+    ts.update(small)
+    grads = {k: leaves[k][0].grad.permute(1, 0, 2) for k in leaves}
+    grads["B"] = proj.grad[r:r + n].permute(1, 0, 2)
+    grads["C"] = proj.grad[r + n:].permute(1, 0, 2)
+    grads.update({k: small[k].grad for k in small})
+    fw, g = oracle_fused(x, dout, dlast, zoh)
+    rt, at = tol("bf16")
+    worst = {"out": close("out", out, fw["out"], rt, at), "last_state": close("last_state", last, fw["last_state"], rt, at)}
+    for k, gt in grads.items():
+        gname = GRAD_OF[k]
+        worst[gname] = close(gname, gt, g[gname], rt, at, scale=g[gname + "_abs"] if gname in REDUCTIONS else None)
+    log("  c5 layer worst err/bound: " + ", ".join(f"{k}={v:.3f}" for k, v in worst.items()))
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("cfg", [C4], ids=["c4"])
 def test_large_config_channel_slice(cfg):
-    """Full L and B of configs 3/4 on a slice of 32 channels (channels are independent;
+    """Full L and B of config 4 on a slice of 32 channels (channels are independent;
     dB/dC of the slice are the slice's own sums)."""
     log(f"case {cfg.name} channel slice")
     sl = ScanConfig(cfg.name + "_slice", cfg.batch, 32, cfg.length, cfg.dstate, cfg.dtype, cfg.varlen)

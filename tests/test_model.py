@@ -11,11 +11,15 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from mamba_amd import _lib
 from mamba_amd.mamba1 import GraphedTrainStep, MambaLM
 from oracle import mamba1_torch as ref
 from oracle import cscan64, scan64
 
 C1 = dict(vocab=16, d_model=64, n_layers=2, expand=2, d_state=16, d_conv=4, batch=8, length=256)
+# Config 5: the Mamba-1 130M shape.
+C5 = dict(vocab=50280, d_model=768, n_layers=24, expand=2, d_state=16, dt_rank=48, d_conv=4, batch=8,
+          length=2048)
 
 
 def test_oracle_conv_matches_torch_conv1d():
@@ -58,6 +62,29 @@ def test_oracle_s6_matches_scan64(euler):
                         sw(x_dbl[..., 6:]), D=p[pre + "D"].numpy(), delta_bias=p[pre + "dt_bias"].numpy(),
                         delta_softplus=True, discretization="euler" if euler else "zoh")
     np.testing.assert_allclose(got.numpy(), np.swapaxes(fw["out"], 1, 2), rtol=1e-9, atol=1e-12)
+
+
+@pytest.mark.parametrize("euler", [True, False])
+def test_oracle_seq_scan_matches_associative_scan(euler):
+    """The oracle model's sequential-scan option (the C oracle's recurrence and adjoint) against
+    its associative scan under torch autograd: outputs and every parameter gradient."""
+    p, _ = small_params()
+    pre = "blocks.0.s6."
+    rng = np.random.default_rng(4)
+    u0 = torch.from_numpy(rng.standard_normal((2, 40, 16)))
+    w = torch.from_numpy(rng.standard_normal((2, 40, 16)))
+    outs = []
+    for seq in (False, True):
+        q = {k: v.clone().requires_grad_(True) for k, v in p.items()}
+        u = u0.clone().requires_grad_(True)
+        y = ref.s6(q, pre, u, 2, 4, euler, seq_scan=seq)
+        (y * w).sum().backward()
+        outs.append((y.detach(), u.grad, {k: v.grad for k, v in q.items() if v.grad is not None}))
+    torch.testing.assert_close(outs[1][0], outs[0][0], rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(outs[1][1], outs[0][1], rtol=1e-9, atol=1e-11)
+    assert outs[1][2].keys() == outs[0][2].keys()
+    for k in outs[0][2]:
+        torch.testing.assert_close(outs[1][2][k], outs[0][2][k], rtol=1e-9, atol=1e-11)
 
 
 @pytest.mark.parametrize("euler", [True, False])
@@ -231,6 +258,124 @@ def test_graphed_train_step_matches_eager():
         _ = (m_g.embedding.sum() * 0).item()  # eager work between replays
     print("  eager", [round(x, 5) for x in eager_losses[warm:]], flush=True)
     print("  graph", [round(x, 5) for x in graph_losses], flush=True)
+    for a, b in zip(eager_losses[warm:], graph_losses):
+        assert abs(a - b) <= 2e-3 * abs(a), (a, b)
+    for (k, pe), pg in zip(m_e.named_parameters(), m_g.parameters()):
+        scale = float(pe.detach().abs().max()) + 1e-12
+        assert float((pe.detach() - pg.detach()).abs().max()) <= 2e-2 * scale, k
+
+
+def _max_err_over_scale(got, want, rows=2048):
+    """max |got - want| and max |want| over (R, C) tensors, in row blocks (bounded memory)."""
+    err = scale = 0.0
+    for i in range(0, want.shape[0], rows):
+        w = want[i:i + rows]
+        err = max(err, float((got[i:i + rows].double() - w).abs().max()))
+        scale = max(scale, float(w.abs().max()))
+    return err, scale
+
+
+@pytest.mark.gpu
+@pytest.mark.slow
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_c5_widths_one_layer_matches_oracle(act):
+    """One block of the config-5 model at its full widths and workload (d_model 768, d_inner
+    1536, dt_rank 48, N 16, vocab 50280, B 8, L 2048): logits, loss and every parameter
+    gradient against the float64 oracle model (sequential-scan option) on the CPU with the
+    same weights. The layer's scan runs the 16-wave backward plan of every config-5 layer.
+    f32 activations: the config-1 bars (logits 1e-4, gradients 1e-3 of each tensor's scale);
+    bf16 activations (config 5's dtype: bf16 GEMM weights and activations, fp32 scan
+    accumulation, fp32 master gradients): logits 2e-2 and gradients 5e-2 of scale."""
+    print(f"case c5 widths one layer act={act}", flush=True)
+    cfg = C5
+    assert _lib.bwd_plan(cfg["batch"], cfg["d_model"] * cfg["expand"], cfg["d_state"])[0] == 16
+    torch.manual_seed(0)
+    model = MambaLM(cfg["vocab"], cfg["d_model"], 1, cfg["expand"], cfg["d_state"], cfg["dt_rank"],
+                    cfg["d_conv"], device="cuda")
+    g = torch.Generator().manual_seed(5)
+    tokens = torch.randint(0, cfg["vocab"], (cfg["batch"], cfg["length"]), generator=g)
+    targets = torch.roll(tokens, -1, dims=1).reshape(-1)
+    adt = torch.float32 if act == "f32" else torch.bfloat16
+    logits = model(tokens.cuda(), act_dtype=adt)
+    loss = F.cross_entropy(logits.float(), targets.cuda())
+    loss.backward()
+    torch.cuda.synchronize()
+    logits = logits.detach().float().cpu()
+    named = {k: v.grad.detach().cpu().double() for k, v in model.named_parameters()}
+    state = {k: v.detach().cpu().double() for k, v in model.state_dict().items()}
+    del model
+    torch.cuda.empty_cache()
+
+    p = {k: v.requires_grad_(True) for k, v in state.items()}
+    ref_logits = ref.mamba_lm(p, tokens, 1, cfg["dt_rank"], cfg["d_state"], True, seq_scan=True)
+    ref_loss = F.cross_entropy(ref_logits, targets)
+    ref_loss.backward()
+    err, scale = _max_err_over_scale(logits, ref_logits.detach())
+    print(f"  logits max_err={err:.3e} max|ref|={scale:.3e} loss {loss.item():.6f} vs {ref_loss.item():.6f}",
+          flush=True)
+    lt, gt = (1e-4, 1e-3) if act == "f32" else (2e-2, 5e-2)
+    assert err <= lt * scale + (1e-4 if act == "f32" else 0.0)
+    assert abs(loss.item() - ref_loss.item()) <= (1e-5 if act == "f32" else 2e-3) * abs(ref_loss.item())
+    for k, v in p.items():
+        got = named[k]
+        sc = float(v.grad.abs().max())
+        e = float((got - v.grad).abs().max())
+        print(f"  grad {k:28s} max|g|={sc:.3e} max_err={e:.3e} ratio={e / sc:.2e}", flush=True)
+        assert e <= gt * sc + 1e-7, k
+
+
+@pytest.mark.gpu
+@pytest.mark.slow
+def test_c5_full_train_step_graph_matches_eager():
+    """The config-5 training step (24 layers, bf16, AdamW) at its workload: every eager step
+    has a finite loss and finite, nonzero gradients, and the HIP-graph step replays the same
+    losses and ends at the same weights as the eager steps (replays checked one by one)."""
+    print("case c5 full train step graph vs eager", flush=True)
+    from mamba_amd.lm_ops import cross_entropy
+
+    cfg = C5
+    g = torch.Generator().manual_seed(6)
+    tokens = torch.randint(0, cfg["vocab"], (cfg["batch"], cfg["length"] + 1), generator=g).cuda()
+    inp, tgt = tokens[:, :-1].contiguous(), tokens[:, 1:].reshape(-1).contiguous()
+
+    def make():
+        torch.manual_seed(7)
+        m = MambaLM(cfg["vocab"], cfg["d_model"], cfg["n_layers"], cfg["expand"], cfg["d_state"], cfg["dt_rank"],
+                    cfg["d_conv"], device="cuda")
+        return m, torch.optim.AdamW(m.parameters(), lr=1e-3, fused=True, capturable=True)
+
+    warm, steps = 3, 3
+    m_e, o_e = make()
+    eager_losses = []
+    for i in range(warm + 1 + steps):
+        o_e.zero_grad(set_to_none=True)
+        loss = cross_entropy(m_e(inp), tgt)
+        loss.backward()
+        for k, prm in m_e.named_parameters():
+            assert prm.grad is not None and bool(torch.isfinite(prm.grad).all()), (i, k)
+            assert bool((prm.grad != 0).any()), (i, k)
+        o_e.step()
+        eager_losses.append(loss.item())
+        assert np.isfinite(eager_losses[-1])
+    del loss
+    m_g, o_g = make()
+    for _ in range(2):
+        o_g.zero_grad(set_to_none=True)
+        loss = cross_entropy(m_g(inp), tgt)
+        loss.backward()
+        o_g.step()
+    del loss
+    torch.cuda.synchronize()
+    gs = GraphedTrainStep(m_g, o_g, cross_entropy, inp, tgt, warmup=warm - 2)
+    torch.cuda.synchronize()
+    graph_losses = []
+    for i in range(1 + steps):
+        graph_losses.append(gs.step().item())
+        torch.cuda.synchronize()
+        _ = (m_g.embedding.sum() * 0).item()  # eager work between replays
+    print("  eager", [round(x, 5) for x in eager_losses], flush=True)
+    print("  graph", [round(x, 5) for x in graph_losses], flush=True)
+    assert eager_losses[0] > eager_losses[-1]
     for a, b in zip(eager_losses[warm:], graph_losses):
         assert abs(a - b) <= 2e-3 * abs(a), (a, b)
     for (k, pe), pg in zip(m_e.named_parameters(), m_g.parameters()):

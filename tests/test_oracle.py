@@ -268,3 +268,54 @@ def test_reference_api_backward_shapes_and_layout():
     ((y * torch.tensor(dy)).sum() + (fin * torch.tensor(dfin)).sum()).backward()
     for got, t in zip((dA, dd, dB, dC, du, dx0), ts):
         np.testing.assert_allclose(got, t.grad.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def _case_inputs(seed, b, d, l, n, extras, lens):
+    rng = np.random.default_rng(seed)
+    x = dict(u=rng.standard_normal((b, d, l)), delta=rng.standard_normal((b, d, l)),
+             A=-np.exp(rng.standard_normal((d, n))), B=rng.standard_normal((b, n, l)),
+             C=rng.standard_normal((b, n, l)))
+    kw = {}
+    if extras:
+        kw = dict(D=rng.standard_normal(d), z=rng.standard_normal((b, d, l)),
+                  delta_bias=0.5 * rng.standard_normal(d) - 2.0, initial_state=rng.standard_normal((b, d, n)),
+                  delta_softplus=True)
+    else:
+        x["delta"] = np.abs(x["delta"]) * 0.1
+    if lens is not None:
+        kw["seq_lens"] = np.asarray(lens, np.int32)
+    return x, kw, rng.standard_normal((b, d, l)), rng.standard_normal((b, d, n))
+
+
+@pytest.mark.parametrize("disc", ["euler", "zoh"])
+@pytest.mark.parametrize("extras,lens", [(True, None), (True, [300, 17, 0]), (False, None)])
+def test_c_oracle_matches_numpy_oracle(disc, extras, lens):
+    """The C restatement (oracle/scan64c.c, used by the GPU tests at full size) against the numpy
+    oracle: every output, gradient and |term| sum, to float64 rounding."""
+    from oracle import scan64c
+    x, kw, dout, dlast = _case_inputs(31, 3, 5, 300, 7, extras, lens)
+    f1 = scan64.forward(**x, **kw, discretization=disc)
+    f2 = scan64c.forward(**x, **kw, discretization=disc)
+    for k in ("out", "y", "last_state", "ref_chunk_states"):
+        np.testing.assert_allclose(f2[k], f1[k], rtol=1e-12, atol=1e-13 * np.abs(f1[k]).max())
+    g1 = scan64.backward(**x, dout=dout, **kw, discretization=disc, dlast_state=dlast, abs_terms=True)
+    g2 = scan64c.backward(**x, dout=dout, **kw, discretization=disc, dlast_state=dlast, abs_terms=True)
+    assert g1.keys() == g2.keys()
+    for k in g1:
+        if g1[k] is None:
+            assert g2[k] is None, k
+            continue
+        np.testing.assert_allclose(g2[k], g1[k], rtol=1e-10, atol=1e-12 * np.abs(g1[k]).max(), err_msg=k)
+
+
+def test_abs_term_sums_bound_the_reduction_gradients():
+    """|sum of terms| <= sum of |terms| everywhere, with equality where every term has one sign:
+    dD = sum g u with z absent and dout = sign(u) makes every term g u = |u| >= 0."""
+    x, kw, dout, dlast = _case_inputs(32, 2, 4, 90, 5, True, None)
+    g = scan64.backward(**x, dout=dout, **kw, dlast_state=dlast, abs_terms=True)
+    for k in ("dA", "dB", "dC", "dD", "ddelta_bias"):
+        assert np.all(np.abs(g[k]) <= g[k + "_abs"] * (1 + 1e-12)), k
+        assert np.all(g[k + "_abs"] > 0), k
+    kw.pop("z")
+    g = scan64.backward(**x, dout=np.sign(x["u"]), **kw, abs_terms=True)
+    np.testing.assert_allclose(g["dD"], g["dD_abs"], rtol=1e-12)
