@@ -49,13 +49,15 @@ extern "C" {
 #define MSS_MAX_DSTATE 16
 #define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
+#define MSS_NOALLOC_SCRATCH_BYTES (128u << 20) /* fixed per-device scratch of mss_bwd_noalloc */
 
 typedef enum mss_status {
   MSS_OK = 0,
   MSS_ERR_INVALID_ARGUMENT = 1, /* bad shape, null required pointer, bad flag */
   MSS_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
   MSS_ERR_HIP = 3,              /* a HIP runtime call failed; see mss_last_hip_error */
-  MSS_ERR_WORKSPACE = 4         /* caller workspace too small */
+  MSS_ERR_WORKSPACE = 4,        /* caller workspace too small */
+  MSS_ERR_SCRATCH_LIMIT = 5     /* mss_bwd_noalloc: shapes need more than its fixed scratch */
 } mss_status;
 
 typedef enum mss_dtype { MSS_F32 = 0, MSS_BF16 = 1 } mss_dtype;
@@ -148,6 +150,17 @@ int mss_bwd_plan(int32_t batch, int32_t dim, int32_t dstate, int32_t varlen, int
 
 int mss_fwd(const mss_fwd_args* args, void* stream);
 int mss_bwd(const mss_bwd_args* args, void* stream);
+
+/* mss_bwd without any allocation, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. args->workspace is ignored: the workspace is a fixed
+ * per-device array of MSS_NOALLOC_SCRATCH_BYTES inside the library, held by every device
+ * the library runs this entry point on until the process ends. Shapes whose workspace
+ * (mss_bwd_workspace_bytes) exceeds it return MSS_ERR_SCRATCH_LIMIT before any launch.
+ * Results equal mss_bwd's bit for bit (same kernels, same plan). All calls on one device
+ * share the one array: calls whose executions overlap on a device (concurrent streams, or
+ * threads) race and must be serialised by the caller. */
+int mss_bwd_noalloc(const mss_bwd_args* args, void* stream);
 
 /* mss_bwd in two stream-ordered phases sharing a caller-provided workspace (NULL ->
  * MSS_ERR_WORKSPACE): mss_bwd_scan writes du/ddelta/dz/dinitial_state and per-block

@@ -11,6 +11,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/mamba_selective_scan.h"
@@ -293,6 +294,35 @@ int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream, bool cplx = f
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching selective scan backward");
 }
 
+// ---- Fixed device scratch of mss_bwd_noalloc: the backward's workspace (dB/dC and
+// dA/dD/dbias partial sums) for callers that cannot allocate. One array per device, held
+// until the process ends. In host code `scratch` names a host-side stand-in: kernels get
+// the device address that hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = static_cast<size_t>(MSS_NOALLOC_SCRATCH_BYTES);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "querying the current device");
+  if (dev < 0 || dev >= kMaxDevices) return MSS_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "looking up the backward scratch");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MSS_OK;
+}
+
 }  // namespace
 
 // ---- causal conv1d
@@ -355,6 +385,9 @@ const char* mss_strerror(int status) {
     case MSS_ERR_UNSUPPORTED: return "unsupported configuration (dstate <= 16, batch * 2 * dstate <= 65535)";
     case MSS_ERR_HIP: return "HIP runtime error";
     case MSS_ERR_WORKSPACE: return "workspace too small";
+    case MSS_ERR_SCRATCH_LIMIT:
+      return "request needs more backward scratch than mss_bwd_noalloc holds "
+             "(MSS_NOALLOC_SCRATCH_BYTES; use mss_bwd with a workspace)";
     default: return "unknown status";
   }
 }
@@ -387,6 +420,20 @@ int mss_bwd(const mss_bwd_args* args, void* stream) {
   const int s = validate_bwd(args);
   if (s != MSS_OK) return s;
   return run_bwd(args, kPhaseBoth, static_cast<hipStream_t>(stream));
+}
+
+int mss_bwd_noalloc(const mss_bwd_args* args, void* stream) {
+  const int s = validate_bwd(args);
+  if (s != MSS_OK) return s;
+  const BwdLayout l = bwd_layout(args->batch, args->dim, args->seqlen, args->dstate, args->seq_lens != nullptr);
+  if (l.total > kScratchBytes) return MSS_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  const int t = scratch_of_current_device(&ws);
+  if (t != MSS_OK) return t;
+  mss_bwd_args a = *args;
+  a.workspace = ws;
+  a.workspace_bytes = kScratchBytes;
+  return run_bwd(&a, kPhaseBoth, static_cast<hipStream_t>(stream));
 }
 
 int mss_bwd_scan(const mss_bwd_args* args, void* stream) {

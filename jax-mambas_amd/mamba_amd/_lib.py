@@ -19,6 +19,8 @@ MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
 MSS_ERR_HIP = 3
 MSS_ERR_WORKSPACE = 4
+MSS_ERR_SCRATCH_LIMIT = 5
+MSS_NOALLOC_SCRATCH_BYTES = 128 << 20
 MSS_F32 = 0
 MSS_BF16 = 1
 MSS_EULER = 0
@@ -33,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "mss_bwd_plan",
     "mss_fwd",
     "mss_bwd",
+    "mss_bwd_noalloc",
     "mss_bwd_scan",
     "mss_bwd_reduce",
     "mss_cbwd_workspace_bytes",
@@ -169,7 +172,7 @@ def register_hip_kernel(library_path=None):
     lib.mss_fwd.restype = ctypes.c_int
     lib.mss_bwd.argtypes = [ctypes.POINTER(BwdArgs), _p]
     lib.mss_bwd.restype = ctypes.c_int
-    for name in ("mss_bwd_scan", "mss_bwd_reduce", "mss_cbwd"):
+    for name in ("mss_bwd_noalloc", "mss_bwd_scan", "mss_bwd_reduce", "mss_cbwd"):
         getattr(lib, name).argtypes = [ctypes.POINTER(BwdArgs), _p]
         getattr(lib, name).restype = ctypes.c_int
     lib.mss_cfwd.argtypes = [ctypes.POINTER(FwdArgs), _p]

@@ -173,6 +173,20 @@ def test_bwd_workspace_too_small(lib):
     assert lib.mss_bwd(a, None) == _lib.MSS_ERR_WORKSPACE
 
 
+def test_noalloc_backward_rejects_shapes_beyond_its_scratch(lib):
+    """mss_bwd_noalloc validates like mss_bwd, then refuses shapes whose workspace exceeds its
+    fixed scratch (config 3's 129 MiB) before any HIP call; config 2 and the config-5 layers fit."""
+    assert lib.mss_bwd_noalloc(None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_bwd_noalloc(bwd_args(carries=None), None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    big = bwd_args(batch=8, dim=2048, seqlen=4096, dstate=16)
+    assert lib.mss_bwd_workspace_bytes(big) > _lib.MSS_NOALLOC_SCRATCH_BYTES
+    assert lib.mss_bwd_noalloc(big, None) == _lib.MSS_ERR_SCRATCH_LIMIT
+    assert b"mss_bwd_noalloc" in lib.mss_strerror(_lib.MSS_ERR_SCRATCH_LIMIT)
+    for b, d, l in ((4, 1536, 2048), (8, 1536, 2048)):
+        assert lib.mss_bwd_workspace_bytes(bwd_args(batch=b, dim=d, seqlen=l, dstate=16)) <= \
+            _lib.MSS_NOALLOC_SCRATCH_BYTES
+
+
 def test_workspace_size_depends_on_shapes_only(lib):
     a = bwd_args(batch=4, dim=1536, seqlen=2048, dstate=16)
     n1 = lib.mss_bwd_workspace_bytes(a)
