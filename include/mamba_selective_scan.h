@@ -140,13 +140,12 @@ typedef struct mss_bwd_args {
  * (0 on invalid arguments). */
 size_t mss_bwd_workspace_bytes(const mss_bwd_args* args);
 
-/* Launch plan of the backward scan kernel for these shapes (varlen: seq_lens given):
- * waves per workgroup and channels one workgroup walks. The plan depends on the shapes
- * only, so a caller (or a test) can tell which kernel variant a configuration runs. No
- * counterpart in the reference, whose backward launch shape is fixed by its traits
+/* Launch plan mss_bwd would use for these arguments: waves per workgroup of the backward
+ * scan kernel and channels one workgroup walks (it depends on the shapes and on whether
+ * seq_lens is given). Validates like mss_bwd; launches nothing. No counterpart in the
+ * reference, whose backward launch shape is fixed by its traits
  * (native/upstream_mamba/selective_scan_bwd_kernel.cuh:499-535). */
-int mss_bwd_plan(int32_t batch, int32_t dim, int32_t dstate, int32_t varlen, int32_t* waves,
-                 int32_t* chan_per_block);
+int mss_bwd_plan(const mss_bwd_args* args, int32_t* waves, int32_t* chan_per_block);
 
 int mss_fwd(const mss_fwd_args* args, void* stream);
 int mss_bwd(const mss_bwd_args* args, void* stream);

@@ -399,12 +399,11 @@ size_t mss_bwd_workspace_bytes(const mss_bwd_args* a) {
   return bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr).total;
 }
 
-int mss_bwd_plan(int32_t batch, int32_t dim, int32_t dstate, int32_t varlen, int32_t* waves,
-                 int32_t* chan_per_block) {
+int mss_bwd_plan(const mss_bwd_args* args, int32_t* waves, int32_t* chan_per_block) {
   if (waves == nullptr || chan_per_block == nullptr) return MSS_ERR_INVALID_ARGUMENT;
-  const int s = check_dims(batch, dim, 1, dstate);
+  const int s = validate_bwd(args);
   if (s != MSS_OK) return s;
-  const BwdLayout l = bwd_layout(batch, dim, 1, dstate, varlen != 0);
+  const BwdLayout l = bwd_layout(args->batch, args->dim, args->seqlen, args->dstate, args->seq_lens != nullptr);
   *waves = l.waves;
   *chan_per_block = l.chan_per_block;
   return MSS_OK;

@@ -180,7 +180,7 @@ def register_hip_kernel(library_path=None):
     for name in ("mss_bwd_workspace_bytes", "mss_cbwd_workspace_bytes"):
         getattr(lib, name).argtypes = [ctypes.POINTER(BwdArgs)]
         getattr(lib, name).restype = ctypes.c_size_t
-    lib.mss_bwd_plan.argtypes = [_i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
+    lib.mss_bwd_plan.argtypes = [ctypes.POINTER(BwdArgs), ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
     lib.mss_bwd_plan.restype = ctypes.c_int
     lib.mss_scan_fwd.argtypes = [_p, _i32, _i32, _i32, _i32, _i32] + [_p] * 9
     lib.mss_scan_fwd.restype = ctypes.c_int
@@ -240,12 +240,21 @@ class MSSError(RuntimeError):
         self.status = status
 
 
-def bwd_plan(batch, dim, dstate, varlen=False):
-    """(waves per workgroup, channels per workgroup) of the backward scan for these shapes."""
+def bwd_plan(batch, dim, dstate, seqlen=2048, varlen=False, zoh=False, io_bf16=False, bc_bf16=None,
+             z=True, strides=None):
+    """(waves per workgroup, channels per workgroup) of the backward scan mss_bwd would run
+    for a call with these shapes."""
     lib = register_hip_kernel()
+    bc_bf16 = io_bf16 if bc_bf16 is None else bc_bf16
+    a = BwdArgs(batch=batch, dim=dim, seqlen=seqlen, dstate=dstate, discretization=MSS_ZOH if zoh else MSS_EULER,
+                io_dtype=MSS_BF16 if io_bf16 else MSS_F32, bc_dtype=MSS_BF16 if bc_bf16 else MSS_F32,
+                u=256, delta=256, A=256, B=256, C=256, carries=256, dout=256, du=256, ddelta=256, dA=256,
+                dB=256, dC=256, seq_lens=256 if varlen else None, z=256 if z else None,
+                y_pre=256 if z else None, dz=256 if z else None)
+    if strides is not None:
+        a.strides = strides
     w, c = _i32(), _i32()
-    check(lib.mss_bwd_plan(batch, dim, dstate, int(bool(varlen)), ctypes.byref(w), ctypes.byref(c)),
-          "mss_bwd_plan")
+    check(lib.mss_bwd_plan(ctypes.byref(a), ctypes.byref(w), ctypes.byref(c)), "mss_bwd_plan")
     return w.value, c.value
 
 

@@ -226,19 +226,21 @@ def test_backward_plan(lib, shape, waves):
         k += 1
     cpb = min(k, 96 // waves, per_row) * waves
     assert _bwd_blocks(lib, b, d, l, n) == -(-d // cpb)
-    assert _lib.bwd_plan(b, d, n) == (waves, cpb)
+    assert _lib.bwd_plan(b, d, n, seqlen=l) == (waves, cpb)
 
 
 def test_backward_plan_of_the_configs(lib):
     """Config 3 and every config-5 layer run the 16-wave backward, config 2 the 12-wave one;
-    invalid shapes are rejected."""
-    assert _lib.bwd_plan(4, 1536, 16)[0] == 12
-    assert _lib.bwd_plan(8, 2048, 16)[0] == 16
-    assert _lib.bwd_plan(8, 1536, 16)[0] == 16
+    invalid arguments are rejected."""
+    assert _lib.bwd_plan(4, 1536, 16, 2048)[0] == 12
+    assert _lib.bwd_plan(8, 2048, 16, 4096, io_bf16=True)[0] == 16
+    c5 = _lib.Strides(io_batch=2048, io_dim=8 * 2048, bc_batch=2048, bc_state=8 * 2048)
+    assert _lib.bwd_plan(8, 1536, 16, 2048, io_bf16=True, strides=c5)[0] == 16
     w = ctypes.c_int32()
-    assert lib.mss_bwd_plan(0, 10, 4, 0, ctypes.byref(w), ctypes.byref(w)) == _lib.MSS_ERR_INVALID_ARGUMENT
-    assert lib.mss_bwd_plan(1, 10, 32, 0, ctypes.byref(w), ctypes.byref(w)) == _lib.MSS_ERR_UNSUPPORTED
-    assert lib.mss_bwd_plan(1, 10, 4, 0, None, ctypes.byref(w)) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_bwd_plan(None, ctypes.byref(w), ctypes.byref(w)) == _lib.MSS_ERR_INVALID_ARGUMENT
+    bad = bwd_args(dstate=32)
+    assert lib.mss_bwd_plan(bad, ctypes.byref(w), ctypes.byref(w)) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_bwd_plan(bwd_args(), None, ctypes.byref(w)) == _lib.MSS_ERR_INVALID_ARGUMENT
 
 
 def test_reference_entry_points_validate(lib):

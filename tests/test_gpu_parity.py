@@ -206,7 +206,7 @@ def test_sixteen_wave_state_counts(n, zoh, dtype):
     library's plan), where N < 16 states give each wave a copy of the rotated dB/dC
     accumulator rows (16 / N copies)."""
     log(f"case sixteen waves N={n} zoh={zoh} {dtype}")
-    assert _lib.bwd_plan(1, 4096, n)[0] == 16
+    assert _lib.bwd_plan(1, 4096, n, 600, zoh=zoh, io_bf16=dtype == "bf16")[0] == 16
     x, dout, dlast = fused_case(960 + n + zoh, 1, 4096, 600, n, dtype=dtype, zoh=zoh)
     ts, out, last = run_fused(x, dout, dlast, dtype, zoh)
     fw, g = oracle_fused(x, dout, dlast, zoh)
@@ -218,11 +218,50 @@ def test_sixteen_wave_varlen(dtype):
     """Variable lengths on a grid whose backward plan is 16 waves per workgroup: whole chunks
     past a row's length (zero gradients, the adjoint passing through) and an empty row."""
     log(f"case sixteen waves varlen {dtype}")
-    assert _lib.bwd_plan(4, 2048, 16, varlen=True)[0] == 16
+    assert _lib.bwd_plan(4, 2048, 16, 1100, varlen=True, io_bf16=dtype == "bf16")[0] == 16
     x, dout, dlast = fused_case(970, 4, 2048, 1100, 16, dtype=dtype, lens=[1100, 530, 0, 1])
     ts, out, last = run_fused(x, dout, dlast, dtype, False)
     fw, g = oracle_fused(x, dout, dlast, False)
     check_fused(ts, out, last, fw, g, *tol(dtype))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("l", [32, 544, 1024, 2080])
+def test_backward_partial_channel_group(l, dtype):
+    """One, two and five chunks (a ragged last one), 40 channels over workgroups of 12 (a
+    partial last group), every fused extra, initial state and final-state cotangent."""
+    log(f"case backward partial group L={l} {dtype}")
+    assert _lib.bwd_plan(3, 40, 16, l, io_bf16=dtype == "bf16") == (12, 12)
+    x, dout, dlast = fused_case(1000 + l, 3, 40, l, 16, dtype=dtype)
+    ts, out, last = run_fused(x, dout, dlast, dtype, False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    check_fused(ts, out, last, fw, g, *tol(dtype))
+
+
+@pytest.mark.parametrize("lens", [[2080, 600, 0, 31, 545], [512, 513, 1, 1024, 2079]])
+def test_varlen_dead_chunks(lens):
+    """Variable lengths over five chunks: whole chunks past a row's length (zero gradients,
+    the adjoint passing through), a row of length 0, partial chunks; garbage in the
+    padding."""
+    log(f"case varlen dead chunks lens={lens}")
+    x, dout, dlast = fused_case(1100, 5, 40, 2080, 16, lens=lens)
+    ts, out, last = run_fused(x, dout, dlast, "f32", False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    check_fused(ts, out, last, fw, g)
+
+
+def test_no_extras_three_chunks_and_determinism():
+    """Without D, z, delta bias, softplus or initial state (raw positive delta) over three
+    whole chunks, and bit-identical reruns."""
+    log("case no extras, three chunks")
+    x, dout, dlast = fused_case(1200, 2, 64, 1536, 16, extras=False)
+    x["delta"] = np.abs(x["delta"]) * 0.1
+    a = run_fused(x, dout, dlast, "f32", False, softplus=False)
+    fw, g = oracle_fused(x, dout, dlast, False, softplus=False)
+    check_fused(*a, fw, g)
+    b = run_fused(x, dout, dlast, "f32", False, softplus=False)
+    for k in ("u", "delta", "A", "B", "C"):
+        assert torch.equal(a[0][k].grad, b[0][k].grad), k
 
 
 @pytest.mark.parametrize("l", [5, 300, 2100])
@@ -379,7 +418,7 @@ def test_config3_full_size_bf16():
     fp32 accumulation): the 16-wave backward plan the config runs, every output and
     gradient against the oracle on the same bf16-rounded inputs."""
     log("case c3 full size")
-    assert _lib.bwd_plan(C3.batch, C3.dim, C3.dstate)[0] == 16
+    assert _lib.bwd_plan(C3.batch, C3.dim, C3.dstate, C3.length, io_bf16=True)[0] == 16
     x = make_scan_inputs(C3, seed=0, with_z=True, with_dout=True)
     dout = x.pop("dout")
     dlast = np.zeros((C3.batch, C3.dim, C3.dstate), np.float32)
@@ -398,7 +437,8 @@ def test_c5_layer_scan_bf16(zoh):
     backward plan; every output and gradient against the oracle."""
     log(f"case c5 layer scan zoh={zoh}")
     b, d, l, n, r = 8, 1536, 2048, 16, 48
-    assert _lib.bwd_plan(b, d, n)[0] == 16
+    st = _lib.Strides(io_batch=l, io_dim=b * l, bc_batch=l, bc_state=b * l)
+    assert _lib.bwd_plan(b, d, n, l, zoh=zoh, io_bf16=True, strides=st)[0] == 16
     cfg = ScanConfig("c5_layer", b, d, l, n, "bf16", None)
     x = make_scan_inputs(cfg, seed=5 + zoh, with_z=True, with_dout=True)
     dout = x.pop("dout")

@@ -285,10 +285,13 @@ def test_c5_widths_one_layer_matches_oracle(act):
     same weights. The layer's scan runs the 16-wave backward plan of every config-5 layer.
     f32 activations: the config-1 bars (logits 1e-4, gradients 1e-3 of each tensor's scale);
     bf16 activations (config 5's dtype: bf16 GEMM weights and activations, fp32 scan
-    accumulation, fp32 master gradients): logits 2e-2 and gradients 5e-2 of scale."""
+    accumulation, fp32 master gradients): logits 1e-2 and gradients 3e-2 of scale."""
     print(f"case c5 widths one layer act={act}", flush=True)
     cfg = C5
-    assert _lib.bwd_plan(cfg["batch"], cfg["d_model"] * cfg["expand"], cfg["d_state"])[0] == 16
+    st = _lib.Strides(io_batch=cfg["length"], io_dim=cfg["batch"] * cfg["length"], bc_batch=cfg["length"],
+                      bc_state=cfg["batch"] * cfg["length"])
+    assert _lib.bwd_plan(cfg["batch"], cfg["d_model"] * cfg["expand"], cfg["d_state"], cfg["length"],
+                         io_bf16=act == "bf16", strides=st)[0] == 16
     torch.manual_seed(0)
     model = MambaLM(cfg["vocab"], cfg["d_model"], 1, cfg["expand"], cfg["d_state"], cfg["dt_rank"],
                     cfg["d_conv"], device="cuda")
@@ -313,7 +316,7 @@ def test_c5_widths_one_layer_matches_oracle(act):
     err, scale = _max_err_over_scale(logits, ref_logits.detach())
     print(f"  logits max_err={err:.3e} max|ref|={scale:.3e} loss {loss.item():.6f} vs {ref_loss.item():.6f}",
           flush=True)
-    lt, gt = (1e-4, 1e-3) if act == "f32" else (2e-2, 5e-2)
+    lt, gt = (1e-4, 1e-3) if act == "f32" else (1e-2, 3e-2)
     assert err <= lt * scale + (1e-4 if act == "f32" else 0.0)
     assert abs(loss.item() - ref_loss.item()) <= (1e-5 if act == "f32" else 2e-3) * abs(ref_loss.item())
     for k, v in p.items():
