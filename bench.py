@@ -26,6 +26,9 @@ Fields beyond the driver contract:
   complex_c2    the complex-A scan (mss_cfwd + mss_cbwd) at the config-2 shape with the
                 reference's complex A initialisation, and a CPU baseline of the reference's
                 complex path (torch restatement of mamba/mamba1.py:143-176)
+  reference_api_c2  the reference-signature entry points (mss_scan_fwd + mss_scan_bwd_ws,
+                the backward from the forward's chunk_states) at the config-2 shape, and
+                mss_scan_fwd_repeat at the reference README's own shapes beside its numbers
 Inputs are drawn on the GPU from each config's recipe (seeded torch generator).
 """
 from __future__ import annotations
@@ -193,6 +196,93 @@ def run_gpu(torch, cfg, steps, warmup, graph=True):
     del t
     torch.cuda.empty_cache()
     return dict(ms=ms, eager_ms=eager_ms, graph=graph, fwd=fwd, bwd_scan=bws, bwd_reduce=red, lens=lens)
+
+
+def _ref_inputs(torch, b, d, l, n, seed):
+    """The reference benchmark's recipe (benchmarks/benchmark_selective_scan.py:83-92) in the
+    kernel boundary's physical layout: A = -exp(N(0,1)) (D, N); deltas = softplus(N(0,1)),
+    u ~ N(0,1) as [B][D][L]; B, C ~ N(0,1) as [B][N][L]; initial_x ~ N(0,1) (B, D, N)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    r = lambda *shape: torch.randn(*shape, generator=g, device="cuda")
+    return dict(A=-torch.exp(r(d, n)), deltas=torch.nn.functional.softplus(r(b, d, l)), B=r(b, n, l),
+                C=r(b, n, l), u=r(b, d, l), x0=r(b, d, n))
+
+
+def run_reference_api(torch, steps, warmup):
+    """The reference-signature entry points (the XLA-FFI handlers' counterparts, float32,
+    Euler, no fused extras): mss_scan_fwd + mss_scan_bwd_ws at the config-2 shape (the
+    backward starts from the forward's 2048-step chunk_states, as the reference's does), and
+    mss_scan_fwd_repeat with 100 launches per call at the reference README's own shapes
+    (B=1, D=256, N=16, L in {512, 2048, 8192}; mamba/README.md:75-83), per launch."""
+    from mamba_amd import _lib
+    from mamba_amd.configs import C2
+
+    lib = _lib.register_hip_kernel()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    P = lambda t: t.data_ptr()
+
+    def timed(fn, n):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(n):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n
+
+    b, d, l, n = C2.batch, C2.dim, C2.length, C2.dstate
+    x = _ref_inputs(torch, b, d, l, n, 0)
+    y = torch.empty(b, d, l, device="cuda")
+    fin = torch.empty(b, d, n, device="cuda")
+    cs = torch.empty(b, d, -(-l // 2048), n, 2, device="cuda")
+    dy = torch.randn(b, d, l, device="cuda")
+    dfin = torch.zeros(b, d, n, device="cuda")
+    grads = [torch.empty_like(x[k]) for k in ("A", "deltas", "B", "C", "u", "x0")]
+    ws_bytes = int(lib.mss_scan_bwd_workspace_bytes(b, l, d, n))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    fwd_args = (sp, 0, b, l, d, n, P(x["A"]), P(x["deltas"]), P(x["B"]), P(x["C"]), P(x["u"]), P(x["x0"]),
+                P(y), P(fin), P(cs))
+    bwd_args = (sp, b, l, d, n, P(x["A"]), P(x["deltas"]), P(x["B"]), P(x["C"]), P(x["u"]), P(x["x0"]), P(cs),
+                P(dy), P(dfin), *[P(t) for t in grads], P(ws), ws_bytes)
+    fwd = lambda: _lib.check(lib.mss_scan_fwd(*fwd_args), "mss_scan_fwd")
+    bwd = lambda: _lib.check(lib.mss_scan_bwd_ws(*bwd_args), "mss_scan_bwd_ws")
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    ms_fwd = timed(fwd, steps)
+    ms_bwd = timed(bwd, steps)
+    ms_step = timed(lambda: (fwd(), bwd()), steps)
+    log(f"[bench] reference API c2: fwd {ms_fwd:.4f} ms, bwd {ms_bwd:.4f} ms, step {ms_step:.4f} ms")
+    out = {"workload": "mss_scan_fwd + mss_scan_bwd_ws (reference signature, fp32, Euler, no fused extras), "
+                       "B=4 D=1536 L=2048 N=16, reference input recipe",
+           "ms_fwd": round(ms_fwd, 5), "ms_bwd": round(ms_bwd, 5), "ms_fwd_bwd": round(ms_step, 5),
+           "tokens_per_s": round(b * l / (ms_step * 1e-3), 1)}
+    del x, y, fin, cs, dy, dfin, grads, ws
+    published = {512: 0.0282, 2048: 0.0560, 8192: 0.1584}  # A100, mamba/README.md:75-83
+    rows = []
+    for length in (512, 2048, 8192):
+        b, d, n, launches = 1, 256, 16, 100
+        x = _ref_inputs(torch, b, d, length, n, 1)
+        y = torch.empty(b, d, length, device="cuda")
+        fin = torch.empty(b, d, n, device="cuda")
+        cs = torch.empty(b, d, -(-length // 2048), n, 2, device="cuda")
+        args = (sp, 0, launches, b, length, d, n, P(x["A"]), P(x["deltas"]), P(x["B"]), P(x["C"]), P(x["u"]),
+                P(x["x0"]), P(y), P(fin), P(cs))
+        call = lambda: _lib.check(lib.mss_scan_fwd_repeat(*args), "mss_scan_fwd_repeat")
+        call()
+        trials = sorted(timed(call, 1) / launches for _ in range(5))
+        rows.append({"length": length, "ms_per_launch_median": round(trials[2], 5),
+                     "reference_a100_ms": published[length]})
+        log(f"[bench] reference shapes L={length}: {trials[2] * 1e3:.1f} us per launch "
+            f"(reference on A100: {published[length] * 1e3:.1f} us)")
+    out["reference_shapes_fwd"] = {
+        "workload": "mss_scan_fwd_repeat, 100 launches per call, B=1 D=256 N=16, fp32, median of 5 calls",
+        "rows": rows,
+        "note": "reference_a100_ms: the reference's own forward kernel on an A100-SXM4-40GB "
+                "(mamba/README.md:75-83), other hardware, context only"}
+    return out
 
 
 def scan_report(cfg, r):
@@ -543,6 +633,9 @@ def main():
                     help="timed single-token decode steps of the config-5 model (0 skips them)")
     ap.add_argument("--complex-steps", type=int, default=10,
                     help="timed steps of the complex-A scan at the config-2 shape (0 skips them)")
+    ap.add_argument("--reference-api-steps", type=int, default=20,
+                    help="timed steps of the reference-signature entry points at the config-2 shape, "
+                         "plus their forward at the reference's own shapes (0 skips them)")
     ap.add_argument("--train-eager", action="store_true",
                     help="time the config-5 step eagerly only (no HIP graph capture)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -597,6 +690,9 @@ def main():
     decode = None
     if args.decode_steps > 0:
         decode = run_decode_c5(torch, args.decode_steps, graph=not args.train_eager)
+    ref_api = None
+    if args.reference_api_steps > 0:
+        ref_api = run_reference_api(torch, args.reference_api_steps, max(1, args.reference_api_steps // 4))
     cplx = None
     if args.complex_steps > 0:
         cplx = run_complex_c2(torch, args.complex_steps, max(1, args.complex_steps // 4))
@@ -636,6 +732,7 @@ def main():
         "train_c5": train,
         "decode_c5": decode,
         "complex_c2": cplx,
+        "reference_api_c2": ref_api,
     }
     print(json.dumps(result), flush=True)
 

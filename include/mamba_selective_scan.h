@@ -375,13 +375,25 @@ int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, i
                         const float* initial_x, float* y, float* final_x, float* chunk_states);
 
 /* Replaces MambaSelectiveScanBackward (reference native/selective_scan_bwd.cu:166-190),
- * Euler discretization. chunk_states is accepted for signature compatibility and
- * shape-checked; the states this kernel needs are recomputed from initial_x. */
+ * Euler discretization, from the forward's chunk_states as the reference does
+ * (native/upstream_mamba/selective_scan_bwd_kernel.cuh:254-264): each 2048-step block's
+ * state recurrence is re-run from the state chunk_states holds at the previous block's end
+ * (initial_x for the first), all blocks in parallel, giving the state entering every
+ * 8-step segment; then the backward kernels run from those. The reference signature has no
+ * workspace operand, so this call makes one stream-ordered allocation of
+ * mss_scan_bwd_workspace_bytes; mss_scan_bwd_ws takes a caller workspace instead (e.g. an
+ * XLA FFI handler's scratch allocation) and allocates nothing. Outputs are overwritten. */
 int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
                  const float* A, const float* deltas, const float* B, const float* C,
                  const float* u, const float* initial_x, const float* chunk_states,
                  const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
                  float* dC, float* du, float* dinitial_x);
+size_t mss_scan_bwd_workspace_bytes(int32_t batch, int32_t length, int32_t dim, int32_t dstate);
+int mss_scan_bwd_ws(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
+                    const float* A, const float* deltas, const float* B, const float* C,
+                    const float* u, const float* initial_x, const float* chunk_states,
+                    const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
+                    float* dC, float* du, float* dinitial_x, void* workspace, size_t workspace_bytes);
 
 /* Human-readable text for a status code. */
 const char* mss_strerror(int status);

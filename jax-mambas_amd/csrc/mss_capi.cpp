@@ -19,6 +19,7 @@
 
 namespace mss {
 hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
+hipError_t launch_carry_rebuild(const FwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16,
                            hipStream_t stream);
 hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, void* dA, void* dB,
@@ -802,51 +803,56 @@ int mss_scan_fwd(void* stream, int32_t discretization, int32_t batch, int32_t le
                              u, initial_x, y, final_x, chunk_states);
 }
 
-int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
-                 const float* A, const float* deltas, const float* B, const float* C,
-                 const float* u, const float* initial_x, const float* chunk_states,
-                 const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
-                 float* dC, float* du, float* dinitial_x) {
+// Workspace of mss_scan_bwd_ws: the 8-step state carries, then mss_bwd's workspace.
+static size_t scan_bwd_carry_bytes(int32_t batch, int32_t length, int32_t dim, int32_t dstate) {
+  const size_t b = static_cast<size_t>(batch) * dim * dstate * n_seg_of(length) * sizeof(float);
+  return (b + 255) / 256 * 256;
+}
+
+size_t mss_scan_bwd_workspace_bytes(int32_t batch, int32_t length, int32_t dim, int32_t dstate) {
+  if (check_dims(batch, dim, length, dstate) != MSS_OK) return 0;
+  return scan_bwd_carry_bytes(batch, length, dim, dstate) + bwd_layout(batch, dim, length, dstate, false).total;
+}
+
+int mss_scan_bwd_ws(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
+                    const float* A, const float* deltas, const float* B, const float* C,
+                    const float* u, const float* initial_x, const float* chunk_states,
+                    const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
+                    float* dC, float* du, float* dinitial_x, void* workspace, size_t workspace_bytes) {
   int s = check_dims(batch, dim, length, dstate);
   if (s != MSS_OK) return s;
   if (!A || !deltas || !B || !C || !u || !initial_x || !chunk_states || !dout || !dfinal_x || !dA ||
       !ddeltas || !dB || !dC || !du || !dinitial_x)
     return MSS_ERR_INVALID_ARGUMENT;
+  if (workspace == nullptr || !aligned16(workspace) ||
+      workspace_bytes < mss_scan_bwd_workspace_bytes(batch, length, dim, dstate))
+    return MSS_ERR_WORKSPACE;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  // The backward needs the state before every 8-step segment; the reference residual
-  // only holds 2048-step ones, so a states-only forward refreshes them.
-  const size_t carry_bytes =
-      static_cast<size_t>(batch) * dim * dstate * n_seg_of(length) * sizeof(float);
-  float* carries = nullptr;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&carries), carry_bytes, st);
-  if (e != hipSuccess) return hip_fail(e, "allocating carry states");
+  char* ws = static_cast<char*>(workspace);
+  float* carries = reinterpret_cast<float*>(ws);
+  const size_t carry_bytes = scan_bwd_carry_bytes(batch, length, dim, dstate);
+  // The backward re-runs each 8-step segment from the state entering it; the reference
+  // residual holds the state at 2048-step block ends only, so each block's recurrence is
+  // re-run from it first (one state pass, blocks in parallel).
   mss::FwdParams p{};
   p.batch = batch;
   p.dim = dim;
   p.seqlen = length;
   p.dstate = dstate;
-  p.io_sb = static_cast<long long>(dim) * length;
-  p.io_sd = length;
-  p.bc_sb = static_cast<long long>(dstate) * length;
-  p.bc_sn = length;
   const size_t row = static_cast<size_t>(length) * sizeof(float);
   p.vec_io = (row % 16 == 0) && aligned16(u) && aligned16(deltas);
-  p.vec_bc = (row % 16 == 0) && aligned16(B) && aligned16(C);
+  p.vec_bc = (row % 16 == 0) && aligned16(B);
   p.n_seg = n_seg_of(length);
   p.n_ref = (length + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK;
   p.u = u;
   p.delta = deltas;
   p.A = A;
   p.B = B;
-  p.C = C;
   p.x0 = initial_x;
-  p.out = nullptr;  // states only
+  p.ref_states = const_cast<float*>(chunk_states);
   p.carries = carries;
-  e = mss::launch_fwd(p, 0, 0, 0, st);
-  if (e != hipSuccess) {
-    (void)hipFreeAsync(carries, st);
-    return hip_fail(e, "launching carry refresh");
-  }
+  hipError_t e = mss::launch_carry_rebuild(p, st);
+  if (e != hipSuccess) return hip_fail(e, "launching carry rebuild");
   mss_bwd_args a{};
   a.batch = batch;
   a.dim = dim;
@@ -869,10 +875,33 @@ int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32
   a.dB = dB;
   a.dC = dC;
   a.dinitial_state = dinitial_x;
-  s = run_bwd(&a, kPhaseBoth, st);
-  e = hipFreeAsync(carries, st);
+  a.workspace = ws + carry_bytes;
+  a.workspace_bytes = workspace_bytes - carry_bytes;
+  return run_bwd(&a, kPhaseBoth, st);
+}
+
+int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
+                 const float* A, const float* deltas, const float* B, const float* C,
+                 const float* u, const float* initial_x, const float* chunk_states,
+                 const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
+                 float* dC, float* du, float* dinitial_x) {
+  int s = check_dims(batch, dim, length, dstate);
   if (s != MSS_OK) return s;
-  return e == hipSuccess ? MSS_OK : hip_fail(e, "freeing carry states");
+  if (!A || !deltas || !B || !C || !u || !initial_x || !chunk_states || !dout || !dfinal_x || !dA ||
+      !ddeltas || !dB || !dC || !du || !dinitial_x)
+    return MSS_ERR_INVALID_ARGUMENT;
+  // The reference signature has no workspace operand: one stream-ordered allocation per call
+  // (mss_scan_bwd_ws takes a caller's workspace and allocates nothing).
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t bytes = mss_scan_bwd_workspace_bytes(batch, length, dim, dstate);
+  void* ws = nullptr;
+  hipError_t e = hipMallocAsync(&ws, bytes, st);
+  if (e != hipSuccess) return hip_fail(e, "allocating backward workspace");
+  s = mss_scan_bwd_ws(stream, batch, length, dim, dstate, A, deltas, B, C, u, initial_x, chunk_states, dout,
+                      dfinal_x, dA, ddeltas, dB, dC, du, dinitial_x, ws, bytes);
+  e = hipFreeAsync(ws, st);
+  if (s != MSS_OK) return s;
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "freeing backward workspace");
 }
 
 }  // extern "C"

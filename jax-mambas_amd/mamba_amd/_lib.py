@@ -44,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "mss_scan_fwd",
     "mss_scan_fwd_repeat",
     "mss_scan_bwd",
+    "mss_scan_bwd_workspace_bytes",
+    "mss_scan_bwd_ws",
     "mss_conv_bwd_workspace_bytes",
     "mss_conv_fwd",
     "mss_conv_bwd",
@@ -188,6 +190,10 @@ def register_hip_kernel(library_path=None):
     lib.mss_scan_fwd_repeat.restype = ctypes.c_int
     lib.mss_scan_bwd.argtypes = [_p, _i32, _i32, _i32, _i32] + [_p] * 15
     lib.mss_scan_bwd.restype = ctypes.c_int
+    lib.mss_scan_bwd_ws.argtypes = [_p, _i32, _i32, _i32, _i32] + [_p] * 16 + [ctypes.c_size_t]
+    lib.mss_scan_bwd_ws.restype = ctypes.c_int
+    lib.mss_scan_bwd_workspace_bytes.argtypes = [_i32, _i32, _i32, _i32]
+    lib.mss_scan_bwd_workspace_bytes.restype = ctypes.c_size_t
     for name in ("mss_conv_fwd", "mss_conv_bwd"):
         getattr(lib, name).argtypes = [ctypes.POINTER(ConvArgs), _p]
         getattr(lib, name).restype = ctypes.c_int

@@ -253,6 +253,23 @@ def test_reference_entry_points_validate(lib):
     assert lib.mss_scan_bwd(None, 1, 10, 3, 4, *[p] * 14, None) == _lib.MSS_ERR_INVALID_ARGUMENT
 
 
+def test_reference_backward_workspace(lib):
+    """mss_scan_bwd_ws: its workspace holds the 8-step state carries and mss_bwd's workspace;
+    it validates before any HIP call and never allocates."""
+    b, l, d, n = 4, 2048, 1536, 16
+    carries = b * d * n * (l // 8) * 4
+    fused = lib.mss_bwd_workspace_bytes(bwd_args(batch=b, dim=d, seqlen=l, dstate=n))
+    assert lib.mss_scan_bwd_workspace_bytes(b, l, d, n) == carries + fused
+    assert lib.mss_scan_bwd_workspace_bytes(b, l, d, 32) == 0
+    p = ctypes.c_void_p(256)
+    args = [None, 1, 64, 3, 4] + [p] * 15
+    assert lib.mss_scan_bwd_ws(*args, None, 1 << 30) == _lib.MSS_ERR_WORKSPACE
+    assert lib.mss_scan_bwd_ws(*args, p, 16) == _lib.MSS_ERR_WORKSPACE
+    assert lib.mss_scan_bwd_ws(*args, ctypes.c_void_p(8), 1 << 30) == _lib.MSS_ERR_WORKSPACE
+    assert lib.mss_scan_bwd_ws(None, 1, 64, 3, 32, *[p] * 15, p, 1 << 30) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_scan_bwd_ws(None, 1, 64, 3, 4, *[p] * 14, None, p, 1 << 30) == _lib.MSS_ERR_INVALID_ARGUMENT
+
+
 def test_strerror(lib):
     assert lib.mss_strerror(0) == b"ok"
     assert b"invalid" in lib.mss_strerror(1)

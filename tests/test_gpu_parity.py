@@ -354,18 +354,23 @@ def test_strided_row_layouts(dtype, l):
     check_fused(ts_c, out_c, last_c, fw, g, *tol)
 
 
-def test_reference_c_entry_points():
-    """mss_scan_fwd / mss_scan_bwd (the reference FFI handlers' counterparts) via ctypes."""
-    log("case reference C entry points")
+@pytest.mark.parametrize("length", [2500, 5000])
+def test_reference_c_entry_points(length):
+    """mss_scan_fwd / mss_scan_bwd / mss_scan_bwd_ws (the reference FFI handlers'
+    counterparts) via ctypes, over two and three 2048-step blocks: the backward re-runs each
+    block from the forward's chunk_states. The workspace variant equals mss_scan_bwd bit for
+    bit; chunk_states from the float64 oracle give the same gradients to the float32 bar, and
+    a corrupted block state changes them (the residual is what the backward starts from)."""
+    log(f"case reference C entry points L={length}")
     lib = _lib.register_hip_kernel()
-    A, deltas, Bs, Cs, u, x0 = ref_recipe(13, batch=2, length=2500, dim=8, n=16)
+    A, deltas, Bs, Cs, u, x0 = ref_recipe(13, batch=2, length=length, dim=8, n=16)
     b, l, d = u.shape
     n = A.shape[1]
     tr = lambda a: T(np.swapaxes(a, 1, 2))  # physical [B][D][L] / [B][N][L]
     tA, td, tB, tC, tu, tx0 = T(A), tr(deltas), tr(Bs), tr(Cs), tr(u), T(x0)
     y = torch.empty(b, d, l, device=dev)
     fin = torch.empty(b, d, n, device=dev)
-    cs = torch.empty(b, d, 2, n, 2, device=dev)
+    cs = torch.empty(b, d, -(-l // 2048), n, 2, device=dev)
     st = torch.cuda.current_stream().cuda_stream
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     _lib.check(lib.mss_scan_fwd(st, 0, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu), P(tx0), P(y), P(fin), P(cs)),
@@ -373,19 +378,41 @@ def test_reference_c_entry_points():
     rng = np.random.default_rng(14)
     dy = rng.standard_normal((b, l, d)).astype(np.float32)
     dfin = rng.standard_normal((b, d, n)).astype(np.float32)
-    outs = [torch.empty_like(t) for t in (tA, td, tB, tC, tu, tx0)]
-    _lib.check(lib.mss_scan_bwd(st, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu), P(tx0), P(cs), P(tr(dy)),
-                                P(T(dfin)), *[P(o) for o in outs]), "mss_scan_bwd")
-    torch.cuda.synchronize()
+    tdy, tdfin = tr(dy), T(dfin)
+
+    def backward(states, ws=None):
+        outs = [torch.full_like(t, float("nan")) for t in (tA, td, tB, tC, tu, tx0)]
+        args = (st, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu), P(tx0), P(states), P(tdy), P(tdfin),
+                *[P(o) for o in outs])
+        if ws is None:
+            _lib.check(lib.mss_scan_bwd(*args), "mss_scan_bwd")
+        else:
+            _lib.check(lib.mss_scan_bwd_ws(*args, P(ws), ws.numel()), "mss_scan_bwd_ws")
+        torch.cuda.synchronize()
+        return outs
+
+    outs = backward(cs)
+    ws_bytes = int(lib.mss_scan_bwd_workspace_bytes(b, l, d, n))
+    outs_ws = backward(cs, torch.empty(ws_bytes, dtype=torch.uint8, device=dev))
+    for o, w in zip(outs, outs_ws):
+        assert torch.equal(o, w)
     ey, efin, ecs = scan64.reference_api_forward(A, deltas, Bs, Cs, u, x0)
     close("y", y.transpose(1, 2), ey)
     close("final_x", fin, efin)
     close("chunk_states", cs, ecs)
     grads, ab = scan64.reference_api_backward(A, deltas, Bs, Cs, u, x0, dy, dfin, abs_terms=True)
     names = ["dA", "ddeltas", "dBs", "dCs", "du", "dinitial_x"]
-    for name, o, g in zip(names, outs, grads):
-        got = o if o.shape == g.shape else o.transpose(1, 2)
-        close(name, got, g, scale=ab.get(name))
+    for label, res in (("gpu chunk_states", outs), ("oracle chunk_states", backward(T(ecs)))):
+        log(f"  from {label}")
+        for name, o, g in zip(names, res, grads):
+            got = o if o.shape == g.shape else o.transpose(1, 2)
+            close(name, got, g, scale=ab.get(name))
+    bad = cs.clone()
+    bad[:, :, 0, :, 1] += 1.0  # the state entering block 1
+    moved = backward(bad)
+    # dC = sum_d g h depends on the forward states: block 1's steps move, block 0's do not
+    assert torch.equal(moved[3][:, :, :2048], outs[3][:, :, :2048])
+    assert not torch.equal(moved[3][:, :, 2048:4096], outs[3][:, :, 2048:4096])
 
 
 def config_tensors(cfg, x, dout):
