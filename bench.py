@@ -302,6 +302,15 @@ def scan_report(cfg, r):
         "hbm_frac": {"fwd": frac(fwd_b, r["fwd"]), "bwd": frac(bwd_b, r["bwd_scan"] + r["bwd_reduce"]),
                      "fwd_bwd": frac(fwd_b + bwd_b, r["ms"])},
     }
+    # The config's dominant kernel (the backward scan) against the HBM roofline, as the
+    # headline line's `roofline`; `traffic` = measured HBM bytes per launch of that kernel and
+    # workload (profiles/bwd_scan_<config>_traffic.txt), or null.
+    kern = f"bwd_scan_{cfg.name}"
+    achieved = bwd_b / (r["bwd_scan"] * 1e-3) / 1e9
+    rep["roofline"] = {"bound": "hbm", "kernel": kern, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(kern),
+                       "algorithmic_bytes": int(bwd_b), "avg_launch_ms": round(r["bwd_scan"], 5),
+                       "fwd_traffic": read_traffic(f"fwd_{cfg.name}")}
     if lens is not None:
         rep["seq_lens"] = [int(x) for x in lens]
         rep["valid_fraction"] = round(float(np.sum(lens)) / (cfg.batch * cfg.length), 4)
