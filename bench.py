@@ -54,14 +54,24 @@ def log(msg):
 
 
 def cpu_model():
-    """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
+    """The host CPU for the CPU baselines: /proc/cpuinfo's model name (a VM may show only
+    the vendor's family name), its family/model/stepping numbers and the logical CPUs."""
+    fields = {}
+    n_cpus = 0
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "processor":
+                n_cpus += 1
+            elif key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                fields[key] = val.strip()
     except OSError:
-        pass
-    return None
+        return None
+    if "model name" not in fields:
+        return None
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{fields['model name']} ({ids}; {n_cpus} logical CPUs on the host)"
 
 
 def read_traffic(kernel_tag):

@@ -32,16 +32,19 @@ __device__ __forceinline__ float to_f32(bf16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
 }
 __device__ __forceinline__ void store_as(float* p, float v) { *p = v; }
+// float32 -> bf16, round to nearest even (NaN stays NaN): gfx950's v_cvt_pk_bf16_f32, one
+// instruction per two values (the compiler selects it for these conversions).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
   bf16_t r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
-    r.bits = static_cast<uint16_t>(u >> 16);
-  }
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
   return r;
+}
+// Two values as one bf16 pair, `lo` in bits 0..15.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 __device__ __forceinline__ void store_as(bf16_t* p, float v) { *p = f32_to_bf16(v); }
 
@@ -203,10 +206,7 @@ __device__ __forceinline__ void store_seg(bf16_t* __restrict__ row, int t, int L
     for (int q = 0; q < N / 8; ++q) {
       uint32_t w[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        w[k] = static_cast<uint32_t>(f32_to_bf16(v[8 * q + 2 * k]).bits) |
-               (static_cast<uint32_t>(f32_to_bf16(v[8 * q + 2 * k + 1]).bits) << 16);
-      }
+      for (int k = 0; k < 4; ++k) w[k] = pack_bf16x2(v[8 * q + 2 * k], v[8 * q + 2 * k + 1]);
       const u32x4 x = {w[0], w[1], w[2], w[3]};
       p[q] = x;
     }

@@ -58,8 +58,7 @@ __device__ __forceinline__ void store_vec(io_t* __restrict__ p, const float (&v)
     unsigned w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      w[i] = static_cast<unsigned>(f32_to_bf16(v[2 * i]).bits) |
-             (static_cast<unsigned>(f32_to_bf16(v[2 * i + 1]).bits) << 16);
+      w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     a.x = w[0]; a.y = w[1]; a.z = w[2]; a.w = w[3];
     *reinterpret_cast<u32x4*>(p) = a;
   }

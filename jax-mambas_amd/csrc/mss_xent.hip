@@ -97,8 +97,7 @@ __global__ __launch_bounds__(kXentThreads) void xent_bwd_kernel(XentParams p) {
       for (int j = 0; j < 4; ++j) {
         float g0 = fast_exp2((v[2 * j] - l) * kLog2e) - (8LL * i + 2 * j == tgt ? 1.f : 0.f);
         float g1 = fast_exp2((v[2 * j + 1] - l) * kLog2e) - (8LL * i + 2 * j + 1 == tgt ? 1.f : 0.f);
-        w[j] = static_cast<unsigned>(f32_to_bf16(g0 * scale).bits) |
-               (static_cast<unsigned>(f32_to_bf16(g1 * scale).bits) << 16);
+        w[j] = pack_bf16x2(g0 * scale, g1 * scale);
       }
       u32x4 o;
       o.x = w[0]; o.y = w[1]; o.z = w[2]; o.w = w[3];
