@@ -302,6 +302,63 @@ def test_bf16(l):
     check_fused(ts, out, last, fw, g, rtol=BF16_RTOL, atol=BF16_RTOL * 0.05)
 
 
+@pytest.mark.parametrize("length", [1024, 999])
+def test_bf16_store_rounding_bit_exact(length):
+    """bf16 outputs are float32 results rounded to nearest, ties to even, bit for bit: with
+    delta = 0 and no softplus every a_bar is 1 and every b_bar*u is 0, so the state stays zero
+    and out = D*u is one float32 product, whose bf16 rounding must equal the integer
+    round-to-nearest-even of the same product (configs.round_to_bf16). Channels cover exact
+    ties (powers of two times 1 + 2^-8, which round down to even), carries into the exponent,
+    products past the largest bf16 (round to inf), subnormals and random values; an odd length
+    also takes the per-element store path of the last chunk."""
+    from mamba_amd.configs import round_to_bf16
+    log(f"case bf16 store rounding L={length}")
+    b, d, l, n = 2, 8, length, 4
+    rng = np.random.default_rng(77 + length)
+    f = np.float32
+    base = rng.standard_normal((b, d, l)).astype(f)
+    u = np.empty((b, d, l), f)
+    Dv = np.empty(d, f)
+    u[:, 0] = base[:, 0]
+    Dv[0] = f(0.7)
+    u[:, 1] = base[:, 1] * f(1e3)
+    Dv[1] = f(1.0 + 3 * 2.0 ** -9)
+    pw = np.ldexp(np.ones((b, l), f), rng.integers(-20, 20, (b, l))).astype(f)
+    u[:, 2] = pw * np.where(rng.random((b, l)) < 0.5, f(1), f(-1))
+    Dv[2] = f(1.0 + 2.0 ** -8)  # exact ties: round to the even neighbour (down)
+    u[:, 3] = (1 + rng.integers(0, 128, (b, l)).astype(f) / 128) * pw
+    Dv[3] = f(1.0 + 2.0 ** -8)  # ties, carries, and values just above a tie
+    u[:, 4] = np.ldexp(f(1) + rng.integers(120, 128, (b, l)).astype(f) / 128, 127).astype(f)
+    Dv[4] = f(1.0 + 2.0 ** -8)  # near the largest bf16: some products round to inf
+    u[:, 5] = base[:, 5] * f(2.0 ** -130)  # float32 subnormals
+    Dv[5] = f(1.3)
+    u[:, 6] = base[:, 6] * f(1e-30)
+    Dv[6] = f(1.0 + 2.0 ** -12)
+    u[:, 7] = base[:, 7] * f(3e37)
+    Dv[7] = f(0.999)
+    u = round_to_bf16(u)
+    u[u == 0] = 0  # -0 inputs: the state sum adds C*h = +0 to D*u, and -0 + +0 = +0
+    with np.errstate(over="ignore"):
+        prod = u * Dv[None, :, None]
+    want = (round_to_bf16(prod).view(np.uint32) >> 16).astype(np.uint16)
+    A = -np.ones((d, n), f)
+    Bm = rng.standard_normal((b, n, l)).astype(f)
+    Cm = rng.standard_normal((b, n, l)).astype(f)
+    out = selective_scan_fn(T(u, torch.bfloat16), T(np.zeros((b, d, l), f), torch.bfloat16), T(A),
+                            T(Bm, torch.bfloat16), T(Cm, torch.bfloat16), D=T(Dv), delta_softplus=False)
+    torch.cuda.synchronize()
+    got = out.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+    bad = got != want
+    for ch in range(d):
+        nb = int(bad[:, ch].sum())
+        if nb:
+            i = np.argwhere(bad[:, ch])[0]
+            log(f"  channel {ch}: {nb} mismatches, e.g. u={u[i[0], ch, i[1]]!r} D={Dv[ch]!r} "
+                f"got=0x{int(got[i[0], ch, i[1]]):04x} want=0x{int(want[i[0], ch, i[1]]):04x}")
+    assert np.isinf(prod[:, 4]).sum() == 0 and np.isinf(round_to_bf16(prod[:, 4])).any()
+    assert not bad.any()
+
+
 def test_deterministic_rerun():
     log("case determinism")
     x, dout, dlast = fused_case(600, 2, 64, 1500, 16)
