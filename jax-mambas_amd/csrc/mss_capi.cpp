@@ -824,6 +824,8 @@ int mss_scan_bwd_ws(void* stream, int32_t batch, int32_t length, int32_t dim, in
   if (!A || !deltas || !B || !C || !u || !initial_x || !chunk_states || !dout || !dfinal_x || !dA ||
       !ddeltas || !dB || !dC || !du || !dinitial_x)
     return MSS_ERR_INVALID_ARGUMENT;
+  // The carry rebuild runs one grid slice per 2048-step block (grid.z).
+  if ((length + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK > 65535) return MSS_ERR_UNSUPPORTED;
   if (workspace == nullptr || !aligned16(workspace) ||
       workspace_bytes < mss_scan_bwd_workspace_bytes(batch, length, dim, dstate))
     return MSS_ERR_WORKSPACE;
@@ -890,6 +892,7 @@ int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32
   if (!A || !deltas || !B || !C || !u || !initial_x || !chunk_states || !dout || !dfinal_x || !dA ||
       !ddeltas || !dB || !dC || !du || !dinitial_x)
     return MSS_ERR_INVALID_ARGUMENT;
+  if ((length + MSS_REF_CHUNK - 1) / MSS_REF_CHUNK > 65535) return MSS_ERR_UNSUPPORTED;
   // The reference signature has no workspace operand: one stream-ordered allocation per call
   // (mss_scan_bwd_ws takes a caller's workspace and allocates nothing).
   const hipStream_t st = static_cast<hipStream_t>(stream);

@@ -268,6 +268,9 @@ def test_reference_backward_workspace(lib):
     assert lib.mss_scan_bwd_ws(*args, ctypes.c_void_p(8), 1 << 30) == _lib.MSS_ERR_WORKSPACE
     assert lib.mss_scan_bwd_ws(None, 1, 64, 3, 32, *[p] * 15, p, 1 << 30) == _lib.MSS_ERR_UNSUPPORTED
     assert lib.mss_scan_bwd_ws(None, 1, 64, 3, 4, *[p] * 14, None, p, 1 << 30) == _lib.MSS_ERR_INVALID_ARGUMENT
+    # more 2048-step blocks than the carry rebuild's grid holds
+    assert lib.mss_scan_bwd_ws(None, 1, 65535 * 2048 + 1, 3, 4, *[p] * 15, p, 1 << 62) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_scan_bwd(None, 1, 65535 * 2048 + 1, 3, 4, *[p] * 15) == _lib.MSS_ERR_UNSUPPORTED
 
 
 def test_strerror(lib):
