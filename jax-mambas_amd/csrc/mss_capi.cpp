@@ -383,7 +383,9 @@ const char* mss_strerror(int status) {
   switch (status) {
     case MSS_OK: return "ok";
     case MSS_ERR_INVALID_ARGUMENT: return "invalid argument";
-    case MSS_ERR_UNSUPPORTED: return "unsupported configuration (dstate <= 16, batch * 2 * dstate <= 65535)";
+    case MSS_ERR_UNSUPPORTED:
+      return "unsupported configuration (a size beyond this build's limits, e.g. dstate > 16 or "
+             "batch * 2 * dstate > 65535; each entry point's limits are in mamba_selective_scan.h)";
     case MSS_ERR_HIP: return "HIP runtime error";
     case MSS_ERR_WORKSPACE: return "workspace too small";
     case MSS_ERR_SCRATCH_LIMIT:
