@@ -45,8 +45,16 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 7
+#define MSS_ABI_VERSION 8
+/* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
+ * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
+ * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
+ * handlers accept N <= 256, reference native/selective_scan_cuda.cu:34, 410-411); their
+ * backward runs over groups of at most MSS_MAX_DSTATE states, so mss_bwd_scan /
+ * mss_bwd_reduce (split phases) stay at MSS_MAX_DSTATE. MSS_MAX_DSTATE for bf16 scans, the
+ * complex-A scan, the decode steps and the split phases. */
 #define MSS_MAX_DSTATE 16
+#define MSS_MAX_DSTATE_WIDE 256
 #define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
 #define MSS_NOALLOC_SCRATCH_BYTES (128u << 20) /* fixed per-device scratch of mss_bwd_noalloc */

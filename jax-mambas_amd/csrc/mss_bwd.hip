@@ -137,8 +137,13 @@ __device__ __forceinline__ void stage_chunk(const bc_t* __restrict__ Bb, const b
   }
 }
 
-template <int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t>
+// kGroup: 0 = the whole state dimension; 1 = the first state group of a float32 scan with
+// more than kMaxN states (A, the state buffers and the carries read with the strides of the
+// full tensors, p.a_ld / p.state_ld / p.carry_cs; dz only where p.dz is given); 2 = a later
+// group (as 1, and du/ddelta add to the values already in their buffers).
+template <int kW, bool kZOH, bool kHasZ, typename io_t, typename bc_t, int kGroup = 0>
 __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
+  constexpr bool kAcc = kGroup == 2;
   constexpr int kT = kBwdT;
   constexpr int kChunk = kBwdChunk;
   constexpr int kRowSlots = kChunk * static_cast<int>(sizeof(bc_t)) / 16;
@@ -164,6 +169,10 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   const int L = p.seqlen;
   const int N = p.dstate;
   const int K = p.chan_per_block / kW;
+  const int a_ld = kGroup ? p.a_ld : N;
+  const int st_ld = kGroup ? p.state_ld : N;
+  const long long carry_cs = kGroup ? p.carry_cs : static_cast<long long>(N) * p.n_seg;
+  const bool has_dz = kGroup ? p.dz != nullptr : true;  // (z given: dz given, ungrouped)
   const int len = p.seq_lens ? min(max(p.seq_lens[b], 0), L) : L;
   const bool vec_io = p.vec_io != 0;
   const bool dma = p.vec_bc != 0;
@@ -182,7 +191,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
     const int d = blk * p.chan_per_block + cl;
     if (lane < kMaxN) {
       float mu0 = 0.f;
-      if (d < p.dim && lane < N && p.dlast) mu0 = p.dlast[(static_cast<size_t>(b) * p.dim + d) * N + lane];
+      if (d < p.dim && lane < N && p.dlast) mu0 = p.dlast[(static_cast<size_t>(b) * p.dim + d) * st_ld + lane];
       s_mu[cl][lane] = mu0;
       s_dA[cl][lane] = 0.f;
     }
@@ -216,11 +225,14 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         float zero[kT];
 #pragma unroll
         for (int j = 0; j < kT; ++j) zero[j] = 0.f;
-        store_seg<kT>(static_cast<io_t*>(p.du) + row, tl, L, fast, zero);
-        store_seg<kT>(static_cast<io_t*>(p.ddelta) + row, tl, L, fast, zero);
-        if constexpr (kHasZ) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, zero);
+        if constexpr (!kAcc) {  // (accumulating: adding zero changes nothing)
+          store_seg<kT>(static_cast<io_t*>(p.du) + row, tl, L, fast, zero);
+          store_seg<kT>(static_cast<io_t*>(p.ddelta) + row, tl, L, fast, zero);
+        }
+        if constexpr (kHasZ)
+          if (has_dz) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, zero);
         if (c == 0 && p.dinit && lane < N)
-          p.dinit[(static_cast<size_t>(b) * p.dim + d) * N + lane] = s_mu[cl][lane];
+          p.dinit[(static_cast<size_t>(b) * p.dim + d) * st_ld + lane] = s_mu[cl][lane];
       }
       // ... and this block's dB/dC partials of the chunk are zero.
       const size_t nl = static_cast<size_t>(N) * L;
@@ -243,12 +255,12 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
       // Carries of this channel and chunk: a uniform base per state plus the lane's segment,
       // so the loads take a scalar base and a fixed per-lane offset (no per-load address
       // registers for later instructions to wait on).
-      const float* __restrict__ carry_chunk = p.carries + chan * N * p.n_seg + t0 / kT;
+      const float* __restrict__ carry_chunk = p.carries + chan * carry_cs + t0 / kT;
 
       // ---- per-step inputs of the row
       // A row through LDS: a global load feeding the state loop would put a wait on all
       // outstanding loads (the carry prefetch included) inside the loop.
-      if (lane < N) s_A[w][lane] = p.A[static_cast<size_t>(d) * N + lane];
+      if (lane < N) s_A[w][lane] = p.A[static_cast<size_t>(d) * a_ld + lane];
       const float Dv = p.D ? p.D[d] : 0.f;
       const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
       float dlt[kT], dlu[kT], uu[kT], g[kT], s1[kT], s2[kT];
@@ -274,7 +286,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
             yp[j] = go * yp[j] * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
             g[j] = go * zr[j] * sz;
           }
-          if (active) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);
+          if (active && has_dz) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);
         }
 #pragma unroll
         for (int j = 0; j < kT; ++j) {
@@ -383,7 +395,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         const float S = wave_sum_to_last(dA_pend);
         if (lane == 63) s_dA[cl][n_pend] += S;
       }
-      if (c == 0 && p.dinit && lane < N) p.dinit[chan * N + lane] = s_mu[cl][lane];
+      if (c == 0 && p.dinit && lane < N) p.dinit[chan * st_ld + lane] = s_mu[cl][lane];
 
       // ---- per-step gradients of the row
       if constexpr (!kZOH) {
@@ -414,6 +426,15 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         db_acc += dd_j;
         duv[j] = du_j;
         ddv[j] = dd_j;
+      }
+      if constexpr (kAcc) {
+        float prev[kT];
+        load_seg<kT>(static_cast<const io_t*>(p.du) + row, tl, L, fast, prev);
+#pragma unroll
+        for (int j = 0; j < kT; ++j) duv[j] += prev[j];
+        load_seg<kT>(static_cast<const io_t*>(p.ddelta) + row, tl, L, fast, prev);
+#pragma unroll
+        for (int j = 0; j < kT; ++j) ddv[j] += prev[j];
       }
       store_seg<kT>(static_cast<io_t*>(p.du) + row, tl, L, fast, duv);
       store_seg<kT>(static_cast<io_t*>(p.ddelta) + row, tl, L, fast, ddv);
@@ -484,7 +505,9 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
 //     ([block][b][B|C][n][t], block stride `stride` floats). The block's row is
 //     blockIdx / x_blocks = (b, which, n); threads walk the row's steps, 4 at a time (16-byte
 //     loads) when kVec (L a multiple of 4), keeping 4 blocks' loads in flight;
-//   the remaining blocks: dA[d][n] = sum_b part_dA[b][d][n]; dD[d], dbias[d] likewise.
+//   the remaining blocks: dA[d][n] = sum_b part_dA[b][d][n] (dA rows a_ld apart); dD[d],
+//     dbias[d] likewise (dbias added to its current value when acc_bias: a state group of a
+//     wider scan).
 template <bool kVec, typename bc_t>
 __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ part, int n_blk,
                                                      size_t stride, int L, int N, int x_blocks,
@@ -493,15 +516,15 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
                                                      const float* __restrict__ part_dA,
                                                      const float* __restrict__ part_dD,
                                                      const float* __restrict__ part_db, int batch,
-                                                     int dim, int na, float* dA, float* dD,
-                                                     float* dbias) {
+                                                     int dim, int na, int a_ld, int acc_bias,
+                                                     float* dA, float* dD, float* dbias) {
   if (static_cast<int>(blockIdx.x) >= n_bc_blocks) {
     const int dn = dim * na;  // dA row width: dstate (real A) or 2 * dstate (complex A)
     const int i = (blockIdx.x - n_bc_blocks) * blockDim.x + threadIdx.x;
     if (i < dn) {
       float s = 0.f;
       for (int bb = 0; bb < batch; ++bb) s += part_dA[static_cast<size_t>(bb) * dn + i];
-      dA[i] = s;
+      dA[static_cast<size_t>(i / na) * a_ld + i % na] = s;
     } else if (i < dn + 2 * dim) {
       const int which = (i - dn) / dim;
       const int dd = (i - dn) - which * dim;
@@ -510,7 +533,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
       if (dst != nullptr) {
         float s = 0.f;
         for (int bb = 0; bb < batch; ++bb) s += src[static_cast<size_t>(bb) * dim + dd];
-        dst[dd] = s;
+        dst[dd] = (acc_bias && which == 1) ? dst[dd] + s : s;
       }
     }
     return;
@@ -554,17 +577,28 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
   }
 }
 
-template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
-static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
+template <bool kZOH, bool kHasZ, typename io_t, typename bc_t, int kGroup>
+static hipError_t launch_bwd_a(const BwdParams& p, hipStream_t stream) {
   dim3 grid(p.n_blocks_d, p.batch);
   if (p.waves == 16) {
     if (!bwd_waves_fit(16, p.dstate) || p.chan_per_block % 16 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((bwd_kernel<16, kZOH, kHasZ, io_t, bc_t>), grid, dim3(16 * 64), 0, stream, p);
+    hipLaunchKernelGGL((bwd_kernel<16, kZOH, kHasZ, io_t, bc_t, kGroup>), grid, dim3(16 * 64), 0, stream, p);
   } else {
     if (p.waves != 12 || p.chan_per_block % 12 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((bwd_kernel<12, kZOH, kHasZ, io_t, bc_t>), grid, dim3(12 * 64), 0, stream, p);
+    hipLaunchKernelGGL((bwd_kernel<12, kZOH, kHasZ, io_t, bc_t, kGroup>), grid, dim3(12 * 64), 0, stream, p);
   }
   return hipGetLastError();
+}
+
+template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
+static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
+  if (p.dstate == p.a_ld) return launch_bwd_a<kZOH, kHasZ, io_t, bc_t, 0>(p, stream);
+  // state groups of a wider scan exist only for float32 scans
+  if constexpr (sizeof(io_t) == 4 && sizeof(bc_t) == 4) {
+    if (p.acc_out) return launch_bwd_a<kZOH, kHasZ, io_t, bc_t, 2>(p, stream);
+    return launch_bwd_a<kZOH, kHasZ, io_t, bc_t, 1>(p, stream);
+  }
+  return hipErrorInvalidValue;
 }
 
 template <typename io_t, typename bc_t>
@@ -619,8 +653,8 @@ hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16
                  : launch_bwd_io<float, float>(p, zoh, stream);
 }
 
-hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, void* dA, void* dB,
-                             void* dC, float* dD, float* dbias, hipStream_t stream) {
+hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, int a_ld, int acc_bias,
+                             void* dA, void* dB, void* dC, float* dD, float* dbias, hipStream_t stream) {
   const int L = p.seqlen;
   const bool vec = (L % 4) == 0;  // partial rows are 16-byte aligned (block stride: 64 floats)
   const int nvec = vec ? L / 4 : L;
@@ -632,7 +666,7 @@ hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, void*
   hipLaunchKernelGGL((reduce_kernel<VEC, T>), grid, dim3(256), 0, stream, p.part_dBC, p.n_blocks_d, \
                      p.part_stride, L, p.dstate, x_blocks, n_bc_blocks, p.bc_sb, p.bc_sn,          \
                      static_cast<T*>(dB), static_cast<T*>(dC), p.part_dA, p.part_dD, p.part_dbias,  \
-                     p.batch, p.dim, a_width, static_cast<float*>(dA), dD, dbias)
+                     p.batch, p.dim, a_width, a_ld, acc_bias, static_cast<float*>(dA), dD, dbias)
   if (bc_bf16) {
     if (vec) MSS_REDUCE(true, bf16_t); else MSS_REDUCE(false, bf16_t);
   } else {

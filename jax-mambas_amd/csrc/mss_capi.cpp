@@ -22,8 +22,8 @@ hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hip
 hipError_t launch_carry_rebuild(const FwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16,
                            hipStream_t stream);
-hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, void* dA, void* dB,
-                             void* dC, float* dD, float* dbias, hipStream_t stream);
+hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, int a_ld, int acc_bias,
+                             void* dA, void* dB, void* dC, float* dD, float* dbias, hipStream_t stream);
 BwdPlan bwd_plan(int batch, int dim, int dstate, int varlen);
 hipError_t launch_cfwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
 hipError_t launch_cbwd_scan(const BwdParams& p, int zoh, int io_bf16, int bc_bf16, hipStream_t stream);
@@ -57,14 +57,31 @@ size_t dtype_size(int dt) { return dt == MSS_BF16 ? 2 : 4; }
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned8(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
-int check_dims(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate) {
+// max_dstate: MSS_MAX_DSTATE, or MSS_MAX_DSTATE_WIDE for the float32 real-A scans (the
+// backward then runs over groups of at most MSS_MAX_DSTATE states).
+int check_dims(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate,
+               int32_t max_dstate = MSS_MAX_DSTATE) {
   if (batch <= 0 || dim <= 0 || seqlen <= 0) return MSS_ERR_INVALID_ARGUMENT;
-  if (dstate <= 0 || dstate > 256) return MSS_ERR_INVALID_ARGUMENT;
-  if (dstate > MSS_MAX_DSTATE) return MSS_ERR_UNSUPPORTED;
-  // Grid limits: batch rows (and the dB/dC reduction's batch*2*dstate rows) on grid.y.
-  if (static_cast<long long>(batch) * 2 * dstate > 65535) return MSS_ERR_UNSUPPORTED;
+  if (dstate <= 0 || dstate > MSS_MAX_DSTATE_WIDE) return MSS_ERR_INVALID_ARGUMENT;
+  if (dstate > max_dstate) return MSS_ERR_UNSUPPORTED;
+  // Grid limits: batch rows (and the dB/dC reduction's batch*2*dstate rows, per state
+  // group) on grid.y.
+  if (static_cast<long long>(batch) * 2 * (dstate < MSS_MAX_DSTATE ? dstate : MSS_MAX_DSTATE) > 65535)
+    return MSS_ERR_UNSUPPORTED;
   // Index arithmetic inside the kernels uses 64-bit offsets; per-row steps are int.
   return MSS_OK;
+}
+
+// Largest dstate of a scan with these dtypes: wide for float32 real-A scans.
+int32_t max_dstate_for(int32_t io_dtype, int32_t bc_dtype, bool cplx) {
+  return (!cplx && io_dtype == MSS_F32 && bc_dtype == MSS_F32) ? MSS_MAX_DSTATE_WIDE : MSS_MAX_DSTATE;
+}
+
+// State groups of a backward wider than MSS_MAX_DSTATE: G balanced groups, group g holding
+// states [group_begin(g), group_begin(g + 1)).
+int state_groups(int32_t dstate) { return (dstate + MSS_MAX_DSTATE - 1) / MSS_MAX_DSTATE; }
+int group_begin(int32_t dstate, int g) {
+  return static_cast<int>(static_cast<long long>(g) * dstate / state_groups(dstate));
 }
 
 int check_common(int32_t discretization, int32_t softplus, int32_t io_dtype, int32_t bc_dtype) {
@@ -142,22 +159,34 @@ BwdLayout bwd_layout(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate,
   return l;
 }
 
-int validate_fwd(const mss_fwd_args* a) {
+// Workspace layout of a backward call: for more than MSS_MAX_DSTATE states the groups run
+// one after another in one workspace, sized for the larger of the two group sizes (its
+// plan is the one reported for the call).
+BwdLayout bwd_layout_call(int32_t batch, int32_t dim, int32_t seqlen, int32_t dstate, bool varlen,
+                          bool cplx = false) {
+  if (cplx || dstate <= MSS_MAX_DSTATE) return bwd_layout(batch, dim, seqlen, dstate, varlen, cplx);
+  const int G = state_groups(dstate);
+  const BwdLayout hi = bwd_layout(batch, dim, seqlen, (dstate + G - 1) / G, varlen);
+  const BwdLayout lo = bwd_layout(batch, dim, seqlen, dstate / G, varlen);
+  return hi.total >= lo.total ? hi : lo;
+}
+
+int validate_fwd(const mss_fwd_args* a, bool cplx = false) {
   if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
-  int s = check_dims(a->batch, a->dim, a->seqlen, a->dstate);
+  int s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
   if (s != MSS_OK) return s;
-  s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
+  s = check_dims(a->batch, a->dim, a->seqlen, a->dstate, max_dstate_for(a->io_dtype, a->bc_dtype, cplx));
   if (s != MSS_OK) return s;
   if (!a->u || !a->delta || !a->A || !a->B || !a->C || !a->out) return MSS_ERR_INVALID_ARGUMENT;
   Strides st;
   return resolve_strides(a->strides, a->batch, a->dim, a->seqlen, a->dstate, &st);
 }
 
-int validate_bwd(const mss_bwd_args* a) {
+int validate_bwd(const mss_bwd_args* a, bool cplx = false) {
   if (a == nullptr) return MSS_ERR_INVALID_ARGUMENT;
-  int s = check_dims(a->batch, a->dim, a->seqlen, a->dstate);
+  int s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
   if (s != MSS_OK) return s;
-  s = check_common(a->discretization, a->delta_softplus, a->io_dtype, a->bc_dtype);
+  s = check_dims(a->batch, a->dim, a->seqlen, a->dstate, max_dstate_for(a->io_dtype, a->bc_dtype, cplx));
   if (s != MSS_OK) return s;
   if (!a->u || !a->delta || !a->A || !a->B || !a->C || !a->carries || !a->dout) return MSS_ERR_INVALID_ARGUMENT;
   if (!a->du || !a->ddelta || !a->dA || !a->dB || !a->dC) return MSS_ERR_INVALID_ARGUMENT;
@@ -256,6 +285,10 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   p.ddelta = a->ddelta;
   p.dz = a->dz;
   p.dinit = a->dinitial_state;
+  p.a_ld = a->dstate;
+  p.state_ld = a->dstate;
+  p.carry_cs = static_cast<long long>(a->dstate) * p.n_seg;
+  p.acc_out = 0;
   p.part_dBC = reinterpret_cast<float*>(ws);
   p.part_stride = l.part_stride;
   p.part_dA = reinterpret_cast<float*>(ws + l.off_dA);
@@ -265,7 +298,12 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
 }
 
 int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream, bool cplx = false) {
-  const BwdLayout l = bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr, cplx);
+  const bool varlen = a->seq_lens != nullptr;
+  const bool grouped = !cplx && a->dstate > MSS_MAX_DSTATE;
+  // State groups hand the du/ddelta/ddelta_bias sums from one group to the next, so the two
+  // phases cannot be split across calls.
+  if (grouped && phases != kPhaseBoth) return MSS_ERR_UNSUPPORTED;
+  const BwdLayout l = bwd_layout_call(a->batch, a->dim, a->seqlen, a->dstate, varlen, cplx);
   char* ws = static_cast<char*>(a->workspace);
   bool owned = false;
   if (ws == nullptr) {
@@ -277,17 +315,50 @@ int run_bwd(const mss_bwd_args* a, int phases, hipStream_t stream, bool cplx = f
   } else if (a->workspace_bytes < l.total || !aligned16(ws)) {
     return MSS_ERR_WORKSPACE;
   }
-  const mss::BwdParams p = pack_bwd(a, l, ws);
   const int zoh = a->discretization == MSS_ZOH;
   const int io_bf16 = a->io_dtype == MSS_BF16;
   const int bc_bf16 = a->bc_dtype == MSS_BF16;
   hipError_t e = hipSuccess;
-  if (phases & kPhaseScan)
-    e = cplx ? mss::launch_cbwd_scan(p, zoh, io_bf16, bc_bf16, stream)
-             : mss::launch_bwd_scan(p, zoh, io_bf16, bc_bf16, stream);
-  if (e == hipSuccess && (phases & kPhaseReduce))
-    e = mss::launch_bwd_reduce(p, bc_bf16, a->dstate * (cplx ? 2 : 1), a->dA, a->dB, a->dC, a->dD,
-                               a->ddelta_bias, stream);
+  if (!grouped) {
+    const mss::BwdParams p = pack_bwd(a, l, ws);
+    if (phases & kPhaseScan)
+      e = cplx ? mss::launch_cbwd_scan(p, zoh, io_bf16, bc_bf16, stream)
+               : mss::launch_bwd_scan(p, zoh, io_bf16, bc_bf16, stream);
+    if (e == hipSuccess && (phases & kPhaseReduce)) {
+      const int na = a->dstate * (cplx ? 2 : 1);
+      e = mss::launch_bwd_reduce(p, bc_bf16, na, na, 0, a->dA, a->dB, a->dC, a->dD, a->ddelta_bias, stream);
+    }
+  } else {
+    // One backward per state group (float32 only), in order on the stream, each in the same
+    // workspace: group 0 writes du/ddelta (with the D term), dz, dD and ddelta_bias; later
+    // groups add their state sums to du/ddelta/ddelta_bias. A, the state buffers and the
+    // carries are read with the full dstate as row stride; dB/dC/dA rows of a group are its
+    // own.
+    const int N = a->dstate;
+    for (int g = 0; g < state_groups(N) && e == hipSuccess; ++g) {
+      const int n0 = group_begin(N, g), ng = group_begin(N, g + 1) - n0;
+      mss::BwdParams p = pack_bwd(a, bwd_layout(a->batch, a->dim, a->seqlen, ng, varlen), ws);
+      const size_t bc_off = static_cast<size_t>(n0) * p.bc_sn * sizeof(float);
+      p.dstate = ng;
+      p.A = a->A + n0;
+      p.B = static_cast<const char*>(a->B) + bc_off;
+      p.C = static_cast<const char*>(a->C) + bc_off;
+      p.x0 = a->initial_state ? a->initial_state + n0 : nullptr;
+      p.dlast = a->dlast_state ? a->dlast_state + n0 : nullptr;
+      p.dinit = a->dinitial_state ? a->dinitial_state + n0 : nullptr;
+      p.carries = a->carries + static_cast<size_t>(n0) * p.n_seg;
+      if (g > 0) {
+        p.D = nullptr;
+        p.dz = nullptr;
+        p.acc_out = 1;
+      }
+      e = mss::launch_bwd_scan(p, zoh, io_bf16, bc_bf16, stream);
+      if (e == hipSuccess)
+        e = mss::launch_bwd_reduce(p, bc_bf16, ng, N, g > 0, a->dA + n0, static_cast<char*>(a->dB) + bc_off,
+                                   static_cast<char*>(a->dC) + bc_off, g == 0 ? a->dD : nullptr,
+                                   a->ddelta_bias, stream);
+    }
+  }
   if (owned) {
     const hipError_t f = hipFreeAsync(ws, stream);
     if (e == hipSuccess) e = f;
@@ -398,15 +469,17 @@ const char* mss_strerror(int status) {
 const char* mss_last_hip_error(void) { return g_last_hip_error.c_str(); }
 
 size_t mss_bwd_workspace_bytes(const mss_bwd_args* a) {
-  if (a == nullptr || check_dims(a->batch, a->dim, a->seqlen, a->dstate) != MSS_OK) return 0;
-  return bwd_layout(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr).total;
+  if (a == nullptr ||
+      check_dims(a->batch, a->dim, a->seqlen, a->dstate, max_dstate_for(a->io_dtype, a->bc_dtype, false)) != MSS_OK)
+    return 0;
+  return bwd_layout_call(a->batch, a->dim, a->seqlen, a->dstate, a->seq_lens != nullptr).total;
 }
 
 int mss_bwd_plan(const mss_bwd_args* args, int32_t* waves, int32_t* chan_per_block) {
   if (waves == nullptr || chan_per_block == nullptr) return MSS_ERR_INVALID_ARGUMENT;
   const int s = validate_bwd(args);
   if (s != MSS_OK) return s;
-  const BwdLayout l = bwd_layout(args->batch, args->dim, args->seqlen, args->dstate, args->seq_lens != nullptr);
+  const BwdLayout l = bwd_layout_call(args->batch, args->dim, args->seqlen, args->dstate, args->seq_lens != nullptr);
   *waves = l.waves;
   *chan_per_block = l.chan_per_block;
   return MSS_OK;
@@ -427,7 +500,7 @@ int mss_bwd(const mss_bwd_args* args, void* stream) {
 int mss_bwd_noalloc(const mss_bwd_args* args, void* stream) {
   const int s = validate_bwd(args);
   if (s != MSS_OK) return s;
-  const BwdLayout l = bwd_layout(args->batch, args->dim, args->seqlen, args->dstate, args->seq_lens != nullptr);
+  const BwdLayout l = bwd_layout_call(args->batch, args->dim, args->seqlen, args->dstate, args->seq_lens != nullptr);
   if (l.total > kScratchBytes) return MSS_ERR_SCRATCH_LIMIT;
   void* ws = nullptr;
   const int t = scratch_of_current_device(&ws);
@@ -458,7 +531,7 @@ size_t mss_cbwd_workspace_bytes(const mss_bwd_args* a) {
 }
 
 int mss_cfwd(const mss_fwd_args* args, void* stream) {
-  const int s = validate_fwd(args);
+  const int s = validate_fwd(args, true);
   if (s != MSS_OK) return s;
   if (!aligned8(args->A) || !aligned8(args->initial_state) || !aligned8(args->last_state) ||
       !aligned8(args->carries))
@@ -467,7 +540,7 @@ int mss_cfwd(const mss_fwd_args* args, void* stream) {
 }
 
 int mss_cbwd(const mss_bwd_args* args, void* stream) {
-  const int s = validate_bwd(args);
+  const int s = validate_bwd(args, true);
   if (s != MSS_OK) return s;
   if (!aligned8(args->A) || !aligned8(args->carries)) return MSS_ERR_INVALID_ARGUMENT;
   return run_bwd(args, kPhaseBoth, static_cast<hipStream_t>(stream), true);
@@ -769,7 +842,7 @@ int mss_scan_fwd_repeat(void* stream, int32_t discretization, int32_t repeats, i
                         const float* deltas, const float* B, const float* C, const float* u,
                         const float* initial_x, float* y, float* final_x, float* chunk_states) {
   if (repeats <= 0) return MSS_ERR_INVALID_ARGUMENT;
-  int s = check_dims(batch, dim, length, dstate);
+  int s = check_dims(batch, dim, length, dstate, MSS_MAX_DSTATE_WIDE);
   if (s != MSS_OK) return s;
   if (discretization != MSS_EULER && discretization != MSS_ZOH) return MSS_ERR_INVALID_ARGUMENT;
   if (!A || !deltas || !B || !C || !u || !initial_x || !y || !final_x || !chunk_states)
@@ -812,8 +885,8 @@ static size_t scan_bwd_carry_bytes(int32_t batch, int32_t length, int32_t dim, i
 }
 
 size_t mss_scan_bwd_workspace_bytes(int32_t batch, int32_t length, int32_t dim, int32_t dstate) {
-  if (check_dims(batch, dim, length, dstate) != MSS_OK) return 0;
-  return scan_bwd_carry_bytes(batch, length, dim, dstate) + bwd_layout(batch, dim, length, dstate, false).total;
+  if (check_dims(batch, dim, length, dstate, MSS_MAX_DSTATE_WIDE) != MSS_OK) return 0;
+  return scan_bwd_carry_bytes(batch, length, dim, dstate) + bwd_layout_call(batch, dim, length, dstate, false).total;
 }
 
 int mss_scan_bwd_ws(void* stream, int32_t batch, int32_t length, int32_t dim, int32_t dstate,
@@ -821,7 +894,7 @@ int mss_scan_bwd_ws(void* stream, int32_t batch, int32_t length, int32_t dim, in
                     const float* u, const float* initial_x, const float* chunk_states,
                     const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
                     float* dC, float* du, float* dinitial_x, void* workspace, size_t workspace_bytes) {
-  int s = check_dims(batch, dim, length, dstate);
+  int s = check_dims(batch, dim, length, dstate, MSS_MAX_DSTATE_WIDE);
   if (s != MSS_OK) return s;
   if (!A || !deltas || !B || !C || !u || !initial_x || !chunk_states || !dout || !dfinal_x || !dA ||
       !ddeltas || !dB || !dC || !du || !dinitial_x)
@@ -889,7 +962,7 @@ int mss_scan_bwd(void* stream, int32_t batch, int32_t length, int32_t dim, int32
                  const float* u, const float* initial_x, const float* chunk_states,
                  const float* dout, const float* dfinal_x, float* dA, float* ddeltas, float* dB,
                  float* dC, float* du, float* dinitial_x) {
-  int s = check_dims(batch, dim, length, dstate);
+  int s = check_dims(batch, dim, length, dstate, MSS_MAX_DSTATE_WIDE);
   if (s != MSS_OK) return s;
   if (!A || !deltas || !B || !C || !u || !initial_x || !chunk_states || !dout || !dfinal_x || !dA ||
       !ddeltas || !dB || !dC || !du || !dinitial_x)

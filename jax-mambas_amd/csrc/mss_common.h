@@ -16,6 +16,9 @@ namespace mss {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxN = 16;
+// Float32 scans with more states: the forward keeps this many per wave; the backward runs
+// over groups of at most kMaxN states.
+constexpr int kMaxNWide = 256;
 // Step granularity of the `carries` residual: the state before every kSegSteps-step segment.
 constexpr int kSegSteps = 8;
 constexpr int kRefChunk = 2048;
@@ -407,6 +410,13 @@ struct BwdParams {
   void* ddelta;
   void* dz;
   float* dinit;
+  // A state group of a wider scan (dstate here is the group's size): row strides of the
+  // full tensors, in elements. a_ld: A rows; state_ld: x0/dlast/dinit rows (per (b, d));
+  // carry_cs: carries per (b, d). acc_out: du/ddelta add to what the buffers hold (the
+  // other groups' terms) instead of overwriting them.
+  int a_ld, state_ld;
+  long long carry_cs;
+  int acc_out;
   // workspace partials
   float* part_dBC;   // [n_blocks_d][part_stride]; block = [batch][2][dstate][L] (+ padding)
   size_t part_stride;  // floats per channel block, a multiple of 64

@@ -98,7 +98,9 @@ __device__ __forceinline__ void stage_round(const bc_t* __restrict__ Bb, const b
   }
 }
 
-template <int kT, int kW, int kNB, int kOcc, bool kZOH, typename io_t, typename bc_t>
+// kMaxS: the per-wave state tables' size (kMaxN, or kMaxNWide for float32 scans with more
+// states).
+template <int kT, int kW, int kNB, int kOcc, bool kZOH, typename io_t, typename bc_t, int kMaxS = kMaxN>
 __global__ __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(kOcc, kOcc)))
 void fwd_kernel(FwdParams p) {
   constexpr int kChunk = 64 * kT;
@@ -108,9 +110,9 @@ void fwd_kernel(FwdParams p) {
   // the compiler can tell the in-flight copy into one from the reads of the other.
   __shared__ uint4 stage0[kNB][2][kRowSlots];  // [state][B|C][slot]
   __shared__ uint4 stage1[kNB][2][kRowSlots];
-  __shared__ float s_run[kW][kMaxN];
-  __shared__ float s_a2[kW][kMaxN];
-  __shared__ float s_a[kW][kMaxN];
+  __shared__ float s_run[kW][kMaxS];
+  __shared__ float s_a2[kW][kMaxS];
+  __shared__ float s_a[kW][kMaxS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -131,11 +133,11 @@ void fwd_kernel(FwdParams p) {
   const bc_t* __restrict__ Bb = static_cast<const bc_t*>(p.B) + b * p.bc_sb;
   const bc_t* __restrict__ Cb = static_cast<const bc_t*>(p.C) + b * p.bc_sb;
 
-  if (lane < N) {
-    s_run[w][lane] = p.x0 ? p.x0[chan * N + lane] : 0.f;
-    const float an = p.A[static_cast<size_t>(d) * N + lane];
-    s_a[w][lane] = an;
-    s_a2[w][lane] = an * kLog2e;
+  for (int n = lane; n < N; n += 64) {
+    s_run[w][n] = p.x0 ? p.x0[chan * N + n] : 0.f;
+    const float an = p.A[static_cast<size_t>(d) * N + n];
+    s_a[w][n] = an;
+    s_a2[w][n] = an * kLog2e;
   }
   const float Dv = p.D ? p.D[d] : 0.f;
   const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
@@ -182,7 +184,8 @@ void fwd_kernel(FwdParams p) {
             rs[1] = s_run[w][n];
           }
         }
-        if (p.last && c == n_chunks - 1 && lane < N) p.last[chan * N + lane] = s_run[w][lane];
+        if (p.last && c == n_chunks - 1)
+          for (int n = lane; n < N; n += 64) p.last[chan * N + n] = s_run[w][n];
       }
       continue;
     }
@@ -300,15 +303,25 @@ void fwd_kernel(FwdParams p) {
   }
 }
 
-template <int kT, int kW, int kNB, int kOcc, bool kZOH, typename io_t, typename bc_t>
+template <int kT, int kW, int kNB, int kOcc, bool kZOH, typename io_t, typename bc_t, int kMaxS = kMaxN>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   dim3 grid((p.dim + kW - 1) / kW, p.batch);
-  hipLaunchKernelGGL((fwd_kernel<kT, kW, kNB, kOcc, kZOH, io_t, bc_t>), grid, dim3(kW * 64), 0, stream, p);
+  hipLaunchKernelGGL((fwd_kernel<kT, kW, kNB, kOcc, kZOH, io_t, bc_t, kMaxS>), grid, dim3(kW * 64), 0, stream, p);
   return hipGetLastError();
 }
 
 template <bool kZOH, typename io_t, typename bc_t>
 static hipError_t launch_fwd_z(const FwdParams& p, hipStream_t stream) {
+  if (p.dstate > kMaxN) {
+    // Wider state (float32 only): 24 KB of state tables per workgroup, two workgroups of
+    // the narrow shape per CU (4 waves per SIMD).
+    if constexpr (sizeof(io_t) == 4 && sizeof(bc_t) == 4) {
+      if (p.dstate > kMaxNWide) return hipErrorInvalidValue;
+      return launch_fwd_t<MSS_FWD_T_NARROW, MSS_FWD_W, MSS_FWD_NB, 4, kZOH, io_t, bc_t, kMaxNWide>(p, stream);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   // Resident workgroups of the narrow shape: 256 CUs * kOcc waves per SIMD * 4 SIMDs / kW.
   constexpr long long kNarrowSlots = 256LL * MSS_FWD_OCC_NARROW * 4 / MSS_FWD_W;
   const long long groups = static_cast<long long>(p.batch) * ((p.dim + MSS_FWD_W - 1) / MSS_FWD_W);
@@ -342,12 +355,13 @@ hipError_t launch_fwd(const FwdParams& p, int zoh, int io_bf16, int bc_bf16, hip
 // 64-lane affine scan, the lane's carry-in stored; no C, no output.
 constexpr int kRebuildW = 8;
 
+template <int kMaxS>
 __global__ __launch_bounds__(kRebuildW * 64) void carry_rebuild_kernel(FwdParams p) {
   constexpr int kT = kSegSteps;
   constexpr int kChunk = 64 * kT;
   constexpr int kChunksPerBlock = kRefChunk / kChunk;
-  __shared__ float s_run[kRebuildW][kMaxN];
-  __shared__ float s_a2[kRebuildW][kMaxN];
+  __shared__ float s_run[kRebuildW][kMaxS];
+  __shared__ float s_a2[kRebuildW][kMaxS];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.y;
@@ -357,11 +371,11 @@ __global__ __launch_bounds__(kRebuildW * 64) void carry_rebuild_kernel(FwdParams
   const int L = p.seqlen;
   const int N = p.dstate;
   const size_t chan = static_cast<size_t>(b) * p.dim + d;
-  if (lane < N) {
+  for (int n = lane; n < N; n += 64) {
     // state entering the block: the initial state, or h at the previous block's end
-    s_run[w][lane] = blk == 0 ? (p.x0 ? p.x0[chan * N + lane] : 0.f)
-                              : p.ref_states[((chan * p.n_ref + blk - 1) * N + lane) * 2 + 1];
-    s_a2[w][lane] = p.A[static_cast<size_t>(d) * N + lane] * kLog2e;
+    s_run[w][n] = blk == 0 ? (p.x0 ? p.x0[chan * N + n] : 0.f)
+                           : p.ref_states[((chan * p.n_ref + blk - 1) * N + n) * 2 + 1];
+    s_a2[w][n] = p.A[static_cast<size_t>(d) * N + n] * kLog2e;
   }
   const float* __restrict__ u_row = static_cast<const float*>(p.u) + chan * L;
   const float* __restrict__ dl_row = static_cast<const float*>(p.delta) + chan * L;
@@ -401,7 +415,11 @@ __global__ __launch_bounds__(kRebuildW * 64) void carry_rebuild_kernel(FwdParams
 
 hipError_t launch_carry_rebuild(const FwdParams& p, hipStream_t stream) {
   const dim3 grid((p.dim + kRebuildW - 1) / kRebuildW, p.batch, p.n_ref);
-  hipLaunchKernelGGL(carry_rebuild_kernel, grid, dim3(kRebuildW * 64), 0, stream, p);
+  if (p.dstate > kMaxNWide) return hipErrorInvalidValue;
+  if (p.dstate > kMaxN)
+    hipLaunchKernelGGL(carry_rebuild_kernel<kMaxNWide>, grid, dim3(kRebuildW * 64), 0, stream, p);
+  else
+    hipLaunchKernelGGL(carry_rebuild_kernel<kMaxN>, grid, dim3(kRebuildW * 64), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 7
+MSS_ABI_VERSION = 8
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -26,6 +26,7 @@ MSS_BF16 = 1
 MSS_EULER = 0
 MSS_ZOH = 1
 MSS_MAX_DSTATE = 16
+MSS_MAX_DSTATE_WIDE = 256  # float32 real-A scans (backward over groups of MSS_MAX_DSTATE states)
 MSS_SEG_STEPS = 8
 MSS_REF_CHUNK = 2048
 

@@ -72,15 +72,20 @@ def _check_f32(name, t, shape):
         raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
 
 
-def _validate_fused(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, discretization):
+def _validate_fused(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, discretization,
+                    cplx=False):
     if u.ndim != 3 or A.ndim != 2:
         raise ValueError("u must have shape (B, D, L) and A shape (D, N)")
     batch, dim, length = u.shape
     n = A.shape[1]
     if length == 0:
         raise ValueError("The sequence length must be positive")
-    if not 1 <= n <= _lib.MSS_MAX_DSTATE:
-        raise ValueError(f"N must be between 1 and {_lib.MSS_MAX_DSTATE}")
+    # float32 real-A scans take up to 256 states (the backward runs over groups of 16)
+    wide = not cplx and u.dtype == torch.float32 and B.dtype == torch.float32
+    n_max = _lib.MSS_MAX_DSTATE_WIDE if wide else _lib.MSS_MAX_DSTATE
+    if not 1 <= n <= n_max:
+        kind = "float32 real-A" if wide else "bf16 or complex-A"
+        raise ValueError(f"N must be between 1 and {n_max} for {kind} scans")
     if discretization not in ("euler", "zoh"):
         raise ValueError("discretization must be 'euler' or 'zoh'")
     _io_tag(u.dtype, "u")
@@ -334,7 +339,7 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
         _validate_complex(A, initial_state)
         _validate_fused(u, delta, torch.view_as_real(A)[..., 0], B, C, D, z, delta_bias,
                         None if initial_state is None else torch.view_as_real(initial_state)[..., 0],
-                        seq_lens, discretization)
+                        seq_lens, discretization, cplx=True)
     else:
         _validate_fused(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, discretization)
     if not torch.compiler.is_compiling():

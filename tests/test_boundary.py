@@ -46,7 +46,7 @@ def test_library_exports_every_header_symbol(lib):
     header = (ROOT / "include" / "mamba_selective_scan.h").read_text()
     version = int(re.search(r"#define MSS_ABI_VERSION (\d+)", header).group(1))
     assert lib.mss_abi_version() == version == _lib.MSS_ABI_VERSION
-    for name in ("MSS_MAX_DSTATE", "MSS_SEG_STEPS", "MSS_REF_CHUNK"):
+    for name in ("MSS_MAX_DSTATE", "MSS_MAX_DSTATE_WIDE", "MSS_SEG_STEPS", "MSS_REF_CHUNK"):
         value = int(re.search(rf"#define {name} (\d+)", header).group(1))
         assert getattr(_lib, name) == value, name
 
@@ -73,7 +73,8 @@ def fwd_args(**kw):
     (dict(seqlen=0), _lib.MSS_ERR_INVALID_ARGUMENT),
     (dict(dstate=0), _lib.MSS_ERR_INVALID_ARGUMENT),
     (dict(dstate=257), _lib.MSS_ERR_INVALID_ARGUMENT),
-    (dict(dstate=17), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(dstate=17, io_dtype=_lib.MSS_BF16), _lib.MSS_ERR_UNSUPPORTED),   # wider states: float32 only
+    (dict(dstate=17, bc_dtype=_lib.MSS_BF16), _lib.MSS_ERR_UNSUPPORTED),
     (dict(discretization=2), _lib.MSS_ERR_INVALID_ARGUMENT),
     (dict(delta_softplus=3), _lib.MSS_ERR_INVALID_ARGUMENT),
     (dict(io_dtype=7), _lib.MSS_ERR_INVALID_ARGUMENT),
@@ -238,9 +239,27 @@ def test_backward_plan_of_the_configs(lib):
     assert _lib.bwd_plan(8, 1536, 16, 2048, io_bf16=True, strides=c5)[0] == 16
     w = ctypes.c_int32()
     assert lib.mss_bwd_plan(None, ctypes.byref(w), ctypes.byref(w)) == _lib.MSS_ERR_INVALID_ARGUMENT
-    bad = bwd_args(dstate=32)
+    bad = bwd_args(dstate=32, io_dtype=_lib.MSS_BF16)
     assert lib.mss_bwd_plan(bad, ctypes.byref(w), ctypes.byref(w)) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_bwd_plan(bwd_args(dstate=257), ctypes.byref(w), ctypes.byref(w)) == _lib.MSS_ERR_INVALID_ARGUMENT
     assert lib.mss_bwd_plan(bwd_args(), None, ctypes.byref(w)) == _lib.MSS_ERR_INVALID_ARGUMENT
+
+
+def test_wide_state_backward_groups(lib):
+    """Float32 scans with more than 16 states: the backward runs over balanced groups of at
+    most 16 states in one workspace, sized for the larger group; the split phases, which
+    cannot carry the groups' sums from one call to the next, refuse them before any HIP call."""
+    for n, groups in ((17, (9, 8)), (32, (16, 16)), (40, (14, 13)), (256, (16,))):
+        got = lib.mss_bwd_workspace_bytes(bwd_args(batch=4, dim=1536, seqlen=2048, dstate=n))
+        want = max(lib.mss_bwd_workspace_bytes(bwd_args(batch=4, dim=1536, seqlen=2048, dstate=g)) for g in groups)
+        assert got == want > 0, n
+        waves, cpb = ctypes.c_int32(), ctypes.c_int32()
+        assert lib.mss_bwd_plan(bwd_args(dstate=n), ctypes.byref(waves), ctypes.byref(cpb)) == _lib.MSS_OK
+        assert waves.value in (12, 16) and cpb.value % waves.value == 0
+        assert lib.mss_bwd_scan(bwd_args(dstate=n), None) == _lib.MSS_ERR_UNSUPPORTED
+        assert lib.mss_bwd_reduce(bwd_args(dstate=n), None) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_bwd_workspace_bytes(bwd_args(dstate=17, io_dtype=_lib.MSS_BF16)) == 0
+    assert lib.mss_bwd_workspace_bytes(bwd_args(dstate=257)) == 0
 
 
 def test_reference_entry_points_validate(lib):
@@ -249,7 +268,7 @@ def test_reference_entry_points_validate(lib):
     assert lib.mss_scan_fwd(None, 2, 1, 10, 3, 4, *[p] * 9) == _lib.MSS_ERR_INVALID_ARGUMENT
     assert lib.mss_scan_fwd(None, 0, 1, 10, 3, 4, *[p] * 8, None) == _lib.MSS_ERR_INVALID_ARGUMENT
     assert lib.mss_scan_fwd_repeat(None, 0, 0, 1, 10, 3, 4, *[p] * 9) == _lib.MSS_ERR_INVALID_ARGUMENT
-    assert lib.mss_scan_bwd(None, 1, 10, 3, 32, *[p] * 15) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_scan_bwd(None, 1, 10, 3, 257, *[p] * 15) == _lib.MSS_ERR_INVALID_ARGUMENT
     assert lib.mss_scan_bwd(None, 1, 10, 3, 4, *[p] * 14, None) == _lib.MSS_ERR_INVALID_ARGUMENT
 
 
@@ -260,13 +279,15 @@ def test_reference_backward_workspace(lib):
     carries = b * d * n * (l // 8) * 4
     fused = lib.mss_bwd_workspace_bytes(bwd_args(batch=b, dim=d, seqlen=l, dstate=n))
     assert lib.mss_scan_bwd_workspace_bytes(b, l, d, n) == carries + fused
-    assert lib.mss_scan_bwd_workspace_bytes(b, l, d, 32) == 0
+    assert lib.mss_scan_bwd_workspace_bytes(b, l, d, 257) == 0
+    wide = b * d * 40 * (l // 8) * 4 + lib.mss_bwd_workspace_bytes(bwd_args(batch=b, dim=d, seqlen=l, dstate=40))
+    assert lib.mss_scan_bwd_workspace_bytes(b, l, d, 40) == wide
     p = ctypes.c_void_p(256)
     args = [None, 1, 64, 3, 4] + [p] * 15
     assert lib.mss_scan_bwd_ws(*args, None, 1 << 30) == _lib.MSS_ERR_WORKSPACE
     assert lib.mss_scan_bwd_ws(*args, p, 16) == _lib.MSS_ERR_WORKSPACE
     assert lib.mss_scan_bwd_ws(*args, ctypes.c_void_p(8), 1 << 30) == _lib.MSS_ERR_WORKSPACE
-    assert lib.mss_scan_bwd_ws(None, 1, 64, 3, 32, *[p] * 15, p, 1 << 30) == _lib.MSS_ERR_UNSUPPORTED
+    assert lib.mss_scan_bwd_ws(None, 1, 64, 3, 257, *[p] * 15, p, 1 << 30) == _lib.MSS_ERR_INVALID_ARGUMENT
     assert lib.mss_scan_bwd_ws(None, 1, 64, 3, 4, *[p] * 14, None, p, 1 << 30) == _lib.MSS_ERR_INVALID_ARGUMENT
     # more 2048-step blocks than the carry rebuild's grid holds
     assert lib.mss_scan_bwd_ws(None, 1, 65535 * 2048 + 1, 3, 4, *[p] * 15, p, 1 << 62) == _lib.MSS_ERR_UNSUPPORTED
@@ -324,8 +345,15 @@ def test_fused_api_validation():
     Bm = torch.randn(1, 4, 8)
     with pytest.raises(TypeError):
         selective_scan_fn(u, u.double(), A, Bm, Bm)
-    with pytest.raises(ValueError, match="N must be"):
-        selective_scan_fn(u, u, -torch.ones(2, 17), torch.randn(1, 17, 8), torch.randn(1, 17, 8))
+    with pytest.raises(ValueError, match="N must be between 1 and 256"):
+        selective_scan_fn(u, u, -torch.ones(2, 257), torch.randn(1, 257, 8), torch.randn(1, 257, 8))
+    ub = u.bfloat16()
+    with pytest.raises(ValueError, match="N must be between 1 and 16"):
+        selective_scan_fn(ub, ub, -torch.ones(2, 17), torch.randn(1, 17, 8).bfloat16(),
+                          torch.randn(1, 17, 8).bfloat16())
+    with pytest.raises(ValueError, match="N must be between 1 and 16"):
+        selective_scan_fn(u, u, -torch.ones(2, 17, dtype=torch.complex64), torch.randn(1, 17, 8),
+                          torch.randn(1, 17, 8))
     with pytest.raises(ValueError, match="discretization"):
         selective_scan_fn(u, u, A, Bm, Bm, discretization="rk4")
     with pytest.raises(TypeError, match="float32"):

@@ -359,6 +359,21 @@ def test_bf16_store_rounding_bit_exact(length):
     assert not bad.any()
 
 
+@pytest.mark.parametrize("n,zoh,lens", [(17, False, None), (32, True, None), (40, False, [700, 333]),
+                                        (64, False, None), (256, True, None)])
+def test_wide_state_fp32(n, zoh, lens):
+    """Float32 scans with more than 16 states (the reference C handler's N <= 256): the
+    forward keeps every state of a wave in LDS; the backward runs over balanced groups of at
+    most 16 states (the first writes dz, dD and the D term, the others add their state sums to
+    du, ddelta and ddelta_bias). Every output and gradient against the oracle, with all fused
+    extras and a ragged varlen case."""
+    log(f"case wide state N={n} zoh={zoh} lens={lens}")
+    x, dout, dlast = fused_case(900 + n, 2, 24, 700, n, lens=lens)
+    ts, out, last = run_fused(x, dout, dlast, "f32", zoh)
+    fw, g = oracle_fused(x, dout, dlast, zoh)
+    check_fused(ts, out, last, fw, g)
+
+
 def test_deterministic_rerun():
     log("case determinism")
     x, dout, dlast = fused_case(600, 2, 64, 1500, 16)
@@ -411,18 +426,17 @@ def test_strided_row_layouts(dtype, l):
     check_fused(ts_c, out_c, last_c, fw, g, *tol)
 
 
-@pytest.mark.parametrize("length", [2500, 5000])
-def test_reference_c_entry_points(length):
+@pytest.mark.parametrize("length,n", [(2500, 16), (5000, 16), (2500, 32)])
+def test_reference_c_entry_points(length, n):
     """mss_scan_fwd / mss_scan_bwd / mss_scan_bwd_ws (the reference FFI handlers'
     counterparts) via ctypes, over two and three 2048-step blocks: the backward re-runs each
     block from the forward's chunk_states. The workspace variant equals mss_scan_bwd bit for
     bit; chunk_states from the float64 oracle give the same gradients to the float32 bar, and
     a corrupted block state changes them (the residual is what the backward starts from)."""
-    log(f"case reference C entry points L={length}")
+    log(f"case reference C entry points L={length} N={n}")
     lib = _lib.register_hip_kernel()
-    A, deltas, Bs, Cs, u, x0 = ref_recipe(13, batch=2, length=length, dim=8, n=16)
+    A, deltas, Bs, Cs, u, x0 = ref_recipe(13, batch=2, length=length, dim=8, n=n)
     b, l, d = u.shape
-    n = A.shape[1]
     tr = lambda a: T(np.swapaxes(a, 1, 2))  # physical [B][D][L] / [B][N][L]
     tA, td, tB, tC, tu, tx0 = T(A), tr(deltas), tr(Bs), tr(Cs), tr(u), T(x0)
     y = torch.empty(b, d, l, device=dev)
