@@ -74,8 +74,10 @@ def _backward(lib, fn, x, carries, y_pre, dout, dlast, b, d, l, n, workspace=Non
 
 def test_noalloc_backward_matches_workspace_backward():
     lib = _lib.register_hip_kernel()
-    # the second call is smaller: fewer rows, channels and steps, and ragged lengths
-    for seed, (b, d, l, n), lens in ((1, (4, 1536, 2048, 16), None), (2, (2, 40, 700, 8), [700, 333])):
+    # the second call is smaller: fewer rows, channels and steps, and ragged lengths; the third
+    # has 32 states (a float32 backward over two groups of 16 in the same scratch)
+    for seed, (b, d, l, n), lens in ((1, (4, 1536, 2048, 16), None), (2, (2, 40, 700, 8), [700, 333]),
+                                     (3, (2, 48, 600, 32), [600, 257])):
         log(f"case noalloc b={b} d={d} l={l} n={n} lens={lens}")
         x, dout, dlast = _inputs(seed, b, d, l, n, lens)
         carries, y_pre = _forward(lib, x, b, d, l, n)
