@@ -173,6 +173,8 @@ int mss_bwd_noalloc(const mss_bwd_args* args, void* stream);
  * MSS_ERR_WORKSPACE): mss_bwd_scan writes du/ddelta/dz/dinitial_state and per-block
  * partial sums of dA/dB/dC/dD/ddelta_bias into the workspace; mss_bwd_reduce sums the
  * partials in a fixed order into dA/dB/dC/dD/ddelta_bias. mss_bwd == scan then reduce.
+ * Both phases take the same arguments (the reduction reads seq_lens: no partials are written
+ * for 512-step chunks past a row's length, whose dB/dC steps it sets to zero).
  * (The reference backward, native/selective_scan_bwd.cu:166-190, is one call; the split
  * lets a caller time or defer the cross-channel reduction.) */
 int mss_bwd_scan(const mss_bwd_args* args, void* stream);

@@ -29,6 +29,7 @@ namespace mss {
 
 constexpr int kBwdT = kSegSteps;  // steps per lane: the granularity of the forward's carries
 constexpr int kBwdChunk = 64 * kBwdT;
+static_assert(kBwdChunk == kPartChunk, "the reduction's chunk is the scan's");
 constexpr int kMaxChanPerBlock = 96;  // channels one workgroup walks, at most
 constexpr int kCUs = 256;             // MI355X compute units
 
@@ -234,14 +235,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         if (c == 0 && p.dinit && lane < N)
           p.dinit[(static_cast<size_t>(b) * p.dim + d) * st_ld + lane] = s_mu[cl][lane];
       }
-      // ... and this block's dB/dC partials of the chunk are zero.
-      const size_t nl = static_cast<size_t>(N) * L;
-      float* part = p.part_dBC + static_cast<size_t>(blk) * p.part_stride + static_cast<size_t>(b) * 2 * nl;
-      const int width = min(kChunk, L - t0);
-      for (int e = tid; e < 2 * N * width; e += kW * 64) {
-        const int rowi = e / width;
-        part[static_cast<size_t>(rowi) * L + t0 + (e - rowi * width)] = 0.f;
-      }
+      // No dB/dC partials: the reduction takes this chunk's steps as zero.
       continue;
     }
 
@@ -504,7 +498,9 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
 //   blocks [0, n_bc_blocks): dB/dC[b][n][t] = sum over channel blocks of the partials
 //     ([block][b][B|C][n][t], block stride `stride` floats). The block's row is
 //     blockIdx / x_blocks = (b, which, n); threads walk the row's steps, 4 at a time (16-byte
-//     loads) when kVec (L a multiple of 4), keeping 4 blocks' loads in flight;
+//     loads) when kVec (L a multiple of 4), keeping 4 blocks' loads in flight. With
+//     seq_lens, steps from live_part_end(len, L) on are zero (the scans write no partials
+//     there);
 //   the remaining blocks: dA[d][n] = sum_b part_dA[b][d][n] (dA rows a_ld apart); dD[d],
 //     dbias[d] likewise (dbias added to its current value when acc_bias: a state group of a
 //     wider scan).
@@ -517,7 +513,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
                                                      const float* __restrict__ part_dD,
                                                      const float* __restrict__ part_db, int batch,
                                                      int dim, int na, int a_ld, int acc_bias,
-                                                     float* dA, float* dD, float* dbias) {
+                                                     float* dA, float* dD, float* dbias,
+                                                     const int* __restrict__ seq_lens) {
   if (static_cast<int>(blockIdx.x) >= n_bc_blocks) {
     const int dn = dim * na;  // dA row width: dstate (real A) or 2 * dstate (complex A)
     const int i = (blockIdx.x - n_bc_blocks) * blockDim.x + threadIdx.x;
@@ -548,7 +545,14 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ p
   bc_t* dst = (which ? dC : dB) + bb * sb + n * sn;
   constexpr int kE = kVec ? 4 : 1;
   const int nvec = (L + kE - 1) / kE;
+  // Elements (of kE steps) holding partials; live_part_end is a multiple of 4 or L.
+  const int nlive = seq_lens ? (live_part_end(min(max(seq_lens[bb], 0), L), L) + kE - 1) / kE : nvec;
   for (int v = xb * blockDim.x + threadIdx.x; v < nvec; v += x_blocks * blockDim.x) {
+    if (v >= nlive) {
+#pragma unroll
+      for (int e = 0; e < kE; ++e) store_as(dst + kE * v + e, 0.f);
+      continue;
+    }
     if constexpr (kVec) {
       const f32x4* src = reinterpret_cast<const f32x4*>(src_row) + v;
       const size_t svec = stride / 4;
@@ -666,7 +670,8 @@ hipError_t launch_bwd_reduce(const BwdParams& p, int bc_bf16, int a_width, int a
   hipLaunchKernelGGL((reduce_kernel<VEC, T>), grid, dim3(256), 0, stream, p.part_dBC, p.n_blocks_d, \
                      p.part_stride, L, p.dstate, x_blocks, n_bc_blocks, p.bc_sb, p.bc_sn,          \
                      static_cast<T*>(dB), static_cast<T*>(dC), p.part_dA, p.part_dD, p.part_dbias,  \
-                     p.batch, p.dim, a_width, a_ld, acc_bias, static_cast<float*>(dA), dD, dbias)
+                     p.batch, p.dim, a_width, a_ld, acc_bias, static_cast<float*>(dA), dD, dbias, \
+                     p.seq_lens)
   if (bc_bf16) {
     if (vec) MSS_REDUCE(true, bf16_t); else MSS_REDUCE(false, bf16_t);
   } else {

@@ -21,6 +21,14 @@ constexpr int kMaxN = 16;
 constexpr int kMaxNWide = 256;
 // Step granularity of the `carries` residual: the state before every kSegSteps-step segment.
 constexpr int kSegSteps = 8;
+// Steps per chunk of the backward scans (a wave pass: 64 lanes of kSegSteps steps). Of a row
+// with a length, the scans write dB/dC partial sums only for chunks holding a valid step; the
+// reduction takes the steps of later chunks as zero.
+constexpr int kPartChunk = 64 * kSegSteps;
+__host__ __device__ constexpr int live_part_end(int len, int L) {
+  const int e = (len + kPartChunk - 1) / kPartChunk * kPartChunk;
+  return e < L ? e : L;
+}
 constexpr int kRefChunk = 2048;
 
 struct bf16_t {

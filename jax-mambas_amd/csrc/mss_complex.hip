@@ -22,6 +22,7 @@ namespace mss {
 
 constexpr int kCT = kSegSteps;     // steps per lane: one carry segment
 constexpr int kCChunk = 64 * kCT;  // steps per wave pass
+static_assert(kCChunk == kPartChunk, "the reduction's chunk is the scan's");
 constexpr int kCFwdW = 4;          // waves (channels) per forward workgroup
 constexpr int kCBwdW = 12;         // waves per backward workgroup (3 per SIMD, one per CU)
 constexpr int kCMaxChan = 48;      // channels one backward workgroup walks, at most
@@ -563,9 +564,10 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
       }
     }
     // This chunk's dB/dC partial rows (copies summed in order), then clear the rows. The
-    // last state iteration's barrier ordered every accumulation before these reads.
+    // last state iteration's barrier ordered every accumulation before these reads. None
+    // past the row's length: the reduction takes those steps as zero (the rows stay zero).
     float* part = p.part_dBC + static_cast<size_t>(blockIdx.x) * p.part_stride;
-    for (int i = tid; i < 2 * N * kCChunk; i += W * 64) {
+    for (int i = tid; live && i < 2 * N * kCChunk; i += W * 64) {
       const int which = i / (N * kCChunk);
       const int rem = i - which * N * kCChunk;
       const int n = rem / kCChunk;
