@@ -21,6 +21,8 @@
  *                                           state h entering every 8-step segment
  *                                           (segment 0: initial_state)
  *   y_pre                                 : [batch][dim][seqlen] y before the z gate
+ *   (carries and y_pre are residuals for the backward: with seq_lens, their values in
+ *   512-step chunks past a row's length are unspecified; the backward does not read them)
  *
  * All entry points are asynchronous on the given stream (a hipStream_t passed as
  * void*; NULL = the default stream), re-entrant, and validate every argument before

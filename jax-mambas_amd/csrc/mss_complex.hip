@@ -144,11 +144,11 @@ __global__ __launch_bounds__(kCFwdW * 64) void cfwd_kernel(FwdParams p) {
     const bool fast_bc = p.vec_bc && t0 + kCChunk <= L;
     float y[kCT];
     if (c >= n_live) {
-      // The whole chunk is past this row's length: the state is frozen, the output zero.
+      // The whole chunk is past this row's length: the state is frozen, the output zero
+      // (the backward reads no residual here, so y_pre is left unwritten).
 #pragma unroll
       for (int j = 0; j < kCT; ++j) y[j] = 0.f;
       store_seg<kCT>(out_row, tl, L, fast, y);
-      if (p.z && p.y_pre) store_seg<kCT>(static_cast<io_t*>(p.y_pre) + row, tl, L, fast, y);
       continue;
     }
     float dlt[kCT], uu[kCT];

@@ -170,13 +170,13 @@ void fwd_kernel(FwdParams p) {
                             : -1;
 
     if (c >= n_active_chunks) {
-      // Entire chunk is past this row's length: state frozen, output zero.
+      // Entire chunk is past this row's length: state frozen, output zero. The backward's
+      // residuals (carries, y_pre) are not written here: it never reads them.
       if (active) {
         float zero[kT];
 #pragma unroll
         for (int j = 0; j < kT; ++j) zero[j] = 0.f;
         if (p.out) store_seg<kT>(out_row, tl, L, fast, zero);
-        if (p.out && p.z && p.y_pre) store_seg<kT>(static_cast<io_t*>(p.y_pre) + row, tl, L, fast, zero);
         if (p.ref_states && lane == 63 && ref_idx >= 0) {
           for (int n = 0; n < N; ++n) {
             float* rs = p.ref_states + ((chan * p.n_ref + ref_idx) * N + n) * 2;
