@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   const int lane = tid & 63;
   const int seg = 63 - lane;  // this lane's segment within a chunk (reversed time order)
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int b = blockIdx.y;
+  const int b = row_longest_first(p.seq_lens, p.batch, p.seqlen, blockIdx.y);
   const int blk = blockIdx.x;
   const int L = p.seqlen;
   const int N = p.dstate;

@@ -114,6 +114,28 @@ __device__ __forceinline__ float wave_sum(float v) {
   return readlane(v, 63);
 }
 
+// Batch row of the workgroups whose grid y index is `rank`, for scans with variable
+// lengths: the rows in order of decreasing length (equal lengths by index). The dispatcher
+// hands out workgroups in grid order, so the longest rows start first and the shortest
+// ones form the tail. Without lengths, or with more than 64 rows, rows keep their order.
+// Each wave computes it alone (no barrier); the result is uniform.
+constexpr int kMaxSortedRows = 64;
+__device__ __forceinline__ int row_longest_first(const int* __restrict__ seq_lens, int batch, int L,
+                                                 int rank) {
+  if (seq_lens == nullptr || batch > kMaxSortedRows) return rank;
+  const int lane = threadIdx.x & 63;
+  const int mine = lane < batch ? min(max(seq_lens[lane], 0), L) : -1;
+  int r = 0;  // rows ordered before this lane's row
+  for (int j = 0; j < batch; ++j) {
+    const int o = __builtin_amdgcn_readlane(mine, j);
+    r += (o > mine) || (o == mine && j < lane);
+  }
+  // The ranks of the rows are a permutation of [0, batch): one lane matches any rank the grid
+  // holds (the fallback only guards a rank outside it).
+  const unsigned long long hit = __ballot(lane < batch && r == rank);
+  return hit ? __builtin_amdgcn_readfirstlane(__ffsll(static_cast<long long>(hit)) - 1) : rank;
+}
+
 // ---------------------------------------------------------------------------------
 // Scalar math.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

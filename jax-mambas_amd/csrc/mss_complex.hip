@@ -114,7 +114,7 @@ template <bool kZOH, typename io_t, typename bc_t>
 __global__ __launch_bounds__(kCFwdW * 64) void cfwd_kernel(FwdParams p) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int b = blockIdx.y;
+  const int b = row_longest_first(p.seq_lens, p.batch, p.seqlen, blockIdx.y);
   const int d = blockIdx.x * kCFwdW + w;
   if (d >= p.dim) return;  // wave-uniform; the kernel has no block-level barrier
   const int L = p.seqlen;
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int b = blockIdx.y;
+  const int b = row_longest_first(p.seq_lens, p.batch, p.seqlen, blockIdx.y);
   const int L = p.seqlen;
   const int N = p.dstate;
   const int len = p.seq_lens ? min(max(p.seq_lens[b], 0), L) : L;

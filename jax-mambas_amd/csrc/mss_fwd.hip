@@ -117,7 +117,7 @@ void fwd_kernel(FwdParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int b = blockIdx.y;
+  const int b = row_longest_first(p.seq_lens, p.batch, p.seqlen, blockIdx.y);
   const int d_raw = blockIdx.x * kW + w;
   const bool active = d_raw < p.dim;
   const int d = active ? d_raw : p.dim - 1;
