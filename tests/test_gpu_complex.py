@@ -168,6 +168,22 @@ def test_complex_varlen(zoh):
     check(x, dout, dlast, zoh)
 
 
+def test_complex_varlen_row_permutation():
+    """Rows go to workgroups longest first: permuted rows give the permuted outputs and
+    per-row gradients bit for bit."""
+    log("case complex varlen row permutation")
+    perm = [2, 0, 3, 1]
+    x, dout, dlast = complex_case(405, 4, 6, 1100, 8, lens=[530, 1100, 0, 530])
+    per_row = ("u", "delta", "z", "B", "C", "initial_state", "seq_lens")
+    xp = {k: (v[perm] if k in per_row else v) for k, v in x.items()}
+    a = run_complex(x, dout, dlast, "f32", False)
+    b = run_complex(xp, dout[perm], dlast[perm], "f32", False)
+    idx = torch.as_tensor(perm, device=dev)
+    assert torch.equal(a[1][idx], b[1]) and torch.equal(a[2][idx], b[2])
+    for k in per_row[:-1]:
+        assert torch.equal(a[0][k].grad[idx], b[0][k].grad), k
+
+
 def test_complex_no_extras():
     log("case complex no extras")
     x, dout, dlast = complex_case(410, 2, 4, 700, 16, extras=False)

@@ -250,6 +250,30 @@ def test_varlen_dead_chunks(lens):
     check_fused(ts, out, last, fw, g)
 
 
+PER_ROW = ("u", "delta", "z", "B", "C", "initial_state", "seq_lens")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_varlen_row_permutation(dtype):
+    """With lengths the kernels hand rows to workgroups longest first (ties by index). Rows
+    permuted give the permuted outputs and per-row gradients bit for bit; the sums over
+    rows (dA, dD, ddelta_bias) change only by summation order."""
+    log(f"case varlen row permutation {dtype}")
+    lens = [2080, 300, 2080, 0, 1500, 700]
+    perm = [4, 2, 5, 0, 3, 1]
+    x, dout, dlast = fused_case(1300, 6, 40, 2080, 16, dtype, lens=lens)
+    xp = {k: (v[perm] if k in PER_ROW else v) for k, v in x.items()}
+    a = run_fused(x, dout, dlast, dtype, False)
+    b = run_fused(xp, dout[perm], dlast[perm], dtype, False)
+    idx = torch.as_tensor(perm, device=dev)
+    assert torch.equal(a[1][idx], b[1]) and torch.equal(a[2][idx], b[2])
+    for k in PER_ROW[:-1]:
+        assert torch.equal(a[0][k].grad[idx], b[0][k].grad), k
+    for k in ("A", "D", "delta_bias"):
+        ga, gb = a[0][k].grad, b[0][k].grad
+        assert torch.allclose(ga, gb, rtol=1e-5, atol=1e-6 * float(ga.abs().max())), k
+
+
 def test_no_extras_three_chunks_and_determinism():
     """Without D, z, delta bias, softplus or initial state (raw positive delta) over three
     whole chunks, and bit-identical reruns."""
