@@ -394,11 +394,15 @@ __global__ __launch_bounds__(kRebuildW * 64) void carry_rebuild_kernel(FwdParams
       ssum += dlt[j];
     }
     const int seg_idx = tl / kT;
+    const bool fast_b = fast && p.vec_bc;
+    // B rows one state ahead: the next state's load is in flight while this one computes.
+    float bv[kT];
+    load_seg<kT>(Bb, tl, L, fast_b, bv);
     for (int n = 0; n < N; ++n) {
       const float a2 = s_a2[w][n];
       const float run = s_run[w][n];
-      float bv[kT];
-      load_seg<kT>(Bb + static_cast<size_t>(n) * L, tl, L, fast && p.vec_bc, bv);
+      float bn[kT];
+      if (n + 1 < N) load_seg<kT>(Bb + static_cast<size_t>(n + 1) * L, tl, L, fast_b, bn);
       float H = 0.f;
 #pragma unroll
       for (int j = 0; j < kT; ++j) H = __builtin_fmaf(fast_exp2(dlt[j] * a2), H, dlu[j] * bv[j]);
@@ -409,6 +413,10 @@ __global__ __launch_bounds__(kRebuildW * 64) void carry_rebuild_kernel(FwdParams
       if (seg_idx < p.n_seg) p.carries[(chan * N + n) * p.n_seg + seg_idx] = hin;
       const float run_new = readlane(hend, 63);
       if (lane == 0) s_run[w][n] = run_new;
+      if (n + 1 < N) {
+#pragma unroll
+        for (int j = 0; j < kT; ++j) bv[j] = bn[j];
+      }
     }
   }
 }
