@@ -406,18 +406,19 @@ class MambaBlock(nn.Module):
     def gemm_weights(self):
         return [self.in_proj, self.z_proj, self.out_proj, self.s6.x_proj, self.s6.dt_proj]
 
-    def forward(self, h, delta, batch, seq_lens=None, act_dtype=torch.bfloat16, weights=None):
+    def forward(self, h, delta, batch, seq_lens=None, act_dtype=torch.bfloat16, weights=None, A=None):
         """h: (d_model, B*L) fp32 residual stream before the previous block's output `delta`
         (act_dtype, or None for the first block) is added. Returns (h + delta, this block's
         output): the residual add is fused into the next norm. The mixer between the norm and
-        the out-projection is one autograd node (_MambaMixer)."""
+        the out-projection is one autograd node (_MambaMixer). A: the S6 state matrix when the
+        caller computed it (MambaLM does so for all blocks at once), else computed here."""
         weights = weights or _PLAIN
         h, x = self.norm(h, delta, act_dtype)
         s6 = self.s6
         w_xz = weights.stacked(self.in_proj, self.z_proj)
         if w_xz is None or w_xz.dtype != act_dtype:
             w_xz = torch.cat([self.in_proj.detach(), self.z_proj.detach()]).to(act_dtype)
-        A = s6.a_matrix()
+        A = s6.a_matrix() if A is None else A
         y, last, xz = _MambaMixer.apply(
             x, self.in_proj, self.z_proj, self.conv_weight, self.conv_bias, s6.x_proj, s6.dt_proj, A,
             None if s6.D is None else s6.D.float(), s6.dt_bias.float(), w_xz,
@@ -476,10 +477,18 @@ class MambaLM(nn.Module):
             weights = self._shadows
         h = self.embedding[tokens.reshape(-1)].t().contiguous()   # (d_model, B*L) fp32
         delta = None
-        for blk in self.blocks:
-            h, delta = blk(h, delta, batch, seq_lens, act_dtype, weights)
+        for blk, A in zip(self.blocks, self.a_matrices()):
+            h, delta = blk(h, delta, batch, seq_lens, act_dtype, weights, A)
         _, hn = self.final_norm(h, delta, act_dtype)
         return weights.head(hn, self.embedding)
+
+    def a_matrices(self):
+        """Every block's S6 state matrix. Real A = -exp(A_log) of all blocks in one batched op
+        (a few launches per step each way instead of two per block and direction)."""
+        s6s = [blk.s6 for blk in self.blocks]
+        if any(s.complex_ssm for s in s6s) or len({tuple(s.A_log.shape) for s in s6s}) != 1:
+            return [s.a_matrix() for s in s6s]
+        return torch.stack([s.A_log for s in s6s]).float().exp().neg().unbind(0)
 
     @torch.no_grad()
     def prefill(self, tokens, act_dtype=torch.bfloat16):
