@@ -144,6 +144,28 @@ def gpu_step_setup(torch, cfg):
     return lib, t, fa, ba, lens
 
 
+DEVICE_WARMUP_S = 0.2
+
+
+def warm_up_device(torch):
+    """Back-to-back bf16 GEMMs for about DEVICE_WARMUP_S seconds, right before a timed leg's
+    warmup steps (its inputs already set up): a GPU that idled, even for the few tens of ms a
+    leg's host-side setup takes, runs its next tens of milliseconds of work slower (kernel
+    trace of a bench run: every config's scan kernels start 8-15 % slow and settle after about
+    60 ms of work), which a short warmup of the measured step alone does not cover. The leg's
+    own warmup and timed steps are unchanged."""
+    if DEVICE_WARMUP_S <= 0:
+        return
+    a = torch.randn(2048, 2048, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(2048, 2048, device="cuda", dtype=torch.bfloat16)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < DEVICE_WARMUP_S:
+        for _ in range(40):
+            a = torch.mm(a, b).mul_(1.0 / 45)
+        torch.cuda.synchronize()
+    del a, b
+
+
 def run_gpu(torch, cfg, steps, warmup, graph=True):
     """Times `steps` fwd+bwd steps of the scan at `cfg`. The step rate comes from a timed
     region holding only the steps (replays of one captured HIP graph of the step's three
@@ -168,6 +190,14 @@ def run_gpu(torch, cfg, steps, warmup, graph=True):
 
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
+    g = None
+    if graph:  # captured before the warm-up: no host work between it and the timed steps
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(torch.cuda.current_stream().cuda_stream)
+        g.replay()  # the first replay uploads the graph
+        torch.cuda.synchronize()
+    warm_up_device(torch)
     for _ in range(warmup):
         step(sp)
     torch.cuda.synchronize()
@@ -187,11 +217,6 @@ def run_gpu(torch, cfg, steps, warmup, graph=True):
     eager_ms = timed(lambda: step(sp))
     ms = eager_ms
     if graph:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step(torch.cuda.current_stream().cuda_stream)
-        g.replay()
-        torch.cuda.synchronize()
         ms = timed(g.replay)
         del g
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
@@ -258,6 +283,7 @@ def run_reference_api(torch, steps, warmup):
                 P(dy), P(dfin), *[P(t) for t in grads], P(ws), ws_bytes)
     fwd = lambda: _lib.check(lib.mss_scan_fwd(*fwd_args), "mss_scan_fwd")
     bwd = lambda: _lib.check(lib.mss_scan_bwd_ws(*bwd_args), "mss_scan_bwd_ws")
+    warm_up_device(torch)
     for _ in range(warmup):
         fwd()
         bwd()
@@ -369,6 +395,7 @@ def run_complex_c2(torch, steps, warmup):
         if evs:
             evs[2].record(stream)
 
+    warm_up_device(torch)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -657,6 +684,9 @@ def main():
                          "plus their forward at the reference's own shapes (0 skips them)")
     ap.add_argument("--train-eager", action="store_true",
                     help="time the config-5 step eagerly only (no HIP graph capture)")
+    ap.add_argument("--device-warmup-s", type=float, default=0.2,
+                    help="seconds of bf16 GEMMs run right before each timed leg's warmup steps, so that "
+                         "the GPU has left its idle clocks (0 disables it)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the timed region, copy a device buffer of this many MiB twice "
                          "(a kernel of known traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -674,14 +704,8 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
     cfg = C2
-    # The other scan configs first: a GPU coming out of idle runs its first tens of ms of work
-    # slower (measured: the c2 backward at 240-260 us in the first calls, 216 us after about
-    # 60 ms), so the headline is timed at working clocks, with its W warmup and K timed steps.
-    others = [c for c in args.configs.split(",") if c and c != "c2"]
-    results = {}
-    for name in others:
-        c = CONFIGS[name]
-        results[name] = run_gpu(torch, c, args.config_steps, max(1, args.config_steps // 4))
+    global DEVICE_WARMUP_S
+    DEVICE_WARMUP_S = args.device_warmup_s
     r2 = run_gpu(torch, cfg, args.steps, args.warmup)
     ms, fwd_ms, bwd_ms, red_ms = r2["ms"], r2["fwd"], r2["bwd_scan"], r2["bwd_reduce"]
     fwd_bytes, bwd_bytes = algorithmic_bytes(cfg)
@@ -705,8 +729,12 @@ def main():
         log(f"[bench] calibration copy of {args.calibration_copy_mib} MiB done")
         del src, dst
     per_config = {"c2": scan_report(cfg, r2)}
+    others = [c for c in args.configs.split(",") if c and c != "c2"]
+    results = {}
     for name in others:
-        per_config[name] = scan_report(CONFIGS[name], results[name])
+        c = CONFIGS[name]
+        results[name] = run_gpu(torch, c, args.config_steps, max(1, args.config_steps // 4))
+        per_config[name] = scan_report(c, results[name])
     train = None
     if args.train_steps > 0:
         train = run_train_c5(torch, args.train_steps, args.train_warmup, graph=not args.train_eager)
