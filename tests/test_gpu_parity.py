@@ -398,6 +398,38 @@ def test_wide_state_fp32(n, zoh, lens):
     check_fused(ts, out, last, fw, g)
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes(seed):
+    """Seeded random cases across the contract at once: batch 1-4, 1-70 channels (partial
+    waves and channel rounds), lengths 1-2600 (ragged chunk tails), 1-16 states (17-40 for
+    some float32 cases: the grouped backward), float32 or bf16, Euler or ZOH, with or without
+    the fused extras and softplus, with or without variable lengths (zeros and full rows
+    included). Every output and gradient against the float64 oracle at the dtype's bar."""
+    rng = np.random.default_rng(7000 + seed)
+    dtype = "bf16" if rng.random() < 0.35 else "f32"
+    b, d = int(rng.integers(1, 5)), int(rng.integers(1, 71))
+    l = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 2601))]))
+    n = int(rng.integers(17, 41)) if dtype == "f32" and rng.random() < 0.2 else int(rng.integers(1, 17))
+    zoh, extras, softplus = bool(rng.random() < 0.4), bool(rng.random() < 0.7), bool(rng.random() < 0.8)
+    lens = None
+    if rng.random() < 0.4:
+        lens = [int(v) for v in rng.integers(0, l + 1, size=b)]
+        lens[int(rng.integers(0, b))] = int(rng.choice([0, l]))
+    log(f"case random seed={seed}: {dtype} B={b} D={d} L={l} N={n} zoh={zoh} extras={extras} "
+        f"softplus={softplus} lens={lens}")
+    x, dout, dlast = fused_case(8000 + seed, b, d, l, n, dtype, lens=lens, extras=extras)
+    if not softplus:  # raw delta + bias must stay positive (a decaying state)
+        x["delta"] = np.abs(x["delta"]) * 0.1
+        if dtype == "bf16":
+            from mamba_amd.configs import round_to_bf16
+            x["delta"] = round_to_bf16(x["delta"])
+        if "delta_bias" in x:
+            x["delta_bias"] = np.abs(x["delta_bias"]) * 0.01
+    ts, out, last = run_fused(x, dout, dlast, dtype, zoh, softplus=softplus)
+    fw, g = oracle_fused(x, dout, dlast, zoh, softplus=softplus)
+    check_fused(ts, out, last, fw, g, *tol(dtype))
+
+
 def test_deterministic_rerun():
     log("case determinism")
     x, dout, dlast = fused_case(600, 2, 64, 1500, 16)
