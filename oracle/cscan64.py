@@ -80,10 +80,16 @@ def forward(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=F
 
 
 def backward(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_softplus=False,
-             initial_state=None, seq_lens=None, discretization="euler", dlast_state=None):
+             initial_state=None, seq_lens=None, discretization="euler", dlast_state=None,
+             abs_terms=False):
     """Gradients of sum(out * dout) + Re(sum(conj(dlast_state) * last_state)) w.r.t. every
     input: dict(du, ddelta, dA (complex), dB, dC, dD, dz, ddelta_bias, dinitial_state
-    (complex)). States are stored in full (O(B*D*N*L)): small cases only."""
+    (complex)). States are stored in full (O(B*D*N*L)): small cases only.
+
+    With ``abs_terms`` the dict also holds, for each gradient that sums over channels, batch
+    rows or steps, the sum of the absolute values of the terms it adds up (``dA_abs``, with
+    the real and imaginary parts summed separately, ``dB_abs``, ``dC_abs``, ``dD_abs``,
+    ``ddelta_bias_abs``): the scale that bounds the rounding error of any summation order."""
     zoh = discretization == "zoh"
     fw = forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, initial_state, seq_lens,
                  discretization)
@@ -110,6 +116,8 @@ def backward(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_sof
     dA = np.zeros((dim, n), np.complex128)
     dB = np.zeros((bsz, n, L))
     dC = np.zeros((bsz, n, L))
+    ddl_a, dA_a, dB_a, dC_a = np.zeros_like(ddl), np.zeros_like(dA), np.zeros_like(dB), np.zeros_like(dC)
+    cabs = lambda c: np.abs(c.real) + 1j * np.abs(c.imag)
     Ar, Ai = A.real[None], A.imag[None]
     for t in range(L - 1, -1, -1):
         a_bar, E, s, _ = disc[t]
@@ -119,30 +127,55 @@ def backward(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_sof
         dl_t = dl[:, :, t][:, :, None]
         u_t = u[:, :, t][:, :, None]
         B_t = B[:, None, :, t]
-        dA += np.sum(dl_t * W, axis=0)
-        ddl[:, :, t] += np.sum(W.real * Ar + W.imag * Ai, axis=2)
+        ta = dl_t * W
+        dA += np.sum(ta, axis=0)
+        tq = W.real * Ar + W.imag * Ai
+        ddl[:, :, t] += np.sum(tq, axis=2)
+        if abs_terms:
+            dA_a += np.sum(cabs(ta), axis=0)
+            ddl_a[:, :, t] += np.sum(np.abs(W.real * Ar) + np.abs(W.imag * Ai), axis=2)
         if zoh:
             ge = (np.conj(E) * lam).real  # d L / d s, s = B u
             du[:, :, t] += np.sum(B_t * ge, axis=2)
-            dB[:, :, t] += np.sum(u_t * ge, axis=1)
-            ddl[:, :, t] += np.sum(s * (np.conj(a_bar) * lam).real, axis=2)
-            dA += np.sum(np.conj((dl_t * a_bar - E) / A[None]) * lam * s, axis=0)
+            tB = u_t * ge
+            dB[:, :, t] += np.sum(tB, axis=1)
+            tr = s * (np.conj(a_bar) * lam).real
+            ddl[:, :, t] += np.sum(tr, axis=2)
+            tb = np.conj((dl_t * a_bar - E) / A[None]) * lam * s
+            dA += np.sum(tb, axis=0)
+            if abs_terms:
+                dB_a[:, :, t] += np.sum(np.abs(tB), axis=1)
+                ddl_a[:, :, t] += np.sum(np.abs(tr), axis=2)
+                dA_a += np.sum(cabs(tb), axis=0)
         else:
             lr = lam.real
             du[:, :, t] += dl_t[:, :, 0] * np.sum(lr * B_t, axis=2)
             ddl[:, :, t] += u_t[:, :, 0] * np.sum(lr * B_t, axis=2)
-            dB[:, :, t] += np.sum(lr * (dl_t * u_t), axis=1)
-        dC[:, :, t] += np.sum(g[:, :, t, None] * h_t.real, axis=1)
+            tB = lr * (dl_t * u_t)
+            dB[:, :, t] += np.sum(tB, axis=1)
+            if abs_terms:
+                ddl_a[:, :, t] += np.abs(u_t[:, :, 0]) * np.sum(np.abs(lr * B_t), axis=2)
+                dB_a[:, :, t] += np.sum(np.abs(tB), axis=1)
+        tC = g[:, :, t, None] * h_t.real
+        dC[:, :, t] += np.sum(tC, axis=1)
+        if abs_terms:
+            dC_a[:, :, t] += np.sum(np.abs(tC), axis=1)
         m = np.conj(a_bar) * lam
-    dD = None
+    dD = dD_a = None
     if Dv is not None:
         du += Dv[None, :, None] * g
         dD = np.sum(g * u, axis=(0, 2))
-    dx = np.where(x > SOFTPLUS_THRESHOLD, ddl, ddl * sigmoid64(x)) if delta_softplus else ddl
-    dx = dx * mask[:, None, :]
+        dD_a = np.sum(np.abs(g * u), axis=(0, 2))
+    sp = np.where(x > SOFTPLUS_THRESHOLD, 1.0, sigmoid64(x)) if delta_softplus else 1.0
+    dx = ddl * sp * mask[:, None, :]
+    dx_a = ddl_a * sp * mask[:, None, :]
     du = du * mask[:, None, :]
     if dz is not None:
         dz = dz * mask[:, None, :]
     ddelta_bias = None if delta_bias is None else np.sum(dx, axis=(0, 2))
-    return dict(du=du, ddelta=dx, dA=dA, dB=dB, dC=dC, dD=dD, dz=dz, ddelta_bias=ddelta_bias,
-                dinitial_state=m)
+    res = dict(du=du, ddelta=dx, dA=dA, dB=dB, dC=dC, dD=dD, dz=dz, ddelta_bias=ddelta_bias,
+               dinitial_state=m)
+    if abs_terms:
+        res.update(dA_abs=dA_a, dB_abs=dB_a, dC_abs=dC_a, dD_abs=dD_a,
+                   ddelta_bias_abs=None if delta_bias is None else np.sum(dx_a, axis=(0, 2)))
+    return res

@@ -80,13 +80,43 @@ def test_real_A_reduces_to_real_scan(disc):
     np.testing.assert_allclose(c["out"], r["out"], rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(c["last_state"], r["last_state"], rtol=1e-12, atol=1e-12)
     gc = cscan64.backward(x["u"], x["delta"], x["A"], x["B"], x["C"], dout,
-                          initial_state=x["initial_state"], dlast_state=dlast + 0j, **kw)
+                          initial_state=x["initial_state"], dlast_state=dlast + 0j, abs_terms=True, **kw)
     gr = scan64.backward(x["u"], x["delta"], x["A"].real, x["B"], x["C"], dout,
-                         initial_state=x["initial_state"].real, dlast_state=dlast, **kw)
+                         initial_state=x["initial_state"].real, dlast_state=dlast, abs_terms=True, **kw)
     for k in ("du", "ddelta", "dB", "dC", "dD", "dz", "ddelta_bias"):
         np.testing.assert_allclose(gc[k], gr[k], rtol=1e-11, atol=1e-11, err_msg=k)
     np.testing.assert_allclose(gc["dA"].real, gr["dA"], rtol=1e-11, atol=1e-11)
     np.testing.assert_allclose(gc["dinitial_state"], gr["dinitial_state"], rtol=1e-11, atol=1e-11)
+    # the |term| sums of the reduction gradients decompose into the real scan's terms too
+    for k in ("dB_abs", "dC_abs", "dD_abs", "ddelta_bias_abs"):
+        np.testing.assert_allclose(gc[k], gr[k], rtol=1e-11, atol=1e-11, err_msg=k)
+    np.testing.assert_allclose(gc["dA_abs"].real, gr["dA_abs"], rtol=1e-11, atol=1e-11)
+    assert np.all(gc["dA_abs"].imag == 0)
+
+
+@pytest.mark.parametrize("zoh", [False, True])
+def test_abs_term_sums_bound_the_reduction_gradients(zoh):
+    """|sum of terms| <= sum of |terms| for every reduction gradient (real and imaginary
+    parts of dA apart), the gradients themselves unchanged by abs_terms, and equality where
+    every term has one sign: dD = sum g u with z absent and dout = sign(u)."""
+    rng = np.random.default_rng(40 + zoh)
+    x = complex_inputs(rng)
+    dout = rng.standard_normal(x["u"].shape)
+    kw = dict(D=x["D"], z=x["z"], delta_bias=x["delta_bias"], delta_softplus=True, seq_lens=[23, 17],
+              initial_state=x["initial_state"], discretization="zoh" if zoh else "euler")
+    args = (x["u"], x["delta"], x["A"], x["B"], x["C"], dout)
+    g = cscan64.backward(*args, abs_terms=True, **kw)
+    g0 = cscan64.backward(*args, **kw)
+    for k in g0:
+        if g0[k] is not None:
+            assert np.array_equal(g[k], g0[k]), k
+    for k in ("dB", "dC", "dD", "ddelta_bias"):
+        assert np.all(np.abs(g[k]) <= g[k + "_abs"] * (1 + 1e-12)), k
+    assert np.all(np.abs(g["dA"].real) <= g["dA_abs"].real * (1 + 1e-12))
+    assert np.all(np.abs(g["dA"].imag) <= g["dA_abs"].imag * (1 + 1e-12))
+    kw.pop("z")
+    g = cscan64.backward(x["u"], x["delta"], x["A"], x["B"], x["C"], np.sign(x["u"]), abs_terms=True, **kw)
+    np.testing.assert_allclose(g["dD"], g["dD_abs"], rtol=1e-12)
 
 
 def test_constant_coefficients_geometric_series():

@@ -5,8 +5,9 @@ recipe, tests/test_selective_scan_cuda.py:11-19, lengths {1, 17, 128, 513} forwa
 
 CPU: the oracle still reproduces every fixture. GPU: the HIP path (reference-signature
 Python API with autograd, and the reference-signature C entry point with chunk_states)
-against the fixtures: fp32 within rtol 1e-4 / atol 1e-5; dA/dB/dC (sums over many terms)
-on the tensor's scale.
+against the fixtures: fp32 within rtol 1e-4 / atol 1e-5 per element; for dA/dB/dC (sums over
+many terms) the relative part is taken of each element's sum of |terms|, which the float64
+oracle returns for the fixture's inputs.
 """
 import ctypes
 import sys
@@ -43,11 +44,11 @@ def test_oracle_reproduces_fixture(name):
         np.testing.assert_allclose(stored[k], fresh[k], rtol=1e-12, atol=1e-12, err_msg=k)
 
 
-def _check(name, got, want, normwise=False):
+def _check(name, got, want, scale=None):
     got = got.detach().double().cpu().numpy() if torch.is_tensor(got) else np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     err = np.abs(got - want)
-    bound = 1e-5 + 1e-4 * (np.abs(want).max() if normwise else np.abs(want))
+    bound = 1e-5 + 1e-4 * (np.abs(want) if scale is None else np.asarray(scale, np.float64))
     assert np.all(err <= bound), f"{name}: max err {err.max():.3e}"
 
 
@@ -69,8 +70,11 @@ def test_hip_matches_fixture(name):
         loss = (y * torch.from_numpy(f["dy"]).cuda()).sum() + (fin * torch.from_numpy(f["dfinal_x"]).cuda()).sum()
         loss.backward()
         torch.cuda.synchronize()
+        from oracle import scan64
+        _, ab = scan64.reference_api_backward(f["A"], f["deltas"], f["Bs"], f["Cs"], f["u"], f["x0"], f["dy"],
+                                              f["dfinal_x"], use_euler_barB_approx=euler, abs_terms=True)
         for k, g in (("A", "dA"), ("deltas", "ddeltas"), ("Bs", "dBs"), ("Cs", "dCs"), ("u", "du"), ("x0", "dx0")):
-            _check(g, ts[k].grad, f[g], normwise=g in ("dA", "dBs", "dCs"))
+            _check(g, ts[k].grad, f[g], scale=ab.get(g))
     else:
         # reference-signature C entry point: [B][D][L] layouts and chunk_states
         lib = _lib.register_hip_kernel()

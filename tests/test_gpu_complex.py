@@ -43,15 +43,19 @@ def as_real(a):
     return (np.stack([a.real, a.imag], -1) if np.iscomplexobj(a) else a).astype(np.float64)
 
 
-def close(name, got, ref, rtol=F32_RTOL, atol=F32_ATOL, normwise=False, sens=0.0):
+def close(name, got, ref, rtol=F32_RTOL, atol=F32_ATOL, scale=None, sens=0.0):
+    """|got - ref| <= atol + rtol * s + 4 * sens per element, s = |ref| or `scale` (the
+    oracle's sum of |terms| of a reduction gradient, real and imaginary parts apart)."""
     if torch.is_tensor(got):
         got = got.detach()
         got = torch.view_as_real(got) if got.is_complex() else got
         got = got.float().cpu().numpy()
     ref = as_real(ref)
     assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    s = np.abs(ref) if scale is None else as_real(scale)
+    assert s.shape == ref.shape, (name, s.shape, ref.shape)
     err = np.abs(got - ref)
-    bound = atol + rtol * (np.abs(ref).max() if normwise else np.abs(ref)) + 4.0 * sens
+    bound = atol + rtol * s + 4.0 * sens
     ok = bool(np.all(err <= bound))
     worst = np.argmax(err - bound)
     log(f"  {name:16s} max_abs={err.max():.3e} worst(got={got.flat[worst]:.6e}, "
@@ -122,7 +126,8 @@ def oracle(x, dout, dlast, zoh):
               initial_state=x.get("initial_state"), seq_lens=x.get("seq_lens"),
               discretization="zoh" if zoh else "euler")
     fw = cscan64.forward(x["u"], x["delta"], x["A"], x["B"], x["C"], **kw)
-    g = cscan64.backward(x["u"], x["delta"], x["A"], x["B"], x["C"], dout, dlast_state=dlast, **kw)
+    g = cscan64.backward(x["u"], x["delta"], x["A"], x["B"], x["C"], dout, dlast_state=dlast,
+                         abs_terms=True, **kw)
     return {"out": fw["out"], "last_state": fw["last_state"], **g}
 
 
@@ -149,8 +154,8 @@ def check(x, dout, dlast, zoh, dtype="f32"):
     close("last_state", last, ref["last_state"], rtol, atol, sens=sens["last_state"])
     for k, gname in GRAD_OF.items():
         if k in ts:
-            close(gname, ts[k].grad, ref[gname], rtol, atol, normwise=gname in REDUCTIONS,
-                  sens=sens[gname])
+            close(gname, ts[k].grad, ref[gname], rtol, atol,
+                  scale=ref[gname + "_abs"] if gname in REDUCTIONS else None, sens=sens[gname])
 
 
 @pytest.mark.parametrize("zoh", [False, True])
