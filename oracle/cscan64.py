@@ -26,7 +26,8 @@ as a real 2-vector, ``h_t = M_t h_{t-1} + bu_t`` with ``M_t`` the rotation-scali
 Complex gradients follow torch's convention for a real loss: ``dRe + 1j * dIm``.
 
 Pinning (tests/test_cscan_oracle.py): torch complex128 autograd of an independent loop,
-central finite differences, and the real scan (``scan64``) when ``Im(A) = 0``.
+central finite differences, and the real scan (``scan64``) when ``Im(A) = 0`` (gradients and
+the |term| sums); the |term| sums also by the triangle inequality and an all-positive case.
 """
 from __future__ import annotations
 
