@@ -18,10 +18,10 @@
 // of two buffers while the previous round is computed (one barrier per round).
 #include "mss_common.h"
 
-// Launch shapes. A "wide" shape (16 steps per lane, 4 waves per SIMD) for grids that fill
-// the GPU several times over, and a "narrow" one (8 steps per lane, 6 waves per SIMD: 50%
-// more resident workgroups) for grids that fit in one pass of it, where the wide shape
-// would leave a half-occupied tail pass. Waves per workgroup and states per staging round
+// Launch shapes. A "wide" shape (16 steps per lane, 4 waves per SIMD) for bf16 grids that
+// fill the GPU several times over, and a "narrow" one (8 steps per lane, 6 waves per SIMD:
+// 50% more resident workgroups) for float32 rows and for grids that fit in one pass of it,
+// where the wide shape would leave a half-occupied tail pass. Waves per workgroup and states per staging round
 // are shared; all are overridable at build time for tuning sweeps.
 #ifndef MSS_FWD_W
 #define MSS_FWD_W 8
@@ -323,9 +323,13 @@ static hipError_t launch_fwd_z(const FwdParams& p, hipStream_t stream) {
     }
   }
   // Resident workgroups of the narrow shape: 256 CUs * kOcc waves per SIMD * 4 SIMDs / kW.
+  // Float32 rows take the narrow shape at every grid size (measured on MI355X: B=16 D=2560
+  // L=8192 with variable lengths 1.69 -> 1.39 ms, B=8 D=2048 L=4096 0.54 -> 0.48 ms); bf16
+  // rows take it only when the grid fits one pass of it (B=8 D=2048 L=4096 428 vs 436 us,
+  // B=8 D=1536 L=2048 167 vs 175 us wide vs narrow).
   constexpr long long kNarrowSlots = 256LL * MSS_FWD_OCC_NARROW * 4 / MSS_FWD_W;
   const long long groups = static_cast<long long>(p.batch) * ((p.dim + MSS_FWD_W - 1) / MSS_FWD_W);
-  if (groups <= kNarrowSlots)
+  if (sizeof(io_t) == 4 || groups <= kNarrowSlots)
     return launch_fwd_t<MSS_FWD_T_NARROW, MSS_FWD_W, MSS_FWD_NB, MSS_FWD_OCC_NARROW, kZOH, io_t, bc_t>(p, stream);
   return launch_fwd_t<MSS_FWD_T_WIDE, MSS_FWD_W, MSS_FWD_NB, MSS_FWD_OCC_WIDE, kZOH, io_t, bc_t>(p, stream);
 }

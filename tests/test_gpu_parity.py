@@ -182,16 +182,18 @@ def test_fused_fp32(l, n):
     check_fused(ts, out, last, fw, g)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("zoh", [False, True])
-def test_fused_wide_grid(zoh):
-    """2 x 4096 channels: 1024 forward workgroups, more than one pass of the single-pass
-    launch shape, so the forward takes its 16-step-per-lane shape (the other tests' grids are
-    small); 1100 steps give a full and a ragged chunk of it."""
-    log(f"case fused wide grid zoh={zoh}")
-    x, dout, dlast = fused_case(950 + zoh, 2, 4096, 1100, 16, zoh=zoh)
-    ts, out, last = run_fused(x, dout, dlast, "f32", zoh)
+def test_fused_wide_grid(zoh, dtype):
+    """2 x 4096 channels: 1024 forward workgroups, more than one pass of the 8-step-per-lane
+    launch shape: bf16 rows take the 16-step shape there, float32 rows keep the 8-step one
+    over two passes (the other tests' grids are small); 1100 steps give full and ragged
+    chunks of either."""
+    log(f"case fused wide grid zoh={zoh} {dtype}")
+    x, dout, dlast = fused_case(950 + zoh, 2, 4096, 1100, 16, dtype, zoh=zoh)
+    ts, out, last = run_fused(x, dout, dlast, dtype, zoh)
     fw, g = oracle_fused(x, dout, dlast, zoh)
-    check_fused(ts, out, last, fw, g)
+    check_fused(ts, out, last, fw, g, *tol(dtype))
 
 
 def tol(dtype):
