@@ -630,10 +630,12 @@ static int chan_per_block_for(int waves, int batch, int dim, long long target) {
 BwdPlan bwd_plan(int batch, int dim, int dstate, int varlen) {
   // One workgroup per CU holds the B/C stage and the dB/dC accumulator (LDS), so the grid
   // should fit one pass over the 256 CUs. With variable lengths rows finish at different
-  // times, so workgroups stay ~4x smaller and the hardware balances them. Of 12 and 16
+  // times, so workgroups stay ~2x smaller and the hardware balances them (rows are handed
+  // out longest first; measured on MI355X at B=16 D=2560 L=8192: 2x 4.68 ms per step, 4x
+  // 4.83 with twice the dB/dC partials, 1x 4.99 with a longer tail). Of 12 and 16
   // waves the plan takes the one with the smaller modelled time: workgroup passes x rounds
   // x time of a round (16 waves: 1.2x that of 12). Depends on shapes only.
-  const long long target = varlen ? 4 * kCUs : kCUs;
+  const long long target = varlen ? 2 * kCUs : kCUs;
   auto cost = [&](int waves, int cpb) {
     const long long grid = static_cast<long long>(batch) * ((dim + cpb - 1) / cpb);
     const double rounds = static_cast<double>(cpb / waves) * (waves == 16 ? 1.2 : 1.0);
