@@ -189,6 +189,26 @@ def test_complex_varlen_row_permutation():
         assert torch.equal(a[0][k].grad[idx], b[0][k].grad), k
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_complex_random_shapes(seed):
+    """Seeded random cases of the complex scan: batch 1-3, 1-30 channels, lengths 1-1500,
+    1-16 states, Euler or ZOH, with or without the fused extras and lengths, float32 or bf16;
+    every output and gradient against the complex float64 oracle."""
+    rng = np.random.default_rng(600 + seed)
+    b, d = int(rng.integers(1, 4)), int(rng.integers(1, 31))
+    l = int(rng.choice([int(rng.integers(1, 100)), int(rng.integers(100, 1501))]))
+    n = int(rng.integers(1, 17))
+    zoh, extras = bool(rng.random() < 0.5), bool(rng.random() < 0.7)
+    dtype = "bf16" if rng.random() < 0.3 else "f32"
+    lens = None
+    if rng.random() < 0.4:
+        lens = [int(v) for v in rng.integers(0, l + 1, size=b)]
+        lens[int(rng.integers(0, b))] = int(rng.choice([0, l]))
+    log(f"case complex random seed={seed}: {dtype} B={b} D={d} L={l} N={n} zoh={zoh} extras={extras} lens={lens}")
+    x, dout, dlast = complex_case(650 + seed, b, d, l, n, dtype=dtype, lens=lens, extras=extras)
+    check(x, dout, dlast, zoh, dtype=dtype)
+
+
 def test_complex_no_extras():
     log("case complex no extras")
     x, dout, dlast = complex_case(410, 2, 4, 700, 16, extras=False)

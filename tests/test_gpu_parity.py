@@ -544,6 +544,67 @@ def test_reference_c_entry_points(length, n):
     assert not torch.equal(moved[3][:, :, 2048:4096], outs[3][:, :, 2048:4096])
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_reference_api(seed):
+    """Seeded random shapes through the reference's own signatures: the C entry points
+    (mss_scan_fwd, then mss_scan_bwd_ws from the forward's chunk_states, Euler as the
+    reference handler) and the Python `selective_scan` VJP (Euler or ZOH), batch 1-3, 1-40
+    channels, lengths 1-4500 (across 2048-step blocks), 1-16 states (17-40 for some). Every
+    output and gradient against the float64 oracle (the Python signature only where its error
+    contract admits N)."""
+    rng = np.random.default_rng(9000 + seed)
+    b, d = int(rng.integers(1, 4)), int(rng.integers(1, 41))
+    l = int(rng.choice([int(rng.integers(1, 200)), int(rng.integers(2000, 4501))]))
+    r = rng.random()
+    n = int(rng.integers(17, 41)) if r < 0.25 else int(rng.choice([1, 2, 4, 8, 16])) if r < 0.7 else int(rng.integers(1, 17))
+    euler = seed % 2 == 0
+    log(f"case random reference API seed={seed}: B={b} D={d} L={l} N={n} euler(python)={euler}")
+    A, deltas, Bs, Cs, u, x0 = ref_recipe(9100 + seed, batch=b, length=l, dim=d, n=n)
+    dy = rng.standard_normal((b, l, d)).astype(np.float32)
+    dfin = rng.standard_normal((b, d, n)).astype(np.float32)
+    # C entry points ([B][D][L] / [B][N][L] physical layouts)
+    lib = _lib.register_hip_kernel()
+    tr = lambda a: T(np.swapaxes(a, 1, 2))
+    tA, td, tB, tC, tu, tx0, tdy, tdfin = T(A), tr(deltas), tr(Bs), tr(Cs), tr(u), T(x0), tr(dy), T(dfin)
+    y = torch.empty(b, d, l, device=dev)
+    fin = torch.empty(b, d, n, device=dev)
+    cs = torch.empty(b, d, -(-l // 2048), n, 2, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    _lib.check(lib.mss_scan_fwd(st, _lib.MSS_EULER, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu), P(tx0),
+                                P(y), P(fin), P(cs)), "mss_scan_fwd")
+    outs = [torch.full_like(t, float("nan")) for t in (tA, td, tB, tC, tu, tx0)]
+    ws = torch.empty(int(lib.mss_scan_bwd_workspace_bytes(b, l, d, n)), dtype=torch.uint8, device=dev)
+    _lib.check(lib.mss_scan_bwd_ws(st, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu), P(tx0), P(cs), P(tdy),
+                                   P(tdfin), *[P(o) for o in outs], P(ws), ws.numel()), "mss_scan_bwd_ws")
+    torch.cuda.synchronize()
+    ey, efin, ecs = scan64.reference_api_forward(A, deltas, Bs, Cs, u, x0)
+    close("y", y.transpose(1, 2), ey)
+    close("final_x", fin, efin)
+    close("chunk_states", cs, ecs)
+    grads, ab = scan64.reference_api_backward(A, deltas, Bs, Cs, u, x0, dy, dfin, abs_terms=True)
+    names = ["dA", "ddeltas", "dBs", "dCs", "du", "dinitial_x"]
+    for name, o, g in zip(names, outs, grads):
+        close(name, o if o.shape == g.shape else o.transpose(1, 2), g, scale=ab.get(name))
+    # the Python reference signature with autograd (its error contract admits N in {1, 2, 4,
+    # 8, 16} only, as the reference's _validate_inputs does)
+    ts = [T(a).requires_grad_(True) for a in (A, deltas, Bs, Cs, u, x0)]
+    if n not in (1, 2, 4, 8, 16):
+        with pytest.raises(ValueError, match="N must be one of"):
+            selective_scan(*ts, use_euler_barB_approx=euler)
+        return
+    py, pfin = selective_scan(*ts, use_euler_barB_approx=euler)
+    ((py * T(dy)).sum() + (pfin * T(dfin)).sum()).backward()
+    torch.cuda.synchronize()
+    ey, efin, _ = scan64.reference_api_forward(A, deltas, Bs, Cs, u, x0, use_euler_barB_approx=euler)
+    close("py y", py, ey)
+    close("py final_x", pfin, efin)
+    grads, ab = scan64.reference_api_backward(A, deltas, Bs, Cs, u, x0, dy, dfin, use_euler_barB_approx=euler,
+                                              abs_terms=True)
+    for name, t, g in zip(names, ts, grads):
+        close("py " + name, t.grad, g, scale=ab.get(name))
+
+
 def config_tensors(cfg, x, dout):
     tdt = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
     ts = {}
