@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 8
+#define MSS_ABI_VERSION 9
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -60,6 +60,7 @@ extern "C" {
 #define MSS_SEG_STEPS 8     /* step granularity of the `carries` residual */
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
 #define MSS_NOALLOC_SCRATCH_BYTES (128u << 20) /* fixed per-device scratch of mss_bwd_noalloc */
+#define MSS_NORM_GEMV_MAX_FEATURES 1024 /* largest norm->features of mss_norm_gemv_conv_step */
 
 typedef enum mss_status {
   MSS_OK = 0,
@@ -347,6 +348,19 @@ typedef struct mss_norm_args {
 size_t mss_norm_bwd_workspace_bytes(const mss_norm_args* args);
 int mss_norm_fwd(const mss_norm_args* args, void* stream);
 int mss_norm_bwd(const mss_norm_args* args, void* stream);
+
+/* mss_norm_fwd followed by mss_gemv_conv_step on its output, as one launch (no counterpart
+ * symbol in the reference: Mamba.step, mamba/mamba1.py:339-363, normalises the residual
+ * stream and feeds it to the in-projection, whose first rows go through the conv window).
+ * A decode step's block entry: the results (norm->hn, norm->rstd when not NULL,
+ * conv_state, conv->y and the rows of gemv->Y past conv->dim) equal those two calls bit
+ * for bit; norm->x and gemv->X are ignored (may be NULL): every workgroup recomputes the
+ * normalised tokens. norm->features == gemv->K <= MSS_NORM_GEMV_MAX_FEATURES
+ * (MSS_ERR_UNSUPPORTED above),
+ * norm->tokens == gemv->N, io_dtype MSS_BF16, h/delta/hn 16-byte aligned, hn not
+ * overlapping h or delta; the conv and GEMM conditions of mss_gemv_conv_step. */
+int mss_norm_gemv_conv_step(const mss_norm_args* norm, const mss_gemv_args* gemv,
+                            const mss_conv_step_args* conv, void* stream);
 
 /* --- Cross-entropy over bf16 logits [rows][vocab] with fp32 math. -------------------
  * No counterpart symbol in the reference (its training loss is optax softmax

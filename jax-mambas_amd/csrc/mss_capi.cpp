@@ -760,12 +760,14 @@ int conv_step_params(const mss_conv_step_args* a, bool need_x, mss::ConvStepPara
   return MSS_OK;
 }
 
-// Validated GemvParams; need_y false when an epilogue replaces every store to Y.
-int gemv_params(const mss_gemv_args* a, bool need_y, mss::GemvParams* p) {
+// Validated GemvParams; need_y false when an epilogue replaces every store to Y, need_x
+// false when a prologue computes X.
+int gemv_params(const mss_gemv_args* a, bool need_y, mss::GemvParams* p, bool need_x = true) {
   if (a == nullptr || a->M <= 0 || a->K <= 0 || a->K % 8 != 0) return MSS_ERR_INVALID_ARGUMENT;
   if (a->N != 1 && a->N != 2 && a->N != 4 && a->N != 8) return MSS_ERR_UNSUPPORTED;
-  if (a->ldw < a->K || a->ldw % 8 != 0 || !a->W || !a->X || (need_y && !a->Y)) return MSS_ERR_INVALID_ARGUMENT;
-  if (!aligned16(a->W) || !aligned16(a->X) || reinterpret_cast<uintptr_t>(a->Y) % 2 != 0)
+  if (a->ldw < a->K || a->ldw % 8 != 0 || !a->W || (need_x && !a->X) || (need_y && !a->Y))
+    return MSS_ERR_INVALID_ARGUMENT;
+  if (!aligned16(a->W) || (need_x && !aligned16(a->X)) || reinterpret_cast<uintptr_t>(a->Y) % 2 != 0)
     return MSS_ERR_INVALID_ARGUMENT;
   if (static_cast<long long>(a->K) * a->N * 2 > 65536) return MSS_ERR_UNSUPPORTED;  // X staged in LDS
   p->M = a->M;
@@ -802,18 +804,60 @@ int mss_gemv(const mss_gemv_args* a, void* stream) {
   return s != MSS_OK ? s : run_gemv(p, stream);
 }
 
-int mss_gemv_conv_step(const mss_gemv_args* g, const mss_conv_step_args* c, void* stream) {
+namespace {
+// GemvParams of a GEMM with the conv-window step fused on its first conv->dim rows.
+int gemv_conv_params(const mss_gemv_args* g, const mss_conv_step_args* c, bool need_x, mss::GemvParams* p) {
   if (g == nullptr || c == nullptr) return MSS_ERR_INVALID_ARGUMENT;
-  mss::GemvParams p{};
-  int s = gemv_params(g, c->dim < g->M, &p);
-  if (s == MSS_OK) s = conv_step_params(c, false, &p.cs);
+  int s = gemv_params(g, c->dim < g->M, p, need_x);
+  if (s == MSS_OK) s = conv_step_params(c, false, &p->cs);
   if (s != MSS_OK) return s;
   if (c->io_dtype != MSS_BF16 || c->batch != g->N || c->dim > g->M) return MSS_ERR_INVALID_ARGUMENT;
   // the fused kernel indexes the step's operands with int offsets
-  const long long span = (c->batch - 1LL) * p.cs.sb + (c->dim - 1LL) * p.cs.sd;
+  const long long span = (c->batch - 1LL) * p->cs.sb + (c->dim - 1LL) * p->cs.sd;
   if (span >= (1LL << 31) || static_cast<long long>(c->batch) * c->dim * c->width >= (1LL << 31))
     return MSS_ERR_UNSUPPORTED;
-  p.epi = 1;
+  p->epi = 1;
+  return MSS_OK;
+}
+
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return a != nullptr && b != nullptr && x < y + nb && y < x + na;
+}
+}  // namespace
+
+int mss_gemv_conv_step(const mss_gemv_args* g, const mss_conv_step_args* c, void* stream) {
+  mss::GemvParams p{};
+  const int s = gemv_conv_params(g, c, true, &p);
+  return s != MSS_OK ? s : run_gemv(p, stream);
+}
+
+int mss_norm_gemv_conv_step(const mss_norm_args* n, const mss_gemv_args* g, const mss_conv_step_args* c,
+                            void* stream) {
+  if (n == nullptr) return MSS_ERR_INVALID_ARGUMENT;
+  mss::GemvParams p{};
+  const int s = gemv_conv_params(g, c, false, &p);
+  if (s != MSS_OK) return s;
+  if (n->features != g->K || n->tokens != g->N || n->io_dtype != MSS_BF16 || !(n->eps >= 0.f) || !n->h ||
+      !n->weight || (n->delta && !n->hn))
+    return MSS_ERR_INVALID_ARGUMENT;
+  if (!aligned16(n->h) || !aligned16(n->delta) || !aligned16(n->hn)) return MSS_ERR_INVALID_ARGUMENT;
+  // workgroup 0 writes hn while the others still read h and delta
+  const size_t stream_bytes = static_cast<size_t>(n->features) * n->tokens * sizeof(float);
+  if (n->delta && (overlaps(n->hn, stream_bytes, n->h, stream_bytes) ||
+                   overlaps(n->hn, stream_bytes, n->delta, stream_bytes / 2)))
+    return MSS_ERR_INVALID_ARGUMENT;
+  static_assert(mss::kNormGemvMaxFeatures == MSS_NORM_GEMV_MAX_FEATURES, "header and kernel disagree");
+  if (n->features > MSS_NORM_GEMV_MAX_FEATURES) return MSS_ERR_UNSUPPORTED;
+  p.norm = 1;
+  p.nm.features = n->features;
+  p.nm.tokens = n->tokens;
+  p.nm.eps = n->eps;
+  p.nm.h = n->h;
+  p.nm.delta = n->delta;
+  p.nm.w = n->weight;
+  p.nm.hn = n->hn;
+  p.nm.rstd = n->rstd;
   return run_gemv(p, stream);
 }
 

@@ -353,6 +353,9 @@ struct ConvStepParams {
   void* y;
 };
 
+// Largest feature count of the RMSNorm prologue fused in front of the decode GEMM.
+constexpr int kNormGemvMaxFeatures = 1024;
+
 struct GemvParams {
   int M, K, N;      // Y [M][N] = W [M][K] X [K][N]
   long long ldw;    // W row stride (elements)
@@ -366,6 +369,11 @@ struct GemvParams {
   int epi, zoh;
   ConvStepParams cs;
   StepParams ss;
+  // norm != 0: X is not read; each workgroup computes it as the residual add + RMSNorm of
+  // nm (features K, tokens N, bf16 delta and x) and workgroup 0 writes nm.hn (when delta)
+  // and nm.rstd (when not null); nm.x is not written.
+  int norm;
+  NormParams nm;
 };
 
 struct ConvParams {

@@ -185,6 +185,126 @@ __device__ __forceinline__ void ssm_epilogue(const StepParams& p, bool zoh, int 
 }
 
 
+// Features of the residual stream one thread holds in the norm prologue.
+constexpr int kNormFeat = kNormGemvMaxFeatures / 256;
+
+// kN float32 values of one stream row (16-byte aligned when kN >= 4).
+template <int kN>
+__device__ __forceinline__ void load_hrow(const float* h, float (&v)[kN]) {
+  if constexpr (kN >= 4) {
+#pragma unroll
+    for (int q = 0; q < kN / 4; ++q) {
+      const f32x4 a = reinterpret_cast<const f32x4*>(h)[q];
+      v[4 * q] = a.x;
+      v[4 * q + 1] = a.y;
+      v[4 * q + 2] = a.z;
+      v[4 * q + 3] = a.w;
+    }
+  } else if constexpr (kN == 2) {
+    const float2 a = *reinterpret_cast<const float2*>(h);
+    v[0] = a.x;
+    v[1] = a.y;
+  } else {
+    v[0] = h[0];
+  }
+}
+
+template <int kN>
+__device__ __forceinline__ void store_hrow(float* h, const float (&v)[kN]) {
+  if constexpr (kN >= 4) {
+#pragma unroll
+    for (int q = 0; q < kN / 4; ++q)
+      reinterpret_cast<f32x4*>(h)[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+  } else if constexpr (kN == 2) {
+    *reinterpret_cast<float2*>(h) = float2{v[0], v[1]};
+  } else {
+    h[0] = v[0];
+  }
+}
+
+// kN bf16 values as one 2kN-byte store (LDS).
+template <int kN>
+__device__ __forceinline__ void store_xrow(bf16_t* x, const float (&v)[kN]) {
+  uint32_t b[kN];
+#pragma unroll
+  for (int c = 0; c < kN; ++c) b[c] = f32_to_bf16(v[c]).bits;
+  if constexpr (kN == 8) {
+    *reinterpret_cast<u32x4*>(x) = u32x4{b[0] | b[1] << 16, b[2] | b[3] << 16, b[4] | b[5] << 16, b[6] | b[7] << 16};
+  } else if constexpr (kN == 4) {
+    *reinterpret_cast<uint2*>(x) = uint2{b[0] | b[1] << 16, b[2] | b[3] << 16};
+  } else if constexpr (kN == 2) {
+    *reinterpret_cast<uint32_t*>(x) = b[0] | b[1] << 16;
+  } else {
+    x[0].bits = static_cast<uint16_t>(b[0]);
+  }
+}
+
+// X = RMSNorm(h + delta) * w of the kN tokens into LDS: the arithmetic of
+// add_rmsnorm_fwd_rows_kernel (mss_norm.hip) for each token, in the same order (thread t
+// sums its features t, t + 256, .. by fma, the waves by wave_sum, then waves 0..3 in
+// order; x = (hn * rstd) * w rounded to bf16), so X equals that kernel's output bit for
+// bit. Every workgroup computes X (a few KB from the L2); workgroup 0 also stores hn and
+// rstd. The stream loads are issued before any use, behind the weights already in flight.
+template <int kN>
+__device__ __forceinline__ void norm_prologue(const NormParams& q, int K, bf16_t* X, float (*s_ss)[4]) {
+  const int tid = threadIdx.x;
+  const bf16_t* __restrict__ delta = static_cast<const bf16_t*>(q.delta);
+  float v[kNormFeat][kN], w[kNormFeat];
+#pragma unroll
+  for (int j = 0; j < kNormFeat; ++j) {
+    const int f = min(tid + 256 * j, K - 1);
+    load_hrow<kN>(q.h + f * kN, v[j]);
+    w[j] = q.w[f];
+  }
+  if (delta) {
+    float dv[kNormFeat][kN];
+#pragma unroll
+    for (int j = 0; j < kNormFeat; ++j) load_xrow<kN>(delta + min(tid + 256 * j, K - 1) * kN, dv[j]);
+#pragma unroll
+    for (int j = 0; j < kNormFeat; ++j)
+#pragma unroll
+      for (int c = 0; c < kN; ++c) v[j][c] += dv[j][c];
+  }
+  float ss[kN];
+#pragma unroll
+  for (int c = 0; c < kN; ++c) ss[c] = 0.f;
+#pragma unroll
+  for (int j = 0; j < kNormFeat; ++j) {
+    if (tid + 256 * j < K) {
+#pragma unroll
+      for (int c = 0; c < kN; ++c) ss[c] = __builtin_fmaf(v[j][c], v[j][c], ss[c]);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kN; ++c) {
+    const float t = wave_sum(ss[c]);
+    if ((tid & 63) == 0) s_ss[c][tid >> 6] = t;
+  }
+  __syncthreads();
+  float r[kN];
+#pragma unroll
+  for (int c = 0; c < kN; ++c) {
+    const float tot = s_ss[c][0] + s_ss[c][1] + s_ss[c][2] + s_ss[c][3];
+    r[c] = 1.f / __builtin_sqrtf(tot / K + q.eps);
+  }
+  const bool first = blockIdx.x == 0;
+#pragma unroll
+  for (int j = 0; j < kNormFeat; ++j) {
+    const int f = tid + 256 * j;
+    if (f < K) {
+      if (first && delta) store_hrow<kN>(q.hn + f * kN, v[j]);
+      float x[kN];
+#pragma unroll
+      for (int c = 0; c < kN; ++c) x[c] = v[j][c] * r[c] * w[j];
+      store_xrow<kN>(X + f * kN, x);
+    }
+  }
+  if (first && q.rstd && tid == 0) {
+#pragma unroll
+    for (int c = 0; c < kN; ++c) q.rstd[c] = r[c];
+  }
+}
+
 // A workgroup of 4 waves stages X (K x N bf16, at most 64 KB) in LDS once; each wave
 // produces kR consecutive rows of Y: lane l covers K elements 8l + 512 s (s = 0, 1, ..),
 // reading 16 bytes of each of its kR weight rows per step, and the wave sums over its
@@ -192,11 +312,12 @@ __device__ __forceinline__ void ssm_epilogue(const StepParams& p, bool zoh, int 
 // before X is staged, so one memory latency covers them all. Rows past M are clamped to
 // M - 1 for the reads and never stored. The row's sums are rounded to bf16 before the
 // epilogue (kEpi, as GemvParams::epi), so a fused epilogue sees the values the separate
-// step kernel would read back from Y.
-template <int kN, int kR, int kEpi, int kPre>
+// step kernel would read back from Y. kNorm: X is the norm prologue's (norm_prologue).
+template <int kN, int kR, int kEpi, int kPre, bool kNorm>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   static_assert(kEpi == 0 || kR == 1, "fused epilogues take one row per wave");
   extern __shared__ u32x4 s_x[];
+  __shared__ float s_ss[kNorm ? kN : 1][4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // wave-uniform row index in a scalar register (the per-channel operands then come
@@ -220,9 +341,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
       wq[st][r] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + (k0 < p.K ? k0 : 0));
     }
   }
-  const int n_q = p.K * kN / 8;  // 16-byte words of X (K % 8 == 0)
-  const u32x4* __restrict__ xg = static_cast<const u32x4*>(p.X);
-  for (int i = tid; i < n_q; i += 256) s_x[i] = xg[i];
+  if constexpr (kNorm) {
+    norm_prologue<kN>(p.nm, p.K, reinterpret_cast<bf16_t*>(s_x), s_ss);
+  } else {
+    const int n_q = p.K * kN / 8;  // 16-byte words of X (K % 8 == 0)
+    const u32x4* __restrict__ xg = static_cast<const u32x4*>(p.X);
+    for (int i = tid; i < n_q; i += 256) s_x[i] = xg[i];
+  }
   __syncthreads();
   if (!wave_on) return;  // after the only barrier
   const bf16_t* X = reinterpret_cast<const bf16_t*>(s_x);
@@ -295,11 +420,23 @@ static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
   if constexpr (kEpi == 0) {
     if (p.M >= 4096) {
       const int waves = (p.M + 3) / 4;
-      hipLaunchKernelGGL((gemv_kernel<kN, 4, kEpi, kPre>), dim3((waves + 3) / 4), dim3(256), lds, stream, p);
+      hipLaunchKernelGGL((gemv_kernel<kN, 4, kEpi, kPre, false>), dim3((waves + 3) / 4), dim3(256), lds, stream, p);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi, kPre>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
+  // the norm prologue is fused only in front of the conv-window step (the in-projection)
+  if constexpr (kEpi == 1) {
+    if (p.norm) {
+      if (p.K > kNormGemvMaxFeatures) return hipErrorInvalidValue;
+      // (workgroups of 8 or 16 waves, each normalising a share of the tokens and so
+      // re-reading the stream 2x or 4x less, measured slower on MI355X: 0.629 and 0.634 ms
+      // per 130M decode step against 0.625 with 4 waves)
+      hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi, kPre, true>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
+      return hipGetLastError();
+    }
+  }
+  if (p.norm) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi, kPre, false>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
   return hipGetLastError();
 }
 

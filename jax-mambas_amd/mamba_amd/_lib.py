@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 8
+MSS_ABI_VERSION = 9
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -29,6 +29,7 @@ MSS_MAX_DSTATE = 16
 MSS_MAX_DSTATE_WIDE = 256  # float32 real-A scans (backward over groups of MSS_MAX_DSTATE states)
 MSS_SEG_STEPS = 8
 MSS_REF_CHUNK = 2048
+MSS_NORM_GEMV_MAX_FEATURES = 1024
 
 # Every symbol include/mamba_selective_scan.h declares.
 EXPORTED_SYMBOLS = (
@@ -61,6 +62,7 @@ EXPORTED_SYMBOLS = (
     "mss_gemv",
     "mss_gemv_conv_step",
     "mss_gemv_scan_step",
+    "mss_norm_gemv_conv_step",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -219,6 +221,9 @@ def register_hip_kernel(library_path=None):
     lib.mss_gemv_conv_step.restype = ctypes.c_int
     lib.mss_gemv_scan_step.argtypes = [ctypes.POINTER(GemvArgs), ctypes.POINTER(StepArgs), _p]
     lib.mss_gemv_scan_step.restype = ctypes.c_int
+    lib.mss_norm_gemv_conv_step.argtypes = [ctypes.POINTER(NormArgs), ctypes.POINTER(GemvArgs),
+                                            ctypes.POINTER(ConvStepArgs), _p]
+    lib.mss_norm_gemv_conv_step.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

@@ -18,6 +18,11 @@ tokens): w (M, K) bf16 with 16-byte aligned rows, x (K, N) bf16 contiguous and 1
 aligned with N in {1, 2, 4, 8}, K % 8 == 0, 2*K*N <= 64 KiB; y (M, N) bf16, float32
 accumulation. Other shapes and dtypes go through ``torch.mm``.
 
+``norm_gemv_conv_update(h, delta, norm_weight, eps, w, conv_state, weight, bias=None)
+-> (hn, u, rest)`` — the block entry of a decode step: hn, x = add_rmsnorm(h, delta,
+norm_weight, eps) followed by gemv_conv_update(w, x, ...), as one kernel (every workgroup
+normalises the few tokens itself) where it applies, else the two calls; same results.
+
 ``gemv_conv_update(w, x, conv_state, weight, bias=None) -> (u, rest)`` and
 ``gemv_state_update(w, x, state, u, A, B, C, ...) -> out`` — a decode GEMM with the next
 step fused behind it (one kernel instead of two): the conv window step on the first D
@@ -31,9 +36,11 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .lm_ops import add_rmsnorm
 from .selective_scan_hip import _io_tag, _ptr, _require_gpu, _stream
 
-__all__ = ["selective_state_update", "causal_conv1d_update", "gemv", "gemv_conv_update", "gemv_state_update"]
+__all__ = ["selective_state_update", "causal_conv1d_update", "gemv", "gemv_conv_update", "gemv_state_update",
+           "norm_gemv_conv_update"]
 
 
 def _strides2(t):
@@ -118,13 +125,18 @@ def causal_conv1d_update(conv_state, x, weight, bias=None, activation="silu"):
     return y
 
 
+def _gemv_w_ok(w, k, n, device):
+    """Whether mss_gemv takes w for a (k, n) bf16 X on `device` (a few token columns,
+    aligned rows, X fits in LDS)."""
+    return not (w.dtype != torch.bfloat16 or not w.is_cuda or w.device != device or w.ndim != 2
+                or w.shape[1] != k or n not in (1, 2, 4, 8) or k % 8 != 0 or 2 * k * n > 65536
+                or w.stride(1) != 1 or w.stride(0) % 8 != 0 or w.data_ptr() % 16 != 0)
+
+
 def _gemv_ok(w, x):
     """Whether mss_gemv takes w @ x (bf16, a few token columns, aligned, X fits in LDS)."""
-    m, k = w.shape
-    return not (w.dtype != torch.bfloat16 or x.dtype != torch.bfloat16 or not w.is_cuda or x.device != w.device
-                or x.ndim != 2 or x.shape[0] != k or x.shape[1] not in (1, 2, 4, 8) or k % 8 != 0
-                or not x.is_contiguous() or x.data_ptr() % 16 != 0 or 2 * k * x.shape[1] > 65536
-                or w.stride(1) != 1 or w.stride(0) % 8 != 0 or w.data_ptr() % 16 != 0)
+    return (x.dtype == torch.bfloat16 and x.ndim == 2 and x.is_contiguous() and x.data_ptr() % 16 == 0
+            and _gemv_w_ok(w, x.shape[0], x.shape[1], x.device))
 
 
 def _gemv_args(w, x, y):
@@ -160,6 +172,40 @@ def gemv_conv_update(w, x, conv_state, weight, bias=None, activation="silu"):
     lib = _lib.register_hip_kernel()
     _lib.check(lib.mss_gemv_conv_step(_gemv_args(w, x, v), a, _stream(x)), "mss_gemv_conv_step")
     return u, v[dim:]
+
+
+def _aligned_matrix(t, shape, dtype):
+    return t.dtype == dtype and tuple(t.shape) == shape and t.is_contiguous() and t.data_ptr() % 16 == 0
+
+
+def norm_gemv_conv_update(h, delta, norm_weight, eps, w, conv_state, weight, bias=None, activation="silu"):
+    """(hn, u, rest): hn, x = add_rmsnorm(h, delta, norm_weight, eps) (h: the float32
+    (features, B) stream, delta: the previous block's bf16 output or None) and
+    u, rest = gemv_conv_update(w, x, conv_state, weight, bias, activation), as one HIP
+    kernel (mss_norm_gemv_conv_step) where it applies, else the calls; same results."""
+    f, n = h.shape
+    dim = weight.shape[0]
+    fused = (_aligned_matrix(h, (f, n), torch.float32) and f <= _lib.MSS_NORM_GEMV_MAX_FEATURES
+             and (delta is None or _aligned_matrix(delta, (f, n), torch.bfloat16))
+             and norm_weight.dtype == torch.float32 and tuple(norm_weight.shape) == (f,)
+             and conv_state.dtype == torch.bfloat16 and dim <= w.shape[0] and _gemv_w_ok(w, f, n, h.device))
+    if not fused:
+        hn, x = add_rmsnorm(h, delta, norm_weight, eps, torch.bfloat16)
+        u, rest = gemv_conv_update(w, x, conv_state, weight, bias, activation)
+        return hn, u, rest
+    _require_gpu(h, delta, norm_weight)
+    hn = torch.empty_like(h) if delta is not None else h
+    u = torch.empty(dim, n, dtype=torch.bfloat16, device=h.device)
+    v = torch.empty(w.shape[0], n, dtype=torch.bfloat16, device=h.device)
+    a, keep = _conv_step_args(conv_state, u.t(), weight, bias, activation, u.t())
+    a.x = None
+    nw = norm_weight.contiguous()
+    na = _lib.NormArgs(features=f, tokens=n, eps=float(eps), io_dtype=_lib.MSS_BF16, h=h.data_ptr(),
+                       delta=_ptr(delta), weight=nw.data_ptr(), hn=hn.data_ptr() if delta is not None else None)
+    g = _lib.GemvArgs(M=w.shape[0], K=f, N=n, ldw=w.stride(0), W=w.data_ptr(), X=None, Y=v.data_ptr())
+    lib = _lib.register_hip_kernel()
+    _lib.check(lib.mss_norm_gemv_conv_step(na, g, a, _stream(h)), "mss_norm_gemv_conv_step")
+    return hn, u, v[dim:]
 
 
 def gemv_state_update(w, x, state, u, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=True,

@@ -29,7 +29,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from .decode import causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update, selective_state_update
+from .decode import (causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update, norm_gemv_conv_update,
+                     selective_state_update)
 from .lm_ops import add_rmsnorm
 from .selective_scan_hip import _io_tag, _ptr, _stream, selective_scan_fn
 
@@ -438,12 +439,14 @@ class MambaBlock(nn.Module):
         """One token per row: h (d_model, B) stream; cache {"conv": (B, d_inner, K-1),
         "ssm": (B, d_inner, N)} updated in place (Mamba.step, mamba/mamba1.py:339-363)."""
         weights = weights or _PLAIN
-        h, x = self.norm(h, delta, act_dtype)
         w_xz = weights.stacked(self.in_proj, self.z_proj)
-        if w_xz is not None and w_xz.dtype == x.dtype:
-            # [xin; z] in one GEMM, the conv window step fused on the xin rows
-            u, z = gemv_conv_update(w_xz, x, cache["conv"], self.conv_weight, self.conv_bias)
+        if w_xz is not None and w_xz.dtype == act_dtype == torch.bfloat16:
+            # residual add + norm, then [xin; z] in one GEMM with the conv window step fused
+            # on the xin rows: one kernel
+            h, u, z = norm_gemv_conv_update(h, delta, self.norm.weight, self.norm.eps, w_xz, cache["conv"],
+                                            self.conv_weight, self.conv_bias)
         else:
+            h, x = self.norm(h, delta, act_dtype)
             xin = weights.mm(self.in_proj, x)
             z = weights.mm(self.z_proj, x)
             u = causal_conv1d_update(cache["conv"], xin.t(), self.conv_weight, self.conv_bias).t()

@@ -46,7 +46,8 @@ def test_library_exports_every_header_symbol(lib):
     header = (ROOT / "include" / "mamba_selective_scan.h").read_text()
     version = int(re.search(r"#define MSS_ABI_VERSION (\d+)", header).group(1))
     assert lib.mss_abi_version() == version == _lib.MSS_ABI_VERSION
-    for name in ("MSS_MAX_DSTATE", "MSS_MAX_DSTATE_WIDE", "MSS_SEG_STEPS", "MSS_REF_CHUNK"):
+    for name in ("MSS_MAX_DSTATE", "MSS_MAX_DSTATE_WIDE", "MSS_SEG_STEPS", "MSS_REF_CHUNK",
+                 "MSS_NORM_GEMV_MAX_FEATURES"):
         value = int(re.search(rf"#define {name} (\d+)", header).group(1))
         assert getattr(_lib, name) == value, name
 

@@ -14,8 +14,10 @@ import torch
 import torch.nn.functional as F
 
 from mamba_amd import _lib
+from mamba_amd import decode
 from mamba_amd.decode import (causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update,
-                              selective_state_update)
+                              norm_gemv_conv_update, selective_state_update)
+from mamba_amd.lm_ops import add_rmsnorm
 from mamba_amd.mamba1 import MambaLM
 from oracle import mamba1_torch as ref
 from oracle import cscan64, scan64
@@ -233,6 +235,28 @@ def test_fused_step_validation(lib):
                                   None) == _lib.MSS_ERR_UNSUPPORTED
 
 
+def test_norm_gemv_conv_step_validation(lib):
+    """mss_norm_gemv_conv_step checks the norm against the GEMM and the stream buffers
+    against each other (CPU, invalid arguments only: nothing is launched)."""
+    g = _lib.GemvArgs(M=32, K=64, N=4, ldw=64, W=16, X=None, Y=16)
+    conv = _lib.ConvStepArgs(batch=4, dim=16, width=4, io_dtype=_lib.MSS_BF16, activation=1, conv_state=16,
+                             weight=16, y=16)
+    stream = 64 * 4 * 4  # bytes of the float32 (64, 4) stream
+    norm = dict(features=64, tokens=4, eps=1e-5, io_dtype=_lib.MSS_BF16, h=1 << 20, delta=2 << 20, weight=16,
+                hn=3 << 20)
+    assert lib.mss_norm_gemv_conv_step(None, g, conv, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_norm_gemv_conv_step(_lib.NormArgs(**norm), None, conv, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_norm_gemv_conv_step(_lib.NormArgs(**norm), g, None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    for kw in (dict(features=72), dict(tokens=2), dict(io_dtype=_lib.MSS_F32), dict(eps=-1.0), dict(h=None),
+               dict(weight=None), dict(hn=None), dict(h=(1 << 20) + 8), dict(delta=(2 << 20) + 8),
+               dict(hn=(1 << 20) + stream - 16), dict(hn=(2 << 20) - stream + 16), dict(hn=(2 << 20) + 64)):
+        assert lib.mss_norm_gemv_conv_step(_lib.NormArgs(**dict(norm, **kw)), g, conv, None) == \
+            _lib.MSS_ERR_INVALID_ARGUMENT, kw
+    big = _lib.GemvArgs(M=32, K=1032, N=4, ldw=1032, W=16, X=None, Y=16)
+    assert lib.mss_norm_gemv_conv_step(_lib.NormArgs(**dict(norm, features=1032)), big, conv, None) == \
+        _lib.MSS_ERR_UNSUPPORTED
+
+
 def _bf16(*shape, scale=1.0, device="cuda"):
     return (torch.randn(*shape, device=device) * scale).to(torch.bfloat16)
 
@@ -291,3 +315,55 @@ def test_gemv_state_update_matches_separate_calls(n, zoh, with_dz, dstate):
                               disc)
         assert torch.equal(y, y_ref)
         assert torch.equal(st_fused, st_ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 2, 4, 8])
+@pytest.mark.parametrize("f,with_delta,extra", [(768, True, 1536), (136, True, 40), (1024, False, 8),
+                                                (520, True, 0)])
+def test_norm_gemv_conv_update_matches_separate_calls(monkeypatch, lib, n, f, with_delta, extra):
+    """Residual add + RMSNorm + GEMM + conv window step as one kernel == add_rmsnorm then
+    gemv_conv_update, bit for bit (the new stream hn, the conv output, the rows past the
+    conv's, the window state, rstd), over three steps in a row; f = 768 is the 130M
+    model's d_model (with its 2 x 1536 in/z rows)."""
+    print(f"case norm+gemv+conv N={n} features={f} delta={with_delta} extra={extra}", flush=True)
+    torch.manual_seed(f + n)
+    dim = 96 if extra != 1536 else 1536
+    w = _bf16(dim + extra, f, scale=f ** -0.5)
+    weight = torch.randn(dim, 4, device="cuda") * 0.5
+    bias = torch.randn(dim, device="cuda") * 0.1
+    nw = torch.rand(f, device="cuda") + 0.5
+    s_fused = _bf16(n, dim, 3)
+    s_ref = s_fused.clone()
+    for it in range(3):
+        h = torch.randn(f, n, device="cuda") * 2
+        delta = _bf16(f, n) if with_delta else None
+        hn_ref, x = add_rmsnorm(h, delta, nw, 1e-5, torch.bfloat16)
+        u_ref, rest_ref = gemv_conv_update(w, x, s_ref, weight, bias)
+        with monkeypatch.context() as m:  # the fused kernel, not the fallback's two calls
+            m.setattr(decode, "add_rmsnorm", None)
+            hn, u, rest = norm_gemv_conv_update(h, delta, nw, 1e-5, w, s_fused, weight, bias)
+        assert torch.equal(hn, hn_ref)
+        assert torch.equal(u, u_ref)
+        assert torch.equal(rest, rest_ref)
+        assert torch.equal(s_fused, s_ref)
+        if it == 0:  # rstd through the C entry point, against mss_norm_fwd's
+            rstd_ref = torch.empty(n, device="cuda")
+            xr = torch.empty(f, n, dtype=torch.bfloat16, device="cuda")
+            hn2 = torch.empty_like(h)
+            na = _lib.NormArgs(features=f, tokens=n, eps=1e-5, io_dtype=_lib.MSS_BF16, h=h.data_ptr(),
+                               delta=None if delta is None else delta.data_ptr(), weight=nw.data_ptr(),
+                               hn=hn2.data_ptr(), x=xr.data_ptr(), rstd=rstd_ref.data_ptr())
+            assert lib.mss_norm_fwd(na, None) == _lib.MSS_OK
+            rstd = torch.full((n,), -1.0, device="cuda")
+            st = s_fused.clone()
+            u2 = torch.empty(dim, n, dtype=torch.bfloat16, device="cuda")
+            v2 = torch.empty(dim + extra, n, dtype=torch.bfloat16, device="cuda")
+            ca, keep = decode._conv_step_args(st, u2.t(), weight, bias, "silu", u2.t())
+            ca.x = None
+            na.x, na.rstd, na.hn = None, rstd.data_ptr(), hn2.data_ptr()
+            g = _lib.GemvArgs(M=dim + extra, K=f, N=n, ldw=f, W=w.data_ptr(), X=None, Y=v2.data_ptr())
+            assert lib.mss_norm_gemv_conv_step(na, g, ca, None) == _lib.MSS_OK
+            torch.cuda.synchronize()
+            assert torch.equal(rstd, rstd_ref)
+            assert torch.equal(xr, x)
