@@ -177,6 +177,31 @@ def test_prefill_and_steps_bf16_match_full_forward():
 
 
 @pytest.mark.gpu
+def test_prefill_and_steps_bf16_at_config5_widths():
+    """The bf16 decode path at the 130M model's widths (d_model 768, d_inner 1536, dt_rank
+    48, vocab 50280, batch 8; two of its 24 layers), so the fused norm + in-projection +
+    conv kernel, the x / dt+state / out GEMVs and the 50280-row head run at their real
+    shapes: decode logits against the bf16 full forward over the same tokens, as above."""
+    print("case prefill + steps bf16 at config-5 widths", flush=True)
+    torch.manual_seed(11)
+    model = MambaLM(50280, 768, 2, 2, 16, 48, 4, device="cuda")
+    g = torch.Generator().manual_seed(12)
+    b, prompt, steps = 8, 61, 4
+    tokens = torch.randint(0, 50280, (b, prompt + steps), generator=g).cuda()
+    with torch.no_grad():
+        full = model(tokens, act_dtype=torch.bfloat16).view(b, prompt + steps, -1).float()
+    last, caches = model.prefill(tokens[:, :prompt], act_dtype=torch.bfloat16)
+    scale = full.abs().max().item()
+    assert (last.float() - full[:, prompt - 1]).abs().max().item() <= 3e-2 * scale
+    for t in range(steps):
+        logits = model.step(tokens[:, prompt + t], caches, act_dtype=torch.bfloat16).float()
+        err = (logits - full[:, prompt + t]).abs().max().item()
+        print(f"  step {t}: max abs err {err:.3e} (logit scale {scale:.3e})", flush=True)
+        assert torch.isfinite(logits).all()
+        assert err <= 3e-2 * scale
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("m,k,n", [(3072, 768, 8), (768, 1536, 8), (80, 1536, 8), (1536, 48, 8),
                                    (300, 4096, 4), (5000, 2560, 2), (40, 2056, 8),
                                    (4099, 768, 4), (5, 8, 1), (257, 136, 2)])
