@@ -30,10 +30,12 @@ constexpr int kNormRegs = 48;  // features per thread held in registers (<= 768 
 
 // Forward, features <= kNormW * kNormRegs. Loads take clamped (valid) addresses and the
 // values are masked, with no branch between them, so a batch of loads is in flight at once.
+// Two batches of 24 features (measured on MI355X at 768 features x 16384 tokens: 30-34 us
+// against 42 with three batches of 16 and 45 with one of 48, which reaches 128 VGPRs).
 template <typename io_t, bool kDelta>
 __device__ __forceinline__ float norm_fwd_load(const NormParams& p, const io_t* __restrict__ delta,
                                                int wv, size_t tc, float (&v)[kNormRegs]) {
-  constexpr int kBatch = 16;
+  constexpr int kBatch = 24;
   const size_t T = p.tokens;
   const int F = p.features;
   float ss = 0.f;
