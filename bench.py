@@ -6,10 +6,11 @@ fused scan over the config-2 batch (fp32, B=4, D=1536, L=2048, N=16; softplus(de
 bias), D skip, silu(z) gate, last state), inputs resident in HBM, seeded synthetic data.
 Timing: HIP events recorded on the stream the kernels run on (torch's current stream,
 which the C ABI launches on), W untimed warmup steps, then exactly K timed steps
-bracketed by device synchronisation: replays of one captured HIP graph of the step's three
-launches (the eager rate is reported beside it); per-kernel means come from a separate
-eager run with events between the launches. Prints ONE JSON line on stdout; progress to
-stderr.
+bracketed by device synchronisation, for each way of launching the step's three kernels
+(eager launches; replays of one captured HIP graph) in three trials that alternate which
+goes first; the faster way's median trial is the step time (`launch` names it, both rates
+are reported); per-kernel means come from a separate eager run with events between the
+launches, taken before the timed trials. Prints ONE JSON line on stdout; progress to stderr.
 
 Fields beyond the driver contract:
   roofline      dominant kernel: algorithmic bytes / its average event-timed duration
@@ -168,10 +169,11 @@ def warm_up_device(torch):
 
 
 def run_gpu(torch, cfg, steps, warmup, graph=True):
-    """Times `steps` fwd+bwd steps of the scan at `cfg`. The step rate comes from a timed
-    region holding only the steps (replays of one captured HIP graph of the step's three
-    launches when `graph`, else eager launches); per-kernel means come from a second,
-    eager run with events between the launches (ms)."""
+    """Times `steps` fwd+bwd steps of the scan at `cfg`. The step rate comes from timed
+    regions holding only the steps: eager launches and (when `graph`) replays of one
+    captured HIP graph of the step's three launches, three trials each in alternating order;
+    the faster way's median trial is `ms`. Per-kernel means come from a second, eager run
+    with events between the launches (ms)."""
     from mamba_amd import _lib
 
     lib, t, fa, ba, lens = gpu_step_setup(torch, cfg)
@@ -215,11 +217,9 @@ def run_gpu(torch, cfg, steps, warmup, graph=True):
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps
 
-    eager_ms = timed(lambda: step(sp))
-    ms = eager_ms
-    if graph:
-        ms = timed(g.replay)
-        del g
+    # Per-kernel means first, from eager steps with events between the launches: after graph
+    # replays the next eager steps on the stream run slow for a while (a c2 forward measured
+    # 0.115-0.122 ms instead of 0.101), which would skew them.
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     for i in range(steps):
         step(sp, stream, evs[i])
@@ -227,11 +227,28 @@ def run_gpu(torch, cfg, steps, warmup, graph=True):
     fwd = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     bws = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
     red = float(np.mean([e[2].elapsed_time(e[3]) for e in evs]))
-    log(f"[bench] {cfg.name}: timed {steps} steps: {ms:.4f} ms/step ({'hip graph' if graph else 'eager'}; eager "
-        f"{eager_ms:.4f}); kernels fwd {fwd:.4f}, bwd_scan {bws:.4f}, bwd_reduce {red:.4f} ms")
+
+    trials = {"eager": []}
+    modes = [("eager", lambda: step(sp))]
+    if graph:
+        trials["graph"] = []
+        modes.append(("graph", g.replay))
+    for i in range(3):
+        for name, fn in (modes if i % 2 == 0 else modes[::-1]):
+            trials[name].append(timed(fn))
+    eager_ms = float(np.median(trials["eager"]))
+    graph_ms = float(np.median(trials["graph"])) if graph else None
+    use_graph = graph_ms is not None and graph_ms < eager_ms
+    ms = graph_ms if use_graph else eager_ms
+    if graph:
+        del g
+    log(f"[bench] {cfg.name}: timed {steps} steps x 3 trials per launch mode: {ms:.4f} ms/step "
+        f"({'hip graph' if use_graph else 'eager'}; eager {eager_ms:.4f}, graph {graph_ms}); kernels fwd {fwd:.4f}, "
+        f"bwd_scan {bws:.4f}, bwd_reduce {red:.4f} ms")
     del t
     torch.cuda.empty_cache()
-    return dict(ms=ms, eager_ms=eager_ms, graph=graph, fwd=fwd, bwd_scan=bws, bwd_reduce=red, lens=lens)
+    return dict(ms=ms, eager_ms=eager_ms, graph_ms=graph_ms, graph=use_graph, fwd=fwd, bwd_scan=bws, bwd_reduce=red,
+                lens=lens)
 
 
 def _ref_inputs(torch, b, d, l, n, seed):
@@ -335,6 +352,7 @@ def scan_report(cfg, r):
         "ms_fwd": round(r["fwd"], 5), "ms_bwd": round(r["bwd_scan"] + r["bwd_reduce"], 5),
         "ms_fwd_bwd": round(r["ms"], 5), "tokens_per_s": round(tokens / (r["ms"] * 1e-3), 1),
         "launch": "hip graph" if r["graph"] else "eager", "ms_fwd_bwd_eager": round(r["eager_ms"], 5),
+        "ms_fwd_bwd_graph": None if r.get("graph_ms") is None else round(r["graph_ms"], 5),
         "algorithmic_mb": {"fwd": round(fwd_b / 1e6, 1), "bwd": round(bwd_b / 1e6, 1)},
         "hbm_frac": {"fwd": frac(fwd_b, r["fwd"]), "bwd": frac(bwd_b, r["bwd_scan"] + r["bwd_reduce"]),
                      "fwd_bwd": frac(fwd_b + bwd_b, r["ms"])},
@@ -767,7 +785,9 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
         "ms_per_step_eager": round(r2["eager_ms"], 5),
-        "launch": "hip graph replay of the step's three launches" if r2["graph"] else "eager",
+        "ms_per_step_graph": None if r2.get("graph_ms") is None else round(r2["graph_ms"], 5),
+        "launch": ("hip graph replay of the step's three launches" if r2["graph"] else
+                   "eager launches of the step's three kernels") + " (the faster median of 3 trials each)",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
