@@ -17,10 +17,11 @@ LIB_NAME = "libmamba_selective_scan_hip.so"
 SOURCES = ["mss_fwd.hip", "mss_bwd.hip", "mss_conv.hip", "mss_norm.hip", "mss_xent.hip", "mss_step.hip", "mss_complex.hip", "mss_gemv.hip",
            "mss_capi.cpp"]
 ARCH = os.environ.get("MSS_OFFLOAD_ARCH", "gfx950")
-# Per-source machine-scheduler choice (MI355X, interleaved timings, bit-identical outputs):
-# the backward scan compiled with the ILP-maximising strategy runs 1-4 % faster (c3 backward
-# 912 -> 900 us, c4 3158 -> 3036, a c5 layer 371 -> 361, c2 215 -> 216); the float32
-# forward runs slower with it (c2 102 -> 109 us), so the other sources keep the default.
+# Per-source machine-scheduler choice (MI355X, 11 interleaved trials, bit-identical outputs):
+# the backward scan compiled with the ILP-maximising strategy runs 2-3.5 % faster (c2
+# backward 221.7 -> 216.3 us, c3 924.5 -> 903.5, c4 3172 -> 3062, a c5 layer 364.0 -> 356.7);
+# the float32 forward runs slower with it (c2 102 -> 108 us), so the other sources keep the
+# default.
 SOURCE_FLAGS = {"mss_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 
 
