@@ -14,15 +14,17 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "build"
 LIB_NAME = "libmamba_selective_scan_hip.so"
-SOURCES = ["mss_fwd.hip", "mss_bwd.hip", "mss_conv.hip", "mss_norm.hip", "mss_xent.hip", "mss_step.hip", "mss_complex.hip", "mss_gemv.hip",
+SOURCES = ["mss_fwd.hip", "mss_fwd_bf16.hip", "mss_bwd.hip", "mss_conv.hip", "mss_norm.hip", "mss_xent.hip", "mss_step.hip", "mss_complex.hip", "mss_gemv.hip",
            "mss_capi.cpp"]
 ARCH = os.environ.get("MSS_OFFLOAD_ARCH", "gfx950")
 # Per-source machine-scheduler choice (MI355X, 11 interleaved trials, bit-identical outputs):
-# the backward scan compiled with the ILP-maximising strategy runs 2-3.5 % faster (c2
-# backward 221.7 -> 216.3 us, c3 924.5 -> 903.5, c4 3172 -> 3062, a c5 layer 364.0 -> 356.7);
-# the float32 forward runs slower with it (c2 102 -> 108 us), so the other sources keep the
-# default.
-SOURCE_FLAGS = {"mss_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
+# the backward scan and the bf16-I/O forward compiled with the ILP-maximising strategy run
+# 2-3.5 % faster (c2 backward 221.7 -> 216.3 us, c3 924.5 -> 903.5, c4 3172 -> 3062, a c5
+# layer 364.0 -> 356.7; c3 forward 424.7 -> 416.4, a c5 layer's 165.7 -> 162.9); the float32
+# forward runs slower with it (c2 102 -> 108 us, c4 1345 -> 1411), so it and the other
+# sources keep the default.
+_MAX_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+SOURCE_FLAGS = {"mss_bwd.hip": _MAX_ILP, "mss_fwd_bf16.hip": _MAX_ILP}
 
 
 def hipcc() -> str:
