@@ -54,6 +54,41 @@ __device__ __forceinline__ float pick(const float (&s)[kN], int i) {
   return v;
 }
 
+// Totals over the wave of 8 values per lane (a row's 8 token sums), returned transposed:
+// every lane holds the total of value (lane & 7). Three in-row exchange steps each keep half
+// of a lane's values and add its partner's matching half (partners: the row_half_mirror
+// pair i <-> 7-i of each 8 lanes, then XOR 2, then XOR 1 within quads; each pairs lanes that
+// hold the same set of values), which leaves value 4*bit2 + 2*bit1 + bit0 = lane & 7 in
+// every lane; then the lanes holding the same value are summed: row_ror:8 within the row,
+// a swizzle across rows (XOR 16), a permute across halves (XOR 32). 26 instructions against
+// 8 full-wave sums of 7; a fixed order, so the result is deterministic.
+constexpr int kRowHalfMirror = 0x141, kQuadXor2 = 0x4E, kQuadXor1 = 0xB1, kRowRor8 = 0x128;
+
+__device__ __forceinline__ float wave_sum8(const float (&x)[8]) {
+  const int lane = threadIdx.x & 63;
+  float y[4], z[2];
+  const bool lo4 = (lane & 4) == 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float keep = lo4 ? x[i] : x[i + 4];
+    const float send = lo4 ? x[i + 4] : x[i];
+    y[i] = keep + dpp_mov<kRowHalfMirror, 0xF>(0.f, send);
+  }
+  const bool lo2 = (lane & 2) == 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float keep = lo2 ? y[i] : y[i + 2];
+    const float send = lo2 ? y[i + 2] : y[i];
+    z[i] = keep + dpp_mov<kQuadXor2, 0xF>(0.f, send);
+  }
+  const bool lo1 = (lane & 1) == 0;
+  float v = (lo1 ? z[0] : z[1]) + dpp_mov<kQuadXor1, 0xF>(0.f, lo1 ? z[1] : z[0]);
+  v += dpp_mov<kRowRor8, 0xF>(0.f, v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, v)));
+  return v;
+}
+
 // Offsets into the step operands are int: the entry points reject calls whose operands
 // span 2^31 elements or more.
 //
@@ -396,8 +431,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   for (int r = 0; r < kR; ++r) {
     const int m = m0 + r;
     float s[kN];  // row m's value for each token, rounded to bf16 (uniform over the wave)
+    if constexpr (kN == 8) {
+      const float t = to_f32(f32_to_bf16(wave_sum8(acc[r])));  // token lane & 7
 #pragma unroll
-    for (int c = 0; c < kN; ++c) s[c] = to_f32(f32_to_bf16(wave_sum(acc[r][c])));
+      for (int c = 0; c < kN; ++c) s[c] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), c));
+    } else {
+#pragma unroll
+      for (int c = 0; c < kN; ++c) s[c] = to_f32(f32_to_bf16(wave_sum(acc[r][c])));
+    }
     if (m >= p.M) continue;
     if constexpr (kEpi == 1) {
       if (m < p.cs.dim) {
