@@ -454,9 +454,104 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   }
 }
 
+// Plain decode GEMM of a tall matrix (M >= 4096: the tied head, M = 50280, K = 768) on the
+// matrix cores: each wave computes a 16-row tile Y[r0..r0+15][0..kN-1] with
+// v_mfma_f32_16x16x16_bf16 (bf16 products, float32 sums), token columns kN..15 of the B
+// operand zero. Operand layout of the instruction (lane l, element e of its 4): A[i][k] at
+// l = i + 16 (k / 4), e = k % 4; B[k][j] at l = j + 16 (k / 4), e = k % 4; D[i][j] at
+// l = j + 16 (i / 4), e = i % 4. A permutation of k applied to both A and B leaves the
+// product unchanged, so a lane's 32-byte slice of its row (16 consecutive k; the 4 lanes of
+// a row read one whole 128-byte line) feeds four instructions, 4 values each as k-group
+// l / 16. X is
+// staged in LDS transposed ([kN][K]), so a lane's B operand is 16 contiguous bytes too;
+// lanes of the token columns kN..15, whose outputs are never stored (column j of D depends
+// on column j of B only), read token row j % kN. The first kMfmaPf weight slices are loaded
+// before X is staged.
+// K % 64 == 0; rows past M read row M - 1 and are not stored. The VALU kernel spends most
+// of its time on the 309 M multiply-adds of the head (float32 VALU, no packed forms); here
+// the matrix cores take them and the weight stream sets the pace.
+typedef short mfma_bf16x4 __attribute__((ext_vector_type(4)));
+typedef float mfma_f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kMfmaPf = 4;  // weight slices (64 k, two 16-byte loads each) in flight per lane
+constexpr int kMfmaMaxK = 4096;  // the same X bytes as the VALU kernel stages (<= 64 KB)
+
+__device__ __forceinline__ mfma_bf16x4 bf16x4_of(uint32_t lo, uint32_t hi) {
+  const uint2 v = {lo, hi};
+  return __builtin_bit_cast(mfma_bf16x4, v);
+}
+
+template <int kN>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
+  extern __shared__ u32x4 s_xt[];  // [kN][K] bf16: X transposed
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int K = p.K;
+  const int steps = K / 64;
+  const int r0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (tid >> 6)) * 16);
+  const int g = lane >> 4;  // k-group of the lane
+  const int row = min(r0 + (lane & 15), p.M - 1);
+  const bf16_t* __restrict__ wrow = static_cast<const bf16_t*>(p.W) + static_cast<size_t>(row) * p.ldw + g * 16;
+  u32x4 wq[kMfmaPf][2];
+#pragma unroll
+  for (int j = 0; j < kMfmaPf; ++j) {
+    const bf16_t* src = wrow + min(j, steps - 1) * 64;
+    wq[j][0] = *reinterpret_cast<const u32x4*>(src);
+    wq[j][1] = *reinterpret_cast<const u32x4*>(src + 8);
+  }
+  bf16_t* __restrict__ xt = reinterpret_cast<bf16_t*>(s_xt);
+  const bf16_t* __restrict__ X = static_cast<const bf16_t*>(p.X);
+  for (int kk = tid; kk < K; kk += 256) {
+    float xv[kN];
+    load_xrow<kN>(X + kk * kN, xv);  // X row kk: kN tokens, one 2kN-byte load
+#pragma unroll
+    for (int c = 0; c < kN; ++c) xt[c * K + kk] = f32_to_bf16(xv[c]);  // exact: bf16 values
+  }
+  __syncthreads();
+  if (r0 >= p.M) return;  // after the only barrier
+  const bf16_t* __restrict__ xrow = xt + ((lane & 15) % kN) * K + g * 16;
+  mfma_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < steps; s0 += kMfmaPf) {
+#pragma unroll
+    for (int j = 0; j < kMfmaPf; ++j) {
+      const int s = s0 + j;
+      if (s < steps) {
+        const u32x4 a0 = wq[j][0], a1 = wq[j][1];
+        if (s + kMfmaPf < steps) {
+          const bf16_t* src = wrow + (s + kMfmaPf) * 64;
+          wq[j][0] = *reinterpret_cast<const u32x4*>(src);
+          wq[j][1] = *reinterpret_cast<const u32x4*>(src + 8);
+        }
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(xrow + s * 64);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(xrow + s * 64 + 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bf16x4_of(a0.x, a0.y), bf16x4_of(b0.x, b0.y), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bf16x4_of(a0.z, a0.w), bf16x4_of(b0.z, b0.w), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bf16x4_of(a1.x, a1.y), bf16x4_of(b1.x, b1.y), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bf16x4_of(a1.z, a1.w), bf16x4_of(b1.z, b1.w), acc, 0, 0, 0);
+      }
+    }
+  }
+  const int col = lane & 15;
+  if (col < kN) {
+    bf16_t* __restrict__ Y = static_cast<bf16_t*>(p.Y);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = r0 + 4 * g + e;
+      if (m < p.M) Y[static_cast<size_t>(m) * kN + col] = f32_to_bf16(acc[e]);
+    }
+  }
+}
+
 template <int kN, int kEpi, int kPre>
 static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(p.K) * kN * sizeof(bf16_t);
+  // Tall plain GEMMs on the matrix cores (X transposed and padded to 16 tokens in LDS).
+  if constexpr (kEpi == 0) {
+    if (p.M >= 4096 && p.K % 64 == 0 && p.K <= kMfmaMaxK && !p.norm) {
+      const size_t lds_t = static_cast<size_t>(p.K) * kN * sizeof(bf16_t);
+      hipLaunchKernelGGL((gemv_mfma_kernel<kN>), dim3((p.M + 63) / 64), dim3(256), lds_t, stream, p);
+      return hipGetLastError();
+    }
+  }
   // 4 rows per wave (X staged once per 16 rows) when that still gives >= 256 workgroups.
   if constexpr (kEpi == 0) {
     if (p.M >= 4096) {
