@@ -122,13 +122,9 @@ __device__ __forceinline__ void load_conv(const ConvStepParams& p, int m, int la
 // Conv-window step of channel m for token `lane` on x (rounded to bf16): the arithmetic
 // of conv_step_kernel (mss_step.hip): pre = bias + sum_k w[k] window[k] over
 // window = [state, x], y = act(pre), the state shifts left and takes x.
-template <int kN>
-__device__ __forceinline__ void conv_epilogue(const ConvStepParams& p, int m, const float (&s)[kN], int lane,
-                                              const ConvOperands& o) {
-  if (lane >= kN) return;
+__device__ __forceinline__ void conv_step_core(const ConvStepParams& p, int m, int b, float x, const ConvOperands& o) {
   const int K = p.width;
-  bf16_t* cache = static_cast<bf16_t*>(p.state) + (lane * p.dim + m) * (K - 1);
-  const float x = pick<kN>(s, lane);
+  bf16_t* cache = static_cast<bf16_t*>(p.state) + (b * p.dim + m) * (K - 1);
   float pre = o.bias;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
@@ -140,7 +136,14 @@ __device__ __forceinline__ void conv_epilogue(const ConvStepParams& p, int m, co
   pre = __builtin_fmaf(pick<4>(o.w, K - 1), x, pre);
   if (K > 1) cache[K - 2] = f32_to_bf16(x);
   const float y = p.act ? pre * sigmoid(pre) : pre;
-  static_cast<bf16_t*>(p.y)[lane * static_cast<int>(p.sb) + m * static_cast<int>(p.sd)] = f32_to_bf16(y);
+  static_cast<bf16_t*>(p.y)[b * static_cast<int>(p.sb) + m * static_cast<int>(p.sd)] = f32_to_bf16(y);
+}
+
+template <int kN>
+__device__ __forceinline__ void conv_epilogue(const ConvStepParams& p, int m, const float (&s)[kN], int lane,
+                                              const ConvOperands& o) {
+  if (lane >= kN) return;
+  conv_step_core(p, m, lane, pick<kN>(s, lane), o);
 }
 
 // Selective-state step of channel d: lanes are (token, state) pairs, 16 lanes (one DPP
@@ -280,7 +283,7 @@ __device__ __forceinline__ void store_xrow(bf16_t* x, const float (&v)[kN]) {
 // order; x = (hn * rstd) * w rounded to bf16), so X equals that kernel's output bit for
 // bit. Every workgroup computes X (a few KB from the L2); workgroup 0 also stores hn and
 // rstd. The stream loads are issued before any use, behind the weights already in flight.
-template <int kN>
+template <int kN, bool kTransposed = false>
 __device__ __forceinline__ void norm_prologue(const NormParams& q, int K, bf16_t* X, float (*s_ss)[4]) {
   const int tid = threadIdx.x;
   const bf16_t* __restrict__ delta = static_cast<const bf16_t*>(q.delta);
@@ -331,7 +334,12 @@ __device__ __forceinline__ void norm_prologue(const NormParams& q, int K, bf16_t
       float x[kN];
 #pragma unroll
       for (int c = 0; c < kN; ++c) x[c] = v[j][c] * r[c] * w[j];
-      store_xrow<kN>(X + f * kN, x);
+      if constexpr (kTransposed) {
+#pragma unroll
+        for (int c = 0; c < kN; ++c) X[c * K + f] = f32_to_bf16(x[c]);  // [kN][K]
+      } else {
+        store_xrow<kN>(X + f * kN, x);
+      }
     }
   }
   if (first && q.rstd && tid == 0) {
@@ -480,43 +488,68 @@ __device__ __forceinline__ mfma_bf16x4 bf16x4_of(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(mfma_bf16x4, v);
 }
 
-template <int kN>
+// kEpi 1: the conv-window step on rows [0, cs.dim) (each lane: its token column, four rows),
+// operands loaded before the X barrier; kNorm: X is the norm prologue's, stored transposed.
+// kSplit 1: each wave owns a 16-row tile (4 tiles per workgroup); kSplit 4: the workgroup's
+// 4 waves share one tile, each taking a quarter of the K steps, and the partial tiles are
+// added in wave order through LDS (more, shorter workgroups for the in-projection's 3072
+// rows).
+template <int kN, int kEpi, bool kNorm, int kSplit>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
+  static_assert(kEpi == 0 || kEpi == 1, "plain store or conv-window step");
+  static_assert(kSplit == 1 || kSplit == 4, "one tile per wave or one per workgroup");
   extern __shared__ u32x4 s_xt[];  // [kN][K] bf16: X transposed
+  __shared__ float s_ss[kNorm ? kN : 1][4];
+  __shared__ mfma_f32x4 s_acc[kSplit > 1 ? kSplit : 1][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = p.K;
   const int steps = K / 64;
-  const int r0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (tid >> 6)) * 16);
+  // the wave's tile and its range of K steps [s_lo, s_hi)
+  const int r0 = kSplit == 1 ? (blockIdx.x * 4 + wv) * 16 : blockIdx.x * 16;
+  const int per = (steps + kSplit - 1) / kSplit;
+  const int s_lo = kSplit == 1 ? 0 : min(wv * per, steps);
+  const int s_hi = kSplit == 1 ? steps : min(s_lo + per, steps);
   const int g = lane >> 4;  // k-group of the lane
   const int row = min(r0 + (lane & 15), p.M - 1);
   const bf16_t* __restrict__ wrow = static_cast<const bf16_t*>(p.W) + static_cast<size_t>(row) * p.ldw + g * 16;
   u32x4 wq[kMfmaPf][2];
 #pragma unroll
-  for (int j = 0; j < kMfmaPf; ++j) {
-    const bf16_t* src = wrow + min(j, steps - 1) * 64;
+  for (int j = 0; j < kMfmaPf; ++j) {  // steps past the range re-read the row's last slice
+    const bf16_t* src = wrow + min(s_lo + j, steps - 1) * 64;
     wq[j][0] = *reinterpret_cast<const u32x4*>(src);
     wq[j][1] = *reinterpret_cast<const u32x4*>(src + 8);
   }
-  bf16_t* __restrict__ xt = reinterpret_cast<bf16_t*>(s_xt);
-  const bf16_t* __restrict__ X = static_cast<const bf16_t*>(p.X);
-  for (int kk = tid; kk < K; kk += 256) {
-    float xv[kN];
-    load_xrow<kN>(X + kk * kN, xv);  // X row kk: kN tokens, one 2kN-byte load
+  const int col = lane & 15;  // the lane's token column of D
+  ConvOperands co[4];
+  if constexpr (kEpi == 1) {
 #pragma unroll
-    for (int c = 0; c < kN; ++c) xt[c * K + kk] = f32_to_bf16(xv[c]);  // exact: bf16 values
+    for (int e = 0; e < 4; ++e) load_conv(p.cs, min(r0 + 4 * g + e, p.M - 1), col, kN, co[e]);
+  }
+  bf16_t* __restrict__ xt = reinterpret_cast<bf16_t*>(s_xt);
+  if constexpr (kNorm) {
+    norm_prologue<kN, true>(p.nm, K, xt, s_ss);
+  } else {
+    const bf16_t* __restrict__ X = static_cast<const bf16_t*>(p.X);
+    for (int kk = tid; kk < K; kk += 256) {
+      float xv[kN];
+      load_xrow<kN>(X + kk * kN, xv);  // X row kk: kN tokens, one 2kN-byte load
+#pragma unroll
+      for (int c = 0; c < kN; ++c) xt[c * K + kk] = f32_to_bf16(xv[c]);  // exact: bf16 values
+    }
   }
   __syncthreads();
-  if (r0 >= p.M) return;  // after the only barrier
+  if (r0 >= p.M) return;  // after the last barrier every wave of a kSplit tile shares
   const bf16_t* __restrict__ xrow = xt + ((lane & 15) % kN) * K + g * 16;
   mfma_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < steps; s0 += kMfmaPf) {
+  for (int s0 = s_lo; s0 < s_hi; s0 += kMfmaPf) {
 #pragma unroll
     for (int j = 0; j < kMfmaPf; ++j) {
       const int s = s0 + j;
-      if (s < steps) {
+      if (s < s_hi) {
         const u32x4 a0 = wq[j][0], a1 = wq[j][1];
-        if (s + kMfmaPf < steps) {
+        if (s + kMfmaPf < s_hi) {
           const bf16_t* src = wrow + (s + kMfmaPf) * 64;
           wq[j][0] = *reinterpret_cast<const u32x4*>(src);
           wq[j][1] = *reinterpret_cast<const u32x4*>(src + 8);
@@ -530,13 +563,27 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
       }
     }
   }
-  const int col = lane & 15;
+  if constexpr (kSplit > 1) {
+    s_acc[wv][lane] = acc;
+    __syncthreads();
+    if (wv != 0) return;
+    acc = s_acc[0][lane];
+#pragma unroll
+    for (int w = 1; w < kSplit; ++w) acc += s_acc[w][lane];
+  }
   if (col < kN) {
     bf16_t* __restrict__ Y = static_cast<bf16_t*>(p.Y);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int m = r0 + 4 * g + e;
-      if (m < p.M) Y[static_cast<size_t>(m) * kN + col] = f32_to_bf16(acc[e]);
+      if (m >= p.M) continue;
+      if constexpr (kEpi == 1) {
+        if (m < p.cs.dim) {  // rounded to bf16 first, as the separate step would read it
+          conv_step_core(p.cs, m, col, to_f32(f32_to_bf16(acc[e])), co[e]);
+          continue;
+        }
+      }
+      Y[static_cast<size_t>(m) * kN + col] = f32_to_bf16(acc[e]);
     }
   }
 }
@@ -544,11 +591,20 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
 template <int kN, int kEpi, int kPre>
 static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(p.K) * kN * sizeof(bf16_t);
-  // Tall plain GEMMs on the matrix cores (X transposed and padded to 16 tokens in LDS).
-  if constexpr (kEpi == 0) {
-    if (p.M >= 4096 && p.K % 64 == 0 && p.K <= kMfmaMaxK && !p.norm) {
-      const size_t lds_t = static_cast<size_t>(p.K) * kN * sizeof(bf16_t);
-      hipLaunchKernelGGL((gemv_mfma_kernel<kN>), dim3((p.M + 63) / 64), dim3(256), lds_t, stream, p);
+  // On the matrix cores (X transposed in LDS, K % 64 == 0): tall plain GEMMs, and every
+  // in-projection with the conv-window step fused (with or without the norm prologue, so
+  // the two fused entry points give the same bits).
+  if constexpr (kEpi == 0 || kEpi == 1) {
+    const bool mfma = p.K % 64 == 0 && p.K <= kMfmaMaxK && (kEpi == 1 || (p.M >= 4096 && !p.norm));
+    if (mfma) {
+      if (p.norm && p.K > kNormGemvMaxFeatures) return hipErrorInvalidValue;
+      constexpr int kSplit = kEpi == 1 ? 4 : 1;
+      const dim3 grid(kSplit == 1 ? (p.M + 63) / 64 : (p.M + 15) / 16);
+      if (p.norm) {
+        hipLaunchKernelGGL((gemv_mfma_kernel<kN, kEpi, true, kSplit>), grid, dim3(256), lds, stream, p);
+      } else {
+        hipLaunchKernelGGL((gemv_mfma_kernel<kN, kEpi, false, kSplit>), grid, dim3(256), lds, stream, p);
+      }
       return hipGetLastError();
     }
   }
