@@ -481,6 +481,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 typedef short mfma_bf16x4 __attribute__((ext_vector_type(4)));
 typedef float mfma_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMfmaPf = 4;  // weight slices (64 k, two 16-byte loads each) in flight per lane
+// Plain GEMMs take the matrix cores from this many rows (the 768-row out-projection of the
+// 130M decode step with K split 4 ways on them: 0.616 ms per token step against 0.571 on the
+// VALU kernel, its 48 workgroups too few).
+#ifndef MSS_MFMA_MIN_M
+#define MSS_MFMA_MIN_M 4096
+#endif
 constexpr int kMfmaMaxK = 4096;  // the same X bytes as the VALU kernel stages (<= 64 KB)
 
 __device__ __forceinline__ mfma_bf16x4 bf16x4_of(uint32_t lo, uint32_t hi) {
@@ -595,15 +601,15 @@ static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
   // in-projection with the conv-window step fused (with or without the norm prologue, so
   // the two fused entry points give the same bits).
   if constexpr (kEpi == 0 || kEpi == 1) {
-    const bool mfma = p.K % 64 == 0 && p.K <= kMfmaMaxK && (kEpi == 1 || (p.M >= 4096 && !p.norm));
+    const bool mfma = p.K % 64 == 0 && p.K <= kMfmaMaxK && (kEpi == 1 || (p.M >= MSS_MFMA_MIN_M && !p.norm));
     if (mfma) {
       if (p.norm && p.K > kNormGemvMaxFeatures) return hipErrorInvalidValue;
-      constexpr int kSplit = kEpi == 1 ? 4 : 1;
-      const dim3 grid(kSplit == 1 ? (p.M + 63) / 64 : (p.M + 15) / 16);
-      if (p.norm) {
-        hipLaunchKernelGGL((gemv_mfma_kernel<kN, kEpi, true, kSplit>), grid, dim3(256), lds, stream, p);
+      if (kEpi == 0 && p.M >= 4096) {
+        hipLaunchKernelGGL((gemv_mfma_kernel<kN, kEpi, false, 1>), dim3((p.M + 63) / 64), dim3(256), lds, stream, p);
+      } else if (p.norm) {
+        hipLaunchKernelGGL((gemv_mfma_kernel<kN, kEpi, true, 4>), dim3((p.M + 15) / 16), dim3(256), lds, stream, p);
       } else {
-        hipLaunchKernelGGL((gemv_mfma_kernel<kN, kEpi, false, kSplit>), grid, dim3(256), lds, stream, p);
+        hipLaunchKernelGGL((gemv_mfma_kernel<kN, kEpi, false, 4>), dim3((p.M + 15) / 16), dim3(256), lds, stream, p);
       }
       return hipGetLastError();
     }
