@@ -356,16 +356,22 @@ __device__ __forceinline__ void norm_prologue(const NormParams& q, int K, bf16_t
 // M - 1 for the reads and never stored. The row's sums are rounded to bf16 before the
 // epilogue (kEpi, as GemvParams::epi), so a fused epilogue sees the values the separate
 // step kernel would read back from Y. kNorm: X is the norm prologue's (norm_prologue).
-template <int kN, int kR, int kEpi, int kPre, bool kNorm>
+// kS 4 (plain GEMMs with one row per wave only): the workgroup's 4 waves share a row, wave
+// ws taking the 512-element K steps ws, ws + 4, ..; their per-token totals are added
+// through LDS in wave order, so launches of few rows fill more of the chip.
+template <int kN, int kR, int kEpi, int kPre, bool kNorm, int kS = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   static_assert(kEpi == 0 || kR == 1, "fused epilogues take one row per wave");
+  static_assert(kS == 1 || (kS == 4 && kR == 1 && kEpi == 0 && !kNorm), "K split: plain GEMMs, one row");
   extern __shared__ u32x4 s_x[];
   __shared__ float s_ss[kNorm ? kN : 1][4];
+  __shared__ float s_red[kS > 1 ? kS : 1][kN];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  const int ws = kS > 1 ? tid >> 6 : 0;  // this wave's share of the K steps
   // wave-uniform row index in a scalar register (the per-channel operands then come
   // through scalar loads)
-  const int m0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (tid >> 6)) * kR);
+  const int m0 = __builtin_amdgcn_readfirstlane(kS > 1 ? blockIdx.x : (blockIdx.x * 4 + (tid >> 6)) * kR);
   const bool wave_on = m0 < p.M;
   const int mc = min(m0, p.M - 1);  // rows past M read row M - 1 (no branch around loads)
   const bf16_t* __restrict__ W = static_cast<const bf16_t*>(p.W);
@@ -376,7 +382,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   if constexpr (kEpi == 2) load_ssm<kN>(p.ss, mc, lane, so);
 #pragma unroll
   for (int st = 0; st < kPre; ++st) {
-    const int k0 = lane * 8 + 512 * st;
+    const int k0 = lane * 8 + 512 * (st * kS + ws);
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
       const int m = min(mc + r, p.M - 1);
@@ -392,7 +398,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     for (int i = tid; i < n_q; i += 256) s_x[i] = xg[i];
   }
   __syncthreads();
-  if (!wave_on) return;  // after the only barrier
+  if constexpr (kS == 1) {
+    if (!wave_on) return;  // after the only barrier
+  }
   const bf16_t* X = reinterpret_cast<const bf16_t*>(s_x);
   float acc[kR][kN];
 #pragma unroll
@@ -422,19 +430,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   };
 #pragma unroll
   for (int st = 0; st < kPre; ++st) {
-    const int k0 = lane * 8 + 512 * st;
+    const int k0 = lane * 8 + 512 * (st * kS + ws);
     if (k0 < p.K) step(k0, wq[st]);
   }
-  for (int k0 = lane * 8 + 512 * kPre; k0 < p.K; k0 += 512) {
+  for (int k0 = lane * 8 + 512 * (kPre * kS + ws); k0 < p.K; k0 += 512 * kS) {
     u32x4 q[kR];
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
-      const int m = min(m0 + r, p.M - 1);
+      const int m = min(mc + r, p.M - 1);
       q[r] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + k0);
     }
     step(k0, q);
   }
   bf16_t* __restrict__ Y = static_cast<bf16_t*>(p.Y);
+  if constexpr (kS > 1) {
+    float t;  // this wave's partial total of token lane (lanes < kN)
+    if constexpr (kN == 8) {
+      t = wave_sum8(acc[0]);  // token lane & 7
+    } else {
+      float s[kN];
+#pragma unroll
+      for (int c = 0; c < kN; ++c) s[c] = wave_sum(acc[0][c]);
+      t = pick<kN>(s, lane);
+    }
+    if (lane < kN) s_red[ws][lane] = t;
+    __syncthreads();
+    if (ws != 0 || lane >= kN) return;
+    float v = s_red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kS; ++w) v += s_red[w][lane];
+    Y[static_cast<size_t>(m0) * kN + lane] = f32_to_bf16(v);
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     const int m = m0 + r;
@@ -594,6 +621,26 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
   }
 }
 
+// Plain GEMMs of at most this many rows (and K > 512) split K over the workgroup's 4 waves,
+// one row per workgroup: the 130M decode step's x projection (80 rows, K 1536; 20
+// workgroups unsplit) and out-projection (768 rows; 192) take it, 0.571 -> 0.534 ms per
+// token step on MI355X (0.544 with the out-projection split 2 ways, 2 rows per workgroup).
+#ifndef MSS_GEMV_SPLIT_MAX_M
+#define MSS_GEMV_SPLIT_MAX_M 1024
+#endif
+
+template <int kN, int kS>
+static hipError_t launch_gemv_split(const GemvParams& p, int steps, size_t lds, hipStream_t stream) {
+  const dim3 grid(p.M);
+  switch (min((steps + kS - 1) / kS, 4)) {  // K steps each wave loads before the X barrier
+    case 1: hipLaunchKernelGGL((gemv_kernel<kN, 1, 0, 1, false, kS>), grid, dim3(256), lds, stream, p); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<kN, 1, 0, 2, false, kS>), grid, dim3(256), lds, stream, p); break;
+    case 3: hipLaunchKernelGGL((gemv_kernel<kN, 1, 0, 3, false, kS>), grid, dim3(256), lds, stream, p); break;
+    default: hipLaunchKernelGGL((gemv_kernel<kN, 1, 0, 4, false, kS>), grid, dim3(256), lds, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
 template <int kN, int kEpi, int kPre>
 static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(p.K) * kN * sizeof(bf16_t);
@@ -634,6 +681,10 @@ static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
     }
   }
   if (p.norm) return hipErrorInvalidValue;
+  if constexpr (kEpi == 0) {
+    const int steps = (p.K + 511) / 512;
+    if (steps >= 2 && p.M <= MSS_GEMV_SPLIT_MAX_M) return launch_gemv_split<kN, 4>(p, steps, lds, stream);
+  }
   hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi, kPre, false>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
   return hipGetLastError();
 }

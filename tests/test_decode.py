@@ -205,7 +205,8 @@ def test_prefill_and_steps_bf16_at_config5_widths():
 @pytest.mark.parametrize("m,k,n", [(3072, 768, 8), (768, 1536, 8), (80, 1536, 8), (1536, 48, 8),
                                    (300, 4096, 4), (5000, 2560, 2), (40, 2056, 8),
                                    (4099, 768, 4), (5, 8, 1), (257, 136, 2), (4100, 768, 8),
-                                   (50280, 768, 8), (4096, 64, 1)])
+                                   (50280, 768, 8), (4096, 64, 1),
+                                   (64, 1024, 1), (200, 1600, 2), (1023, 2048, 4)])
 def test_gemv_matches_float32_product(m, k, n):
     """The decode-shaped GEMM against the float32 product of the same bf16 operands: each
     output is one float32 sum over K rounded to bf16 once, so it sits within a bf16
