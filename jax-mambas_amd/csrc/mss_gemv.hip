@@ -357,8 +357,9 @@ __device__ __forceinline__ void norm_prologue(const NormParams& q, int K, bf16_t
 // epilogue (kEpi, as GemvParams::epi), so a fused epilogue sees the values the separate
 // step kernel would read back from Y. kNorm: X is the norm prologue's (norm_prologue).
 // kS 4 (plain GEMMs with one row per wave only): the workgroup's 4 waves share a row, wave
-// ws taking the 512-element K steps ws, ws + 4, ..; their per-token totals are added
-// through LDS in wave order, so launches of few rows fill more of the chip.
+// ws taking the 512-element K steps ws, ws + 4, .. (their X rows read straight into
+// registers); their per-token totals are added through LDS in wave order, so launches of
+// few rows fill more of the chip.
 template <int kN, int kR, int kEpi, int kPre, bool kNorm, int kS = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   static_assert(kEpi == 0 || kR == 1, "fused epilogues take one row per wave");
@@ -390,59 +391,102 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
       wq[st][r] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + (k0 < p.K ? k0 : 0));
     }
   }
-  if constexpr (kNorm) {
-    norm_prologue<kN>(p.nm, p.K, reinterpret_cast<bf16_t*>(s_x), s_ss);
+  // K split over the waves (kRegX): each lane reads only its own K slices of X (8 k x kN
+  // tokens = kN 16-byte words per step), straight from global memory into registers, issued
+  // with the weight slices: no LDS stage and no barrier before the products (130M decode
+  // step: 0.533 -> 0.500 ms). Otherwise X is staged once per workgroup in LDS (reading it
+  // into registers there too, with one row per wave, measured 0.513 ms).
+  constexpr bool kRegX = kS > 1;
+  const u32x4* __restrict__ xg = static_cast<const u32x4*>(p.X);
+  u32x4 xq[kRegX ? kPre : 1][kN];
+  if constexpr (kRegX) {
+#pragma unroll
+    for (int st = 0; st < kPre; ++st) {
+      const int k0 = lane * 8 + 512 * (st * kS + ws);
+      const int kk = k0 < p.K ? k0 : 0;  // steps past K re-read the first slice (unused)
+#pragma unroll
+      for (int j = 0; j < kN; ++j) xq[st][j] = xg[kk * kN / 8 + j];
+    }
   } else {
-    const int n_q = p.K * kN / 8;  // 16-byte words of X (K % 8 == 0)
-    const u32x4* __restrict__ xg = static_cast<const u32x4*>(p.X);
-    for (int i = tid; i < n_q; i += 256) s_x[i] = xg[i];
+    if constexpr (kNorm) {
+      norm_prologue<kN>(p.nm, p.K, reinterpret_cast<bf16_t*>(s_x), s_ss);
+    } else {
+      const int n_q = p.K * kN / 8;  // 16-byte words of X (K % 8 == 0)
+      for (int i = tid; i < n_q; i += 256) s_x[i] = xg[i];
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if constexpr (kS == 1) {
-    if (!wave_on) return;  // after the only barrier
-  }
+  if (!wave_on) return;  // (kS > 1: every wave has a row; its later barrier is reached by all)
   const bf16_t* X = reinterpret_cast<const bf16_t*>(s_x);
   float acc[kR][kN];
 #pragma unroll
   for (int r = 0; r < kR; ++r)
 #pragma unroll
     for (int c = 0; c < kN; ++c) acc[r][c] = 0.f;
-  auto step = [&](int k0, const u32x4 (&q)[kR]) {
-    float w[kR][8];
+  if constexpr (kRegX) {
+    // products of one step from registers: weight slice q, X words x
+    auto reg_step = [&](const u32x4& q, const u32x4 (&x)[kN]) {
+      const uint32_t a[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int r = 0; r < kR; ++r) {
-      const uint32_t a[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+      for (int e = 0; e < 8; ++e) {
+        const float w = e & 1 ? __uint_as_float(a[e / 2] & 0xffff0000u) : __uint_as_float(a[e / 2] << 16);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        w[r][2 * i] = __uint_as_float(a[i] << 16);
-        w[r][2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+        for (int c = 0; c < kN; ++c) {
+          const int i = e * kN + c;  // bf16 element i of the step's kN words
+          const uint32_t v[4] = {x[i / 8].x, x[i / 8].y, x[i / 8].z, x[i / 8].w};
+          const float xv = i & 1 ? __uint_as_float(v[(i % 8) / 2] & 0xffff0000u) : __uint_as_float(v[(i % 8) / 2] << 16);
+          acc[0][c] = __builtin_fmaf(w, xv, acc[0][c]);
+        }
       }
+    };
+#pragma unroll
+    for (int st = 0; st < kPre; ++st) {
+      if (lane * 8 + 512 * (st * kS + ws) < p.K) reg_step(wq[st][0], xq[st]);
     }
+    for (int k0 = lane * 8 + 512 * (kPre * kS + ws); k0 < p.K; k0 += 512 * kS) {
+      const u32x4 q = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(mc) * p.ldw + k0);
+      u32x4 x[kN];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x[kN];
-      load_xrow<kN>(X + (k0 + e) * kN, x);
-#pragma unroll
-      for (int r = 0; r < kR; ++r)
-#pragma unroll
-        for (int c = 0; c < kN; ++c) acc[r][c] = __builtin_fmaf(w[r][e], x[c], acc[r][c]);
+      for (int j = 0; j < kN; ++j) x[j] = xg[k0 * kN / 8 + j];
+      reg_step(q, x);
     }
-  };
+  } else {
+    auto step = [&](int k0, const u32x4 (&q)[kR]) {
+      float w[kR][8];
 #pragma unroll
-  for (int st = 0; st < kPre; ++st) {
-    const int k0 = lane * 8 + 512 * (st * kS + ws);
-    if (k0 < p.K) step(k0, wq[st]);
+      for (int r = 0; r < kR; ++r) {
+        const uint32_t a[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w[r][2 * i] = __uint_as_float(a[i] << 16);
+          w[r][2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float x[kN];
+        load_xrow<kN>(X + (k0 + e) * kN, x);
+#pragma unroll
+        for (int r = 0; r < kR; ++r)
+#pragma unroll
+          for (int c = 0; c < kN; ++c) acc[r][c] = __builtin_fmaf(w[r][e], x[c], acc[r][c]);
+      }
+    };
+#pragma unroll
+    for (int st = 0; st < kPre; ++st) {
+      const int k0 = lane * 8 + 512 * st;
+      if (k0 < p.K) step(k0, wq[st]);
+    }
+    for (int k0 = lane * 8 + 512 * kPre; k0 < p.K; k0 += 512) {
+      u32x4 q[kR];
+#pragma unroll
+      for (int r = 0; r < kR; ++r) {
+        const int m = min(mc + r, p.M - 1);
+        q[r] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + k0);
+      }
+      step(k0, q);
+    }
   }
-  for (int k0 = lane * 8 + 512 * (kPre * kS + ws); k0 < p.K; k0 += 512 * kS) {
-    u32x4 q[kR];
-#pragma unroll
-    for (int r = 0; r < kR; ++r) {
-      const int m = min(mc + r, p.M - 1);
-      q[r] = *reinterpret_cast<const u32x4*>(W + static_cast<size_t>(m) * p.ldw + k0);
-    }
-    step(k0, q);
-  }
-  bf16_t* __restrict__ Y = static_cast<bf16_t*>(p.Y);
   if constexpr (kS > 1) {
     float t;  // this wave's partial total of token lane (lanes < kN)
     if constexpr (kN == 8) {
@@ -459,9 +503,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     float v = s_red[0][lane];
 #pragma unroll
     for (int w = 1; w < kS; ++w) v += s_red[w][lane];
-    Y[static_cast<size_t>(m0) * kN + lane] = f32_to_bf16(v);
+    static_cast<bf16_t*>(p.Y)[static_cast<size_t>(m0) * kN + lane] = f32_to_bf16(v);
     return;
   }
+  bf16_t* __restrict__ Y = static_cast<bf16_t*>(p.Y);
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     const int m = m0 + r;
@@ -624,14 +669,16 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
 // Plain GEMMs of at most this many rows (and K > 512) split K over the workgroup's 4 waves,
 // one row per workgroup: the 130M decode step's x projection (80 rows, K 1536; 20
 // workgroups unsplit) and out-projection (768 rows; 192) take it, 0.571 -> 0.534 ms per
-// token step on MI355X (0.544 with the out-projection split 2 ways, 2 rows per workgroup).
+// token step on MI355X with X staged in LDS (0.544 with the out-projection split 2 ways, 2
+// rows per workgroup), 0.500 with X read into registers.
 #ifndef MSS_GEMV_SPLIT_MAX_M
 #define MSS_GEMV_SPLIT_MAX_M 1024
 #endif
 
 template <int kN, int kS>
-static hipError_t launch_gemv_split(const GemvParams& p, int steps, size_t lds, hipStream_t stream) {
+static hipError_t launch_gemv_split(const GemvParams& p, int steps, hipStream_t stream) {
   const dim3 grid(p.M);
+  const size_t lds = 0;  // X is read into registers
   switch (min((steps + kS - 1) / kS, 4)) {  // K steps each wave loads before the X barrier
     case 1: hipLaunchKernelGGL((gemv_kernel<kN, 1, 0, 1, false, kS>), grid, dim3(256), lds, stream, p); break;
     case 2: hipLaunchKernelGGL((gemv_kernel<kN, 1, 0, 2, false, kS>), grid, dim3(256), lds, stream, p); break;
@@ -683,7 +730,7 @@ static hipError_t launch_gemv_p(const GemvParams& p, hipStream_t stream) {
   if (p.norm) return hipErrorInvalidValue;
   if constexpr (kEpi == 0) {
     const int steps = (p.K + 511) / 512;
-    if (steps >= 2 && p.M <= MSS_GEMV_SPLIT_MAX_M) return launch_gemv_split<kN, 4>(p, steps, lds, stream);
+    if (steps >= 2 && steps <= 16 && p.M <= MSS_GEMV_SPLIT_MAX_M) return launch_gemv_split<kN, 4>(p, steps, stream);
   }
   hipLaunchKernelGGL((gemv_kernel<kN, 1, kEpi, kPre, false>), dim3((p.M + 3) / 4), dim3(256), lds, stream, p);
   return hipGetLastError();
