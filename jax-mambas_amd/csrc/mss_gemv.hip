@@ -553,6 +553,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 typedef short mfma_bf16x4 __attribute__((ext_vector_type(4)));
 typedef float mfma_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMfmaPf = 4;  // weight slices (64 k, two 16-byte loads each) in flight per lane
+// the same for the one-tile-per-wave tall GEMMs (the tied head: 6 or all 12 slices of
+// K = 768 in flight measured 0.504 / 0.505 ms per 130M decode step against 0.503 with 4)
+#ifndef MSS_MFMA_PF_TALL
+#define MSS_MFMA_PF_TALL 4
+#endif
 // Plain GEMMs take the matrix cores from this many rows (the 768-row out-projection of the
 // 130M decode step with K split 4 ways on them: 0.616 ms per token step against 0.571 on the
 // VALU kernel, its 48 workgroups too few).
@@ -574,6 +579,7 @@ __device__ __forceinline__ mfma_bf16x4 bf16x4_of(uint32_t lo, uint32_t hi) {
 // rows).
 template <int kN, int kEpi, bool kNorm, int kSplit>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
+  constexpr int kPf = kSplit == 1 ? MSS_MFMA_PF_TALL : kMfmaPf;
   static_assert(kEpi == 0 || kEpi == 1, "plain store or conv-window step");
   static_assert(kSplit == 1 || kSplit == 4, "one tile per wave or one per workgroup");
   extern __shared__ u32x4 s_xt[];  // [kN][K] bf16: X transposed
@@ -592,9 +598,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
   const int g = lane >> 4;  // k-group of the lane
   const int row = min(r0 + (lane & 15), p.M - 1);
   const bf16_t* __restrict__ wrow = static_cast<const bf16_t*>(p.W) + static_cast<size_t>(row) * p.ldw + g * 16;
-  u32x4 wq[kMfmaPf][2];
+  u32x4 wq[kPf][2];
 #pragma unroll
-  for (int j = 0; j < kMfmaPf; ++j) {  // steps past the range re-read the row's last slice
+  for (int j = 0; j < kPf; ++j) {  // steps past the range re-read the row's last slice
     const bf16_t* src = wrow + min(s_lo + j, steps - 1) * 64;
     wq[j][0] = *reinterpret_cast<const u32x4*>(src);
     wq[j][1] = *reinterpret_cast<const u32x4*>(src + 8);
@@ -621,14 +627,14 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvParams p) {
   if (r0 >= p.M) return;  // after the last barrier every wave of a kSplit tile shares
   const bf16_t* __restrict__ xrow = xt + ((lane & 15) % kN) * K + g * 16;
   mfma_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = s_lo; s0 < s_hi; s0 += kMfmaPf) {
+  for (int s0 = s_lo; s0 < s_hi; s0 += kPf) {
 #pragma unroll
-    for (int j = 0; j < kMfmaPf; ++j) {
+    for (int j = 0; j < kPf; ++j) {
       const int s = s0 + j;
       if (s < s_hi) {
         const u32x4 a0 = wq[j][0], a1 = wq[j][1];
-        if (s + kMfmaPf < s_hi) {
-          const bf16_t* src = wrow + (s + kMfmaPf) * 64;
+        if (s + kPf < s_hi) {
+          const bf16_t* src = wrow + (s + kPf) * 64;
           wq[j][0] = *reinterpret_cast<const u32x4*>(src);
           wq[j][1] = *reinterpret_cast<const u32x4*>(src + 8);
         }
