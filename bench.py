@@ -339,6 +339,19 @@ def run_reference_api(torch, steps, warmup):
     return out
 
 
+# What the backward's algorithmic bytes are divided over in `roofline`.
+BWD_BYTES_OVER = ("bwd_kernel alone: every tensor the backward reads or writes once, including the dB/dC "
+                  "(and dA/dD/dbias) outputs that reduce_kernel writes from the scan's partial sums")
+
+
+def as_launched(bwd_bytes, scan_ms, reduce_ms):
+    """The backward as launched (scan kernel + reduction kernel) against the HBM roofline."""
+    ms = scan_ms + reduce_ms
+    achieved = bwd_bytes / (ms * 1e-3) / 1e9
+    return {"kernels": ["bwd_kernel", "reduce_kernel"], "ms": round(ms, 5), "achieved": round(achieved, 1),
+            "frac": round(achieved / HBM_PEAK_GBS, 4)}
+
+
 def scan_report(cfg, r):
     """ms, tokens/s and fractions of the 8 TB/s HBM roofline for one config's timings."""
     from mamba_amd.configs import algorithmic_bytes
@@ -365,6 +378,8 @@ def scan_report(cfg, r):
     rep["roofline"] = {"bound": "hbm", "kernel": kern, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(kern),
                        "algorithmic_bytes": int(bwd_b), "avg_launch_ms": round(r["bwd_scan"], 5),
+                       "bytes_over": BWD_BYTES_OVER,
+                       "backward_as_launched": as_launched(bwd_b, r["bwd_scan"], r["bwd_reduce"]),
                        "fwd_traffic": read_traffic(f"fwd_{cfg.name}")}
     if lens is not None:
         rep["seq_lens"] = [int(x) for x in lens]
@@ -739,6 +754,9 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(tag),
                 "kernel": tag, "algorithmic_bytes": bytes_, "avg_launch_ms": round(dur, 5)}
+    if tag.startswith("bwd"):
+        roofline["bytes_over"] = BWD_BYTES_OVER
+        roofline["backward_as_launched"] = as_launched(bwd_bytes, bwd_ms, red_ms)
     if args.calibration_copy_mib > 0:
         src = torch.ones(args.calibration_copy_mib * (1 << 20) // 4, device="cuda")
         dst = torch.empty_like(src)

@@ -169,7 +169,9 @@ int mss_bwd(const mss_bwd_args* args, void* stream);
  * (mss_bwd_workspace_bytes) exceeds it return MSS_ERR_SCRATCH_LIMIT before any launch.
  * Results equal mss_bwd's bit for bit (same kernels, same plan). All calls on one device
  * share the one array: calls whose executions overlap on a device (concurrent streams, or
- * threads) race and must be serialised by the caller. */
+ * threads) race and must be serialised by the caller. The array's device address is looked
+ * up once per device and kept for the life of the process: after hipDeviceReset on a device
+ * (which unloads the library's code objects) this entry point must not be called there. */
 int mss_bwd_noalloc(const mss_bwd_args* args, void* stream);
 
 /* mss_bwd in two stream-ordered phases sharing a caller-provided workspace (NULL ->
@@ -302,9 +304,13 @@ int mss_gemv(const mss_gemv_args* args, void* stream);
 
 /* mss_gemv with the next decode step fused behind it (no counterpart symbol in the
  * reference: Mamba.step, mamba/mamba1.py:339-363, applies the conv window and S6.step,
- * :200-214, to the projections' outputs). Each entry computes the products exactly as
- * mss_gemv (rounded to bf16), then, instead of storing some rows of Y, applies the step to
- * them; the results equal mss_gemv followed by the separate step call, bit for bit.
+ * :200-214, to the projections' outputs). Each entry computes the products with float32
+ * sums rounded to bf16 once, then, instead of storing some rows of Y, applies the step to
+ * those bf16 rows exactly as the separate step call would (bit for bit, given the same rows).
+ * The rows themselves equal mss_gemv's bit for bit except where the fused entry sums on the
+ * matrix cores and mss_gemv does not: mss_gemv_conv_step (and mss_norm_gemv_conv_step) with
+ * K % 64 == 0 and M below 4096 rows, where the two summation orders can leave a row one
+ * bf16 rounding apart.
  *
  * mss_gemv_conv_step: rows [0, conv->dim) of W X are conv->x (ignored, may be null) of
  * mss_conv_step: conv_state and conv->y are updated as that call would, and those rows of

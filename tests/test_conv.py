@@ -3,7 +3,8 @@ mamba/mamba1.py:250-255, 313-329) through the C ABI.
 
 CPU: argument validation before any HIP call. GPU: forward and gradients vs the float64
 oracle conv (oracle/mamba1_torch.py, itself checked against torch.conv1d), float32 within
-rtol 1e-4 / atol 1e-5 (outputs; weight sums on the scale of the sum), bf16 within 2e-2;
+rtol 1e-4 / atol 1e-5 (outputs per element; the weight and bias sums per element against
+the sum of the absolute values of their terms), bf16 within 2e-2;
 widths 1-4, ragged lengths, channel-outer row layouts, variable lengths, determinism.
 """
 import numpy as np
@@ -68,16 +69,29 @@ def test_conv_python_errors():
 
 # ------------------------------------------------------------------ GPU parity
 def oracle(x, w, b, lens, silu):
-    """float64 forward + grads of sum(y * dy) from the oracle conv (B, L, D layout)."""
+    """float64 forward + grads of sum(y * dy) from the oracle conv (B, L, D layout); `pre`
+    (the pre-activation, its gradient retained) is returned for the |term| sums."""
     xt = torch.from_numpy(np.swapaxes(x, 1, 2).astype(np.float64)).requires_grad_(True)
     wt = torch.from_numpy(w.astype(np.float64)).requires_grad_(True)
     bt = torch.from_numpy(b.astype(np.float64)).requires_grad_(True)
     pre = ref.causal_depthwise_conv(xt, wt, bt)
+    pre.retain_grad()
     y = F.silu(pre) if silu else pre
     if lens is not None:
         mask = (torch.arange(x.shape[2])[None, :, None] < torch.as_tensor(lens)[:, None, None]).double()
         y = y * mask
-    return xt, wt, bt, y
+    return xt, wt, bt, y, pre
+
+
+def weight_abs_terms(x, w, b, dpre):
+    """Per element of dweight and dbias, the sum of the absolute values of the terms summed
+    into it: sum over (b, t) of |dpre[t]| |x[t - (K-1) + k]| and of |dpre[t]| (the oracle conv
+    run on |x| and contracted with |dpre|)."""
+    xa = torch.from_numpy(np.abs(np.swapaxes(x, 1, 2)).astype(np.float64))
+    wa = torch.from_numpy(w.astype(np.float64)).requires_grad_(True)
+    ba = torch.from_numpy(b.astype(np.float64)).requires_grad_(True)
+    (ref.causal_depthwise_conv(xa, wa, ba) * dpre.abs()).sum().backward()
+    return wa.grad, ba.grad
 
 
 def run_case(b, d, l, k, dtype, layout="brl", lens=None, silu=True, seed=0):
@@ -104,8 +118,9 @@ def run_case(b, d, l, k, dtype, layout="brl", lens=None, silu=True, seed=0):
     assert y.stride() == xg.stride() and y.dtype == tdt
     (y.float() * torch.from_numpy(dy).cuda()).sum().backward()
     torch.cuda.synchronize()
-    xt, wt, bt, yr = oracle(x, w, bias, lens, silu)
+    xt, wt, bt, yr, pre = oracle(x, w, bias, lens, silu)
     (yr * torch.from_numpy(np.swapaxes(dy, 1, 2).astype(np.float64))).sum().backward()
+    w_abs, b_abs = weight_abs_terms(x, w, bias, pre.grad)
     rtol, atol = (2e-2, 2e-2) if dtype == "bf16" else (1e-4, 1e-5)
     got_y = y.detach().float().cpu().double()
     torch.testing.assert_close(got_y, yr.detach().transpose(1, 2), rtol=rtol, atol=atol)
@@ -113,10 +128,15 @@ def run_case(b, d, l, k, dtype, layout="brl", lens=None, silu=True, seed=0):
     if layout == "rbl":
         dx = dx.permute(1, 0, 2)
     torch.testing.assert_close(dx, xt.grad.transpose(1, 2), rtol=rtol, atol=atol)
-    for got, want in ((wg.grad, wt.grad), (bg.grad, bt.grad)):
-        scale = float(want.abs().max()) + 1.0
-        err = float((got.cpu().double() - want).abs().max())
-        assert err <= (rtol if dtype == "bf16" else 1e-5) * scale * 4, (err, scale)
+    # dweight / dbias are sums over (batch, step): per element |got - want| <= atol + rtol * s,
+    # s the sum of the absolute values of the terms (any summation order stays within it).
+    srtol, satol = (2e-2, 1e-3) if dtype == "bf16" else (1e-4, 1e-5)
+    for name, got, want, s_abs in (("dweight", wg.grad, wt.grad, w_abs), ("dbias", bg.grad, bt.grad, b_abs)):
+        err = (got.cpu().double() - want).abs()
+        bound = satol + srtol * s_abs
+        ratio = float((err / bound).max())
+        print(f"  {name} max_abs={float(err.max()):.3e} worst err/bound={ratio:.3f}", flush=True)
+        assert bool(torch.all(err <= bound)), (name, float(err.max()), ratio)
     return y, leaf.grad, wg.grad, bg.grad
 
 

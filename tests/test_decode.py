@@ -314,6 +314,35 @@ def test_gemv_conv_update_matches_separate_calls(n, k, act, extra):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("n", [1, 2, 4, 8])
+def test_gemv_conv_update_matrix_core_shape(n):
+    """The 130M in-projection's shape (M = 3072 rows [x; z], K = 768, K % 64 == 0): the
+    conv-fused GEMM sums on the matrix cores, in another order than the plain decode GEMM of
+    3072 rows, so its bf16 rows may differ from mss_gemv's by one rounding of the float32 sum.
+    With the z rows a copy of the x rows, the z rows the fused call writes are the very rows
+    its conv step consumed: the conv window step applied to them by the separate call gives
+    the fused u and window state bit for bit, over three steps in a row; and every fused row
+    is within one bf16 rounding of mss_gemv's."""
+    torch.manual_seed(70 + n)
+    dim, kin = 1536, 768
+    wx = _bf16(dim, kin, scale=kin ** -0.5)
+    w = torch.cat([wx, wx]).contiguous()
+    weight = torch.randn(dim, 4, device="cuda") * 0.5
+    bias = torch.randn(dim, device="cuda") * 0.1
+    s_fused = _bf16(n, dim, 3)
+    s_ref = s_fused.clone()
+    for _ in range(3):
+        x = _bf16(kin, n)
+        u, rest = gemv_conv_update(w, x, s_fused, weight, bias, "silu")
+        u_ref = causal_conv1d_update(s_ref, rest.t(), weight, bias, "silu").t()
+        assert torch.equal(u, u_ref)
+        assert torch.equal(s_fused, s_ref)
+        v = gemv(w, x)[dim:].float()
+        ulp = torch.exp2(torch.floor(torch.log2(v.abs().clamp_min(1e-30))) - 7)
+        assert bool(torch.all((rest.float() - v).abs() <= ulp)), float(((rest.float() - v).abs() / ulp).max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 2, 4, 8])
 @pytest.mark.parametrize("zoh,with_dz,dstate", [(False, True, 16), (True, True, 16), (False, False, 5),
                                                 (True, False, 11)])
 def test_gemv_state_update_matches_separate_calls(n, zoh, with_dz, dstate):

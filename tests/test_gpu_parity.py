@@ -252,6 +252,28 @@ def test_varlen_dead_chunks(lens):
     check_fused(ts, out, last, fw, g)
 
 
+MULTI_ROUND_LENS = [1100, 530, 0, 1, 1099, 512, 513, 700]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("n,zoh", [(16, False), (11, False), (8, True)])
+def test_varlen_multi_round(n, zoh, dtype):
+    """Variable lengths on a grid whose backward workgroups walk several channel rounds (the
+    plan of config 4: more channels per workgroup than waves): per round the adjoint message,
+    dA, dD and ddelta_bias bookkeeping restarts from the round's channels, the dead chunks
+    past a row's length pass the message through and write zero gradients for every round,
+    and rows are handed out longest first. 16 waves x 2 rounds (N = 16, 8) and 12 waves x 2
+    rounds (N = 11, two accumulator copies); an empty row, a one-step row, lengths one short
+    of / exactly at / one past a 512-step chunk; garbage in the padding; every fused extra."""
+    log(f"case varlen multi-round N={n} zoh={zoh} {dtype}")
+    waves, cpb = _lib.bwd_plan(8, 1536, n, 1100, varlen=True, zoh=zoh, io_bf16=dtype == "bf16")
+    assert cpb >= 2 * waves, (waves, cpb)
+    x, dout, dlast = fused_case(1400 + n + zoh, 8, 1536, 1100, n, dtype, lens=MULTI_ROUND_LENS, zoh=zoh)
+    ts, out, last = run_fused(x, dout, dlast, dtype, zoh)
+    fw, g = oracle_fused(x, dout, dlast, zoh)
+    check_fused(ts, out, last, fw, g, *tol(dtype))
+
+
 PER_ROW = ("u", "delta", "z", "B", "C", "initial_state", "seq_lens")
 
 
@@ -643,6 +665,59 @@ def test_config3_full_size_bf16():
     fw, g = oracle_fused(x, dout, dlast, False)
     worst = check_fused(ts, out, last, fw, g, *tol("bf16"))
     log("  c3 worst err/bound: " + ", ".join(f"{k}={v:.3f}" for k, v in worst.items()))
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(900)
+def test_config4_full_size():
+    """Config 4 at its full shape (B=16, D=2560, L=8192, N=16, float32, seed-0 lengths in
+    [512, 8192] right-padded with N(0,1) garbage): the backward plan the config runs (16 waves
+    x 80 channels, five channel rounds per workgroup, dead chunks past each row's length), a
+    random final-state cotangent, every output and gradient against the float64 oracle."""
+    log("case c4 full size")
+    assert _lib.bwd_plan(C4.batch, C4.dim, C4.dstate, C4.length, varlen=True) == (16, 80)
+    x = make_scan_inputs(C4, seed=0, with_z=True, with_dout=True)
+    dout = x.pop("dout")
+    log(f"  lengths {x['seq_lens'].tolist()}")
+    dlast = np.random.default_rng(1).standard_normal((C4.batch, C4.dim, C4.dstate)).astype(np.float32)
+    ts, out, last = run_fused(x, dout, dlast, "f32", False)
+    log("  gpu done, running the oracle")
+    fw, g = oracle_fused(x, dout, dlast, False)
+    worst = check_fused(ts, out, last, fw, g)
+    log("  c4 worst err/bound: " + ", ".join(f"{k}={v:.3f}" for k, v in worst.items()))
+
+
+@pytest.mark.parametrize("zoh", [False, True])
+def test_reference_fwd_repeat(zoh):
+    """mss_scan_fwd_repeat (the reference benchmark handler's counterpart, which launches the
+    forward `repeats` times into the same outputs, native/selective_scan_cuda.cu:470-477):
+    three launches leave y, final_x and chunk_states bit for bit as one launch does, and
+    those match the float64 oracle (three 2048-step blocks, a ragged last one)."""
+    log(f"case reference fwd repeat zoh={zoh}")
+    lib = _lib.register_hip_kernel()
+    A, deltas, Bs, Cs, u, x0 = ref_recipe(17 + zoh, batch=2, length=4500, dim=8, n=16)
+    b, l, d = u.shape
+    n = A.shape[1]
+    tr = lambda a: T(np.swapaxes(a, 1, 2))
+    tA, td, tB, tC, tu, tx0 = T(A), tr(deltas), tr(Bs), tr(Cs), tr(u), T(x0)
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def run(repeats):
+        outs = [torch.full((b, d, l), float("nan"), device=dev), torch.full((b, d, n), float("nan"), device=dev),
+                torch.full((b, d, -(-l // 2048), n, 2), float("nan"), device=dev)]
+        _lib.check(lib.mss_scan_fwd_repeat(st, int(zoh), repeats, b, l, d, n, P(tA), P(td), P(tB), P(tC), P(tu),
+                                           P(tx0), *[P(o) for o in outs]), "mss_scan_fwd_repeat")
+        torch.cuda.synchronize()
+        return outs
+
+    one, three = run(1), run(3)
+    for name, o1, o3 in zip(("y", "final_x", "chunk_states"), one, three):
+        assert torch.equal(o1, o3), name
+    ey, efin, ecs = scan64.reference_api_forward(A, deltas, Bs, Cs, u, x0, use_euler_barB_approx=not zoh)
+    close("y", three[0].transpose(1, 2), ey)
+    close("final_x", three[1], efin)
+    close("chunk_states", three[2], ecs)
 
 
 @pytest.mark.slow
