@@ -101,6 +101,14 @@ void fwd_kernel(FwdParams p) {
   __shared__ float s_run[kW][kMaxS];
   __shared__ float s_a2[kW][kMaxS];
   __shared__ float s_a[kW][kMaxS];
+  // 16-step lanes: each wave's z row for the current chunk, copied from global memory at the
+  // chunk start (direct-to-LDS) so its latency passes under the state loop instead of after
+  // it; lane i's q-th 16-byte slot at [q * 64 + i]. (Measured on MI355X, c3 forward 414 ->
+  // 406 us, a c5 layer's 162 -> 158; with the 8-step float32 shape, whose three workgroups
+  // per CU it would take 16 KB of LDS each, c2 102 -> 111, so that shape keeps the load.)
+  constexpr bool kZLds = kT == 16;
+  constexpr int kZq = kT * static_cast<int>(sizeof(io_t)) / 16;
+  __shared__ uint4 s_z[kW][kZLds ? kZq * 64 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -180,9 +188,19 @@ void fwd_kernel(FwdParams p) {
 
     float dlt[kT], dlu[kT], y[kT];
     float ssum = 0.f;
+    // z through LDS for whole vectorisable chunks (wave-uniform); the first round barrier's
+    // wait covers the copies.
+    const bool z_lds = kZLds && active && fast && p.z != nullptr && p.out != nullptr;
     if (active) {
       load_seg<kT>(dl_row, tl, L, fast, dlt);
       load_seg<kT>(u_row, tl, L, fast, y);
+      if (kZLds && z_lds) {
+        const io_t* zsrc = static_cast<const io_t*>(p.z) + row + tl;
+#pragma unroll
+        for (int q = 0; q < kZq; ++q)
+          __builtin_amdgcn_global_load_lds((gbl_void_t)(zsrc + q * (16 / static_cast<int>(sizeof(io_t)))),
+                                           (lds_void_t)(&s_z[w][q * 64]), 16, 0, 0);
+      }
 #pragma unroll
       for (int j = 0; j < kT; ++j) {
         const bool valid = tl + j < len;
@@ -280,7 +298,32 @@ void fwd_kernel(FwdParams p) {
           store_seg<kT>(static_cast<io_t*>(p.y_pre) + row, tl, L, fast, yp);
         }
         float zv[kT];
-        load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zv);
+        if (kZLds && z_lds) {
+          // the wave's own copies, completed at the first round barrier
+          if constexpr (sizeof(io_t) == 4) {
+#pragma unroll
+            for (int q = 0; q < kZq; ++q) {
+              const uint4 x = s_z[w][q * 64 + lane];
+              zv[4 * q + 0] = __uint_as_float(x.x);
+              zv[4 * q + 1] = __uint_as_float(x.y);
+              zv[4 * q + 2] = __uint_as_float(x.z);
+              zv[4 * q + 3] = __uint_as_float(x.w);
+            }
+          } else {
+#pragma unroll
+            for (int q = 0; q < kZq; ++q) {
+              const uint4 x = s_z[w][q * 64 + lane];
+              const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                zv[8 * q + 2 * k + 0] = __uint_as_float(wd[k] << 16);
+                zv[8 * q + 2 * k + 1] = __uint_as_float(wd[k] & 0xffff0000u);
+              }
+            }
+          }
+        } else {
+          load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zv);
+        }
 #pragma unroll
         for (int j = 0; j < kT; ++j) y[j] *= zv[j] * sigmoid(zv[j]);
       }
