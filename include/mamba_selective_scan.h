@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 9
+#define MSS_ABI_VERSION 10
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -386,6 +386,28 @@ typedef struct mss_xent_args {
 
 int mss_xent_fwd(const mss_xent_args* args, void* stream);
 int mss_xent_bwd(const mss_xent_args* args, void* stream);
+
+/* --- Skinny projection GEMMs of the training step (bf16, float32 sums). ------------
+ * No counterpart symbol in the reference: its S6 input projections (s_B, s_C, Linear_R:
+ * d_inner -> R + 2N; Linear_Delta: R -> d_inner, mamba/mamba1.py:52-67, 107-124) run as
+ * XLA dot products. Matrices are row-major; activations channel-major [features][tokens].
+ *
+ * mss_proj: C[M][T] = W[M][K] X[K][T] (+ C when accumulate != 0, the old C read as bf16 and
+ * the sum rounded once), C rounded to bf16. With w_trans != 0 the weight is passed as its
+ * transpose, W^T [K][M] with row stride ldw >= M (e.g. the input-gradient products W^T dY
+ * from the stored W). M % 16 == 0, T % 64 == 0, and either K <= 128 with K % 16 == 0, or
+ * K % 64 == 0 with M <= 128; W, X, C 16-byte aligned with ldw, ldx, ldc multiples of 8
+ * (elements); C overlapping neither W nor X. MSS_ERR_UNSUPPORTED for other shapes. */
+typedef struct mss_proj_args {
+  int32_t M, K, T, accumulate, w_trans;
+  int64_t ldw, ldx, ldc;
+  const void* W;
+  const void* X;
+  void* C;
+} mss_proj_args;
+
+int mss_proj(const mss_proj_args* args, void* stream);
+
 
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------
  * Same argument order, attribute meaning and buffer shapes as the reference's XLA-FFI

@@ -41,6 +41,7 @@ hipError_t launch_xent(const XentParams& p, bool bwd, bool vec, hipStream_t stre
 hipError_t launch_ssm_step(const StepParams& p, bool zoh, bool io_bf16, bool bc_bf16, hipStream_t stream);
 hipError_t launch_conv_step(const ConvStepParams& p, bool io_bf16, hipStream_t stream);
 hipError_t launch_gemv(const GemvParams& p, hipStream_t stream);
+hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -686,6 +687,51 @@ int mss_xent_bwd(const mss_xent_args* args, void* stream) {
   const int s = validate_xent(args, true);
   return s != MSS_OK ? s : run_xent(args, true, static_cast<hipStream_t>(stream));
 }
+
+namespace {
+bool spans_overlap(const void* a, long long rows_a, long long ld_a, long long cols_a, const void* b,
+                   long long rows_b, long long ld_b, long long cols_b) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  const uintptr_t xe = x + static_cast<uintptr_t>(((rows_a - 1) * ld_a + cols_a) * 2);
+  const uintptr_t ye = y + static_cast<uintptr_t>(((rows_b - 1) * ld_b + cols_b) * 2);
+  return x < ye && y < xe;
+}
+
+}  // namespace
+
+int mss_proj(const mss_proj_args* a, void* stream) {
+  if (a == nullptr || a->M <= 0 || a->K <= 0 || a->T <= 0 || !a->W || !a->X || !a->C)
+    return MSS_ERR_INVALID_ARGUMENT;
+  if (a->ldw < (a->w_trans ? a->M : a->K) || a->ldx < a->T || a->ldc < a->T) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->ldw % 8 != 0 || a->ldx % 8 != 0 || a->ldc % 8 != 0 || !aligned16(a->W) || !aligned16(a->X) ||
+      !aligned16(a->C))
+    return MSS_ERR_INVALID_ARGUMENT;
+  const bool expand = a->K <= mss::kProjExpandMaxK && a->K % 16 == 0;
+  const bool reduce = a->K % 64 == 0 && a->M <= mss::kProjReduceMaxM;
+  if (a->M % 16 != 0 || a->T % 64 != 0 || (!expand && !reduce)) return MSS_ERR_UNSUPPORTED;
+  if (static_cast<long long>(a->M) * a->ldc >= (1LL << 40) || static_cast<long long>(a->K) * a->ldx >= (1LL << 40))
+    return MSS_ERR_UNSUPPORTED;
+  if ((a->w_trans ? spans_overlap(a->C, a->M, a->ldc, a->T, a->W, a->K, a->ldw, a->M)
+                  : spans_overlap(a->C, a->M, a->ldc, a->T, a->W, a->M, a->ldw, a->K)) ||
+      spans_overlap(a->C, a->M, a->ldc, a->T, a->X, a->K, a->ldx, a->T))
+    return MSS_ERR_INVALID_ARGUMENT;
+  mss::ProjParams p{};
+  p.M = a->M;
+  p.K = a->K;
+  p.T = a->T;
+  p.accumulate = a->accumulate != 0;
+  p.w_trans = a->w_trans != 0;
+  p.ldw = a->ldw;
+  p.ldx = a->ldx;
+  p.ldc = a->ldc;
+  p.W = a->W;
+  p.X = a->X;
+  p.C = a->C;
+  const hipError_t e = mss::launch_proj(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching projection GEMM");
+}
+
+
 
 namespace {
 // Validated StepParams of a scan-step call; need_delta false when delta comes from elsewhere.

@@ -327,6 +327,20 @@ struct XentParams {
   bf16_t* dz;
 };
 
+// Skinny projection GEMM C[M][T] (+)= W[M][K] X[K][T], bf16 with float32 sums: K <= 128
+// takes the expand kernel (M % 16 == 0), else the reduce kernel (M <= 128, M % 16 == 0,
+// K % 64 == 0); T % 64 == 0.
+constexpr int kProjExpandMaxK = 128;
+constexpr int kProjReduceMaxM = 128;
+struct ProjParams {
+  int M, K, T, accumulate;
+  int w_trans;  // W given as W^T [K][M] (row stride ldw)
+  long long ldw, ldx, ldc;
+  const void* W;
+  const void* X;
+  void* C;
+};
+
 struct StepParams {
   int batch, dim, dstate, delta_softplus;
   long long io_sb, io_sd, bc_sb, bc_sn;

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 9
+MSS_ABI_VERSION = 10
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -63,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "mss_gemv_conv_step",
     "mss_gemv_scan_step",
     "mss_norm_gemv_conv_step",
+    "mss_proj",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -140,6 +141,11 @@ class StepArgs(ctypes.Structure):
 
 class GemvArgs(ctypes.Structure):
     _fields_ = [("M", _i32), ("K", _i32), ("N", _i32), ("ldw", ctypes.c_int64), ("W", _p), ("X", _p), ("Y", _p)]
+
+
+class ProjArgs(ctypes.Structure):
+    _fields_ = [("M", _i32), ("K", _i32), ("T", _i32), ("accumulate", _i32), ("w_trans", _i32), ("ldw", ctypes.c_int64),
+                ("ldx", ctypes.c_int64), ("ldc", ctypes.c_int64), ("W", _p), ("X", _p), ("C", _p)]
 
 
 class ConvStepArgs(ctypes.Structure):
@@ -224,6 +230,8 @@ def register_hip_kernel(library_path=None):
     lib.mss_norm_gemv_conv_step.argtypes = [ctypes.POINTER(NormArgs), ctypes.POINTER(GemvArgs),
                                             ctypes.POINTER(ConvStepArgs), _p]
     lib.mss_norm_gemv_conv_step.restype = ctypes.c_int
+    lib.mss_proj.argtypes = [ctypes.POINTER(ProjArgs), _p]
+    lib.mss_proj.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

@@ -32,6 +32,7 @@ from . import _lib
 from .decode import (causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update, norm_gemv_conv_update,
                      selective_state_update)
 from .lm_ops import add_rmsnorm
+from .proj import proj, proj_fits
 from .selective_scan_hip import _io_tag, _ptr, _stream, selective_scan_fn
 
 __all__ = ["S6", "MambaBlock", "MambaLM", "RMSNormCM", "ShadowWeights", "GraphedTrainStep"]
@@ -52,6 +53,19 @@ def _mm_fp32(a, b):
     if _MM_FP32_OUT:
         return torch.mm(a, b, out_dtype=torch.float32)
     return torch.mm(a, b).float()
+
+
+def _proj_mm(w, x, out=None, accumulate=False):
+    """w @ x (+ out when accumulate) for the S6 input projections (w may be a transposed view
+    of a stored weight): the skinny-GEMM kernels where the shape and layout fit, else the
+    library GEMM."""
+    if proj_fits(w, x, out):
+        return proj(w, x, out=out, accumulate=accumulate)
+    if out is None:
+        return torch.mm(w, x)
+    if accumulate:
+        return out.addmm_(w, x)
+    return torch.mm(w, x, out=out)
 
 
 class _WeightMM(torch.autograd.Function):
@@ -306,8 +320,8 @@ class _MambaMixer(torch.autograd.Function):
                            x=xin.data_ptr(), weight=conv_w.data_ptr(), bias=_ptr(conv_b),
                            seq_lens=_ptr(seq_lens), y=u.data_ptr(), strides=st)
         _lib.check(lib.mss_conv_fwd(ca, stream), "mss_conv_fwd")
-        x_dbl = torch.mm(w_x_act, u)                     # (R + 2N, T)
-        dt = torch.mm(w_dt_act, x_dbl[:r])               # (di, T), bias fused in the scan
+        x_dbl = _proj_mm(w_x_act, u)                     # (R + 2N, T)
+        dt = _proj_mm(w_dt_act, x_dbl[:r])               # (di, T), bias fused in the scan
         n_seg = (L + _lib.MSS_SEG_STEPS - 1) // _lib.MSS_SEG_STEPS
         sdt = torch.complex64 if cplx else torch.float32
         rv = (lambda t: torch.view_as_real(t).data_ptr()) if cplx else (lambda t: t.data_ptr())
@@ -364,9 +378,9 @@ class _MambaMixer(torch.autograd.Function):
         ba.workspace, ba.workspace_bytes = ws.data_ptr(), ws_bytes
         _lib.check((lib.mss_cbwd if cplx else lib.mss_bwd)(ba, stream), "scan backward")
         dw_dt = _mm_fp32(ddt, x_dbl[:r].t())
-        torch.mm(w_dt_act.t(), ddt, out=dx_dbl[:r])
+        _proj_mm(w_dt_act.t(), ddt, out=dx_dbl[:r])
         dw_x = _mm_fp32(dx_dbl, u.t())
-        du.addmm_(w_x_act.t(), dx_dbl)                    # du += W_x^T dx_dbl
+        _proj_mm(w_x_act.t(), dx_dbl, out=du, accumulate=True)  # du += W_x^T dx_dbl
         dconv_w = torch.empty_like(conv_w)
         dconv_b = None if conv_b is None else torch.empty_like(conv_b)
         ca = _lib.ConvArgs(batch=batch, dim=di, seqlen=L, width=conv_w.shape[1], io_dtype=io, activation=1,

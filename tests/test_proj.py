@@ -1,0 +1,145 @@
+"""Skinny projection GEMMs of the training step (mss_proj): the S6 input projections
+(mamba/mamba1.py:52-67, 107-124) and their input gradients on the matrix cores.
+
+CPU: argument validation (rejected calls only, before any launch) and the shape gates.
+GPU: against float32 products computed on the CPU from the same bf16 values —
+  * small-integer operands, whose float32 sums are exact in any order: mss_proj equals the
+    bf16 rounding of the exact product (and of old C + product when accumulating) bit for
+    bit;
+  * random operands: per element |got - ref| <= 2^-8 |ref| + 1e-6 sum|terms| (one bf16
+    rounding plus float32 summation-order differences);
+  * the weight passed transposed gives the same bits; strided row views (a row slice of a
+    wider matrix as X or C); repeated calls bit for bit; the config-5 mixer's four products
+    take these kernels.
+"""
+import pytest
+import torch
+
+from mamba_amd import _lib
+from mamba_amd.proj import proj, proj_fits
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.register_hip_kernel()
+
+
+def _proj_base(**kw):
+    # Distinct, 16-byte aligned fake addresses far apart: only rejected calls are made here.
+    base = dict(M=80, K=1536, T=4096, accumulate=0, ldw=1536, ldx=4096, ldc=4096,
+                W=1 << 32, X=1 << 36, C=1 << 40)
+    base.update(kw)
+    return _lib.ProjArgs(**base)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(M=0), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(W=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(C=None), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(ldw=1000), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(ldx=4100), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(X=(1 << 36) + 8), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(M=88), _lib.MSS_ERR_UNSUPPORTED), (dict(T=4000, ldx=4000, ldc=4000), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(M=144), _lib.MSS_ERR_UNSUPPORTED), (dict(K=1544, ldw=1544), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(K=136, ldw=136), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(C=(1 << 36) + 4096 * 2 * 8), _lib.MSS_ERR_INVALID_ARGUMENT),  # C inside X
+    (dict(w_trans=1, ldw=72), _lib.MSS_ERR_INVALID_ARGUMENT),  # W^T rows hold M = 80 values
+])
+def test_proj_validation(lib, kw, status):
+    assert lib.mss_proj(_proj_base(**kw), None) == status
+
+
+def test_fits_gates_cpu_tensors():
+    w = torch.zeros(80, 1536, dtype=torch.bfloat16)
+    x = torch.zeros(1536, 4096, dtype=torch.bfloat16)
+    assert not proj_fits(w, x)  # not on a GPU
+
+
+# ------------------------------------------------------------------------------ GPU
+def _ints(shape, gen, lo=-4, hi=4):
+    return torch.randint(lo, hi + 1, shape, generator=gen).to(torch.bfloat16)
+
+
+def _randn(shape, gen, scale=1.0):
+    return (torch.randn(shape, generator=gen) * scale).to(torch.bfloat16)
+
+
+def _check_bf16(got, W, X, old=None):
+    ref = W.float() @ X.float()
+    terms = W.float().abs() @ X.float().abs()
+    if old is not None:
+        ref = ref + old.float()
+        terms = terms + old.float().abs()
+    bound = 2.0 ** -8 * ref.abs() + 1e-6 * terms
+    err = (got.float().cpu() - ref).abs()
+    assert bool((err <= bound).all()), f"max err/bound {float((err / bound.clamp_min(1e-30)).max()):.3g}"
+
+
+PROJ_SHAPES = [  # (M, K, T): reduce kernel (K % 64, M <= 128) and expand kernel (K <= 128)
+    (80, 1536, 4096), (48, 1536, 2048), (16, 64, 64), (128, 192, 128), (112, 256, 320),
+    (1536, 48, 2048), (1536, 80, 4096), (1552, 16, 128), (16, 128, 64), (32, 112, 192),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,T", PROJ_SHAPES)
+def test_proj_exact_small_integers(M, K, T):
+    gen = torch.Generator().manual_seed(M * 7 + K * 3 + T)
+    W, X = _ints((M, K), gen), _ints((K, T), gen)
+    want = (W.float() @ X.float()).to(torch.bfloat16)
+    got = proj(W.cuda(), X.cuda())
+    assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
+    old = _ints((M, T), gen, -1000, 1000)
+    want = (old.float() + W.float() @ X.float()).to(torch.bfloat16)
+    out = old.cuda()
+    proj(W.cuda(), X.cuda(), out=out, accumulate=True)
+    assert torch.equal(out.cpu().view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,T", PROJ_SHAPES)
+def test_proj_random(M, K, T):
+    gen = torch.Generator().manual_seed(1000 + M + K + T)
+    W, X = _randn((M, K), gen, K ** -0.5), _randn((K, T), gen)
+    got = proj(W.cuda(), X.cuda())
+    _check_bf16(got, W, X)
+    again = proj(W.cuda(), X.cuda())
+    assert torch.equal(got.view(torch.int16), again.view(torch.int16))
+    old = _randn((M, T), gen)
+    out = old.cuda()
+    proj(W.cuda(), X.cuda(), out=out, accumulate=True)
+    _check_bf16(out, W, X, old)
+    # the weight passed as the transposed view of its (K, M) transpose: same sums, same bits
+    Wt = W.t().contiguous().cuda()
+    assert torch.equal(proj(Wt.t(), X.cuda()).view(torch.int16), got.view(torch.int16))
+    out_t = old.cuda()
+    proj(Wt.t(), X.cuda(), out=out_t, accumulate=True)
+    assert torch.equal(out_t.view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.gpu
+def test_proj_row_views():
+    """X and C as row slices of wider matrices (the model's x_dbl[:R] / dx_dbl[:R])."""
+    gen = torch.Generator().manual_seed(5)
+    T = 2048
+    big = _randn((80, T), gen).cuda()
+    W = _randn((1536, 48), gen, 48 ** -0.5)
+    got = proj(W.cuda(), big[:48])
+    _check_bf16(got, W, big[:48].cpu())
+    W2 = _randn((48, 1536), gen, 1536 ** -0.5)
+    X2 = _randn((1536, T), gen)
+    sink = torch.full((80, T), 7.0, dtype=torch.bfloat16, device="cuda")
+    proj(W2.cuda(), X2.cuda(), out=sink[:48])
+    _check_bf16(sink[:48], W2, X2)
+    assert bool((sink[48:] == 7.0).all())  # rows past the view untouched
+
+
+@pytest.mark.gpu
+def test_model_projection_shapes_take_the_kernels():
+    """The config-5 mixer's four projection products fit the kernels (so the model runs
+    them, not the library GEMM)."""
+    dev = "cuda"
+    T, di, r, n = 16384, 1536, 48, 16
+    u = torch.empty(di, T, dtype=torch.bfloat16, device=dev)
+    x_dbl = torch.empty(r + 2 * n, T, dtype=torch.bfloat16, device=dev)
+    w_x = torch.empty(r + 2 * n, di, dtype=torch.bfloat16, device=dev)
+    w_dt = torch.empty(di, r, dtype=torch.bfloat16, device=dev)
+    assert proj_fits(w_x, u) and proj_fits(w_dt, x_dbl[:r])
+    assert proj_fits(w_dt.t(), u, x_dbl[:r]) and proj_fits(w_x.t(), x_dbl, u)
