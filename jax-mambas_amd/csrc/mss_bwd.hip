@@ -19,8 +19,9 @@
 //            the right (dlast for the last chunk), then a re-run producing lambda_t and
 //            every per-step gradient term; dB partial lambda_t*delta_t*u_t
 // dB/dC are sums over channels: each wave adds its per-(n, t) terms into an LDS
-// accumulator shared by the workgroup (rows owned in rotation, plain read-add-write, one
-// barrier per state), flushed once per chunk to a per-channel-block partial; a second
+// accumulator shared by the workgroup (rows owned in rotation, plain read-add-write; a wave
+// takes its next row once that row's previous owner has marked the iteration done in LDS,
+// no workgroup barrier per state), flushed once per chunk to a per-channel-block partial; a second
 // kernel sums the partials in a fixed order. This replaces the reference's
 // one-global-atomic-per-(b,d,n,t) scheme (selective_scan_bwd_kernel.cuh:295-318).
 #include "mss_common.h"
@@ -160,6 +161,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   __shared__ float s_dD[kMaxChanPerBlock];
   __shared__ float s_db[kMaxChanPerBlock];
   __shared__ float s_A[kW][kMaxN];  // A row of each wave's current channel
+  __shared__ int s_done[kW];         // state iterations of the current chunk each wave has finished
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -186,6 +188,16 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
   uint4(*const stage)[2][kRowSlots] = reinterpret_cast<uint4(*)[2][kRowSlots]>(lds + acc_floats);
   const int wmod = w % N;
   float* const acc_w = acc + (w / N) * 2 * N * kChunk;
+  // Rows of a copy rotate one wave down per state iteration, so the previous owner of this
+  // wave's row at chunk iteration g is the copy's next wave at g - 1 or, for the copy's last
+  // wave, its first wave at g - (N - wmod): every wait is on an earlier iteration, so the
+  // waits always resolve. (A workgroup barrier per iteration instead, measured on MI355X:
+  // backward 906 / 357 / 3121 us at c3 / a c5 layer / c4 against 882 / 350 / 3033, c2 the
+  // same.)
+  const int copy_waves = min(N, kW - (w / N) * N);
+  const int pred = wmod + 1 < copy_waves ? w + 1 : w - wmod;
+  const int pred_lag = wmod + 1 < copy_waves ? 1 : N - wmod;
+  if (tid < kW) s_done[tid] = 0;
   for (int i = tid; i < acc_floats; i += kW * 64) acc[i] = 0.f;
   for (int k = 0; k < K; ++k) {
     const int cl = k * kW + w;
@@ -315,8 +327,23 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         float bv[kT], cg[kT];
         read_staged<kT, bc_t>(stage[n][0], seg, bv);
         read_staged<kT, bc_t>(stage[n][1], seg, cg);
-        __syncthreads();
-        if (!active) continue;
+        const int gi = k * N + i;  // state iteration within the chunk
+        {
+          // Row n is free once its previous owner has finished its iteration. The poll is
+          // bounded only so that it ends in every case; the owner always progresses.
+          const int need = gi - pred_lag + 1;
+          if (need > 0) {
+            int spins = 0;
+            while (__hip_atomic_load(&s_done[pred], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need &&
+                   ++spins < (1 << 22))
+              __builtin_amdgcn_s_sleep(1);
+          }
+          asm volatile("" ::: "memory");  // the row's reads stay below the poll
+        }
+        if (!active) {  // owns the row without touching it: passes it on
+          if (lane == 0) __hip_atomic_store(&s_done[w], gi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          continue;
+        }
         const float An = s_A[w][n];
         const float a2 = An * kLog2e;
         const float mu = s_mu[cl][n];
@@ -381,6 +408,8 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         }
 #pragma unroll
         for (int j = 0; j < kT; ++j) accn[j * 128] = accB[j];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's row writes have landed
+        if (lane == 0) __hip_atomic_store(&s_done[w], gi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         dA_pend = dA_l;
         n_pend = n;
       }
@@ -443,6 +472,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
     // ---- all waves are done with this chunk's stage and accumulator: start staging the
     // next chunk (to the left), then flush this chunk's dB/dC sums over the block's channels.
     __syncthreads();
+    if (tid < kW) s_done[tid] = 0;  // (read again only after the barrier that ends the flush)
     if (c > 0) stage_chunk<kT, kW, bc_t>(Bb, Cb, N, t0 - kChunk, L, p.bc_sn, dma, stage, tid);
     const size_t nl = static_cast<size_t>(N) * L;
     float* part = p.part_dBC + static_cast<size_t>(blk) * p.part_stride + static_cast<size_t>(b) * 2 * nl;
