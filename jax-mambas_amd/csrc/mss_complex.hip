@@ -268,10 +268,11 @@ __global__ __launch_bounds__(kCFwdW * 64) void cfwd_kernel(FwdParams p) {
 // state (carries), aggregate the segment's adjoint map from a zero seed, scan the maps
 // across the lanes, then re-run the adjoint from the true seed and form the gradients.
 // dB/dC of the chunk accumulate in LDS rows: at state iteration i wave w handles state
-// (i + w) mod N in copy w / N of that state's row, so no two waves share a row between
-// barriers and the sum order is fixed. After every channel round the rows (copies summed
-// in order) go to this workgroup's partial rows; a second kernel sums the partials over
-// workgroups in a fixed order.
+// (i + w) mod N in copy w / N of that state's row, so no two waves share a row at once and
+// the sum order is fixed; a wave adds into its row once the row's previous owner has
+// counted that iteration done in LDS (no workgroup barrier per iteration). After every
+// chunk the rows (copies summed in order) go to this workgroup's partial rows; a second
+// kernel sums the partials over workgroups in a fixed order.
 template <bool kZOH, bool kHasZ, typename io_t, typename bc_t>
 __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
   constexpr int W = kCBwdW;
@@ -280,6 +281,7 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
   __shared__ float s_dA[kCMaxChan][kMaxN][2];
   __shared__ float s_dD[kCMaxChan];
   __shared__ float s_db[kCMaxChan];
+  __shared__ int s_done[W];  // state iterations of the current chunk each wave has finished
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -312,6 +314,14 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
   }
   for (int i = tid; i < cpb; i += W * 64) s_dD[i] = s_db[i] = 0.f;
   for (int i = tid; i < copies * N * 2 * kCChunk; i += W * 64) (&s_acc[0][0][0])[i] = 0.f;
+  if (tid < W) s_done[tid] = 0;
+  // The previous owner of this wave's row at chunk iteration g: the copy's next wave at
+  // g - 1, or, for the copy's last wave, the copy's first wave at g - (N - w % N); every
+  // wait is on an earlier iteration, so all waits resolve.
+  const int wmod = w % N;
+  const int copy_waves = min(N, W - (w / N) * N);
+  const int pred = wmod + 1 < copy_waves ? w + 1 : w - wmod;
+  const int pred_lag = wmod + 1 < copy_waves ? 1 : N - wmod;
   __syncthreads();
 
   const int n_chunks = (L + kCChunk - 1) / kCChunk;
@@ -521,7 +531,18 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
             s_dA[k][n][0] += sar;
             s_dA[k][n][1] += sai;
           }
-          // This wave's rows for the iteration: accumulate the segment's dB/dC.
+          // This wave's rows for the iteration: accumulate the segment's dB/dC once the
+          // rows' previous owner is done with them (bounded poll: it always progresses).
+          {
+            const int need = r * N + it - pred_lag + 1;
+            if (need > 0) {
+              int spins = 0;
+              while (__hip_atomic_load(&s_done[pred], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need &&
+                     ++spins < (1 << 22))
+                __builtin_amdgcn_s_sleep(1);
+            }
+            asm volatile("" ::: "memory");  // the row's reads stay below the poll
+          }
           f32x4* rb = reinterpret_cast<f32x4*>(&s_acc[arow][0][seg * kCT]);
           f32x4* rc = reinterpret_cast<f32x4*>(&s_acc[arow][1][seg * kCT]);
 #pragma unroll
@@ -538,8 +559,19 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
             rb[q] = vb;
             rc[q] = vc;
           }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the row writes have landed
+        } else {
+          // An inactive wave owns its rows without touching them: it passes them on after
+          // their previous owner.
+          const int need = r * N + it - pred_lag + 1;
+          if (need > 0) {
+            int spins = 0;
+            while (__hip_atomic_load(&s_done[pred], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < need &&
+                   ++spins < (1 << 22))
+              __builtin_amdgcn_s_sleep(1);
+          }
         }
-        __syncthreads();  // accumulator rows change hands
+        if (lane == 0) __hip_atomic_store(&s_done[w], r * N + it + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
       if (active) {
         float dsum = 0.f, gsum = 0.f;
@@ -563,9 +595,11 @@ __global__ __launch_bounds__(kCBwdW * 64) void cbwd_kernel(BwdParams p) {
         }
       }
     }
-    // This chunk's dB/dC partial rows (copies summed in order), then clear the rows. The
-    // last state iteration's barrier ordered every accumulation before these reads. None
-    // past the row's length: the reduction takes those steps as zero (the rows stay zero).
+    // This chunk's dB/dC partial rows (copies summed in order), then clear the rows, after
+    // every wave's last accumulation. None past the row's length: the reduction takes those
+    // steps as zero (the rows stay zero).
+    __syncthreads();
+    if (tid < W) s_done[tid] = 0;  // (read again only after the barrier that ends the flush)
     float* part = p.part_dBC + static_cast<size_t>(blockIdx.x) * p.part_stride;
     for (int i = tid; live && i < 2 * N * kCChunk; i += W * 64) {
       const int which = i / (N * kCChunk);
