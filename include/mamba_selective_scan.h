@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 10
+#define MSS_ABI_VERSION 11
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -407,6 +407,31 @@ typedef struct mss_proj_args {
 } mss_proj_args;
 
 int mss_proj(const mss_proj_args* args, void* stream);
+
+/* --- Weight-gradient GEMM of the training step (bf16 operands, float32 output). -------
+ * No counterpart symbol in the reference: the gradients of its dense projections
+ * (mamba/mamba1.py:272-276, 330-337) are XLA dot products.
+ *
+ * mss_wgrad: C[M][N] = A[M][K] B[N][K]^T (+ C when accumulate != 0), float32, i.e.
+ * dW = dY X^T over channel-major activations (rows contiguous along K, the tokens).
+ * M and N multiples of 192, K a multiple of 64; A, B 16-byte aligned with lda, ldb >= K,
+ * multiples of 8 (elements); C 16-byte aligned with ldc >= N, a multiple of 4; C overlapping
+ * neither operand nor the workspace. The tokens are split over workgroups and the partial
+ * tiles added in a fixed order (results do not depend on timing): `workspace` holds
+ * mss_wgrad_workspace_bytes(M, N, K) bytes, 16-byte aligned (may be NULL when that is 0).
+ * MSS_ERR_UNSUPPORTED for other shapes (mss_wgrad_workspace_bytes returns 0 for them). */
+typedef struct mss_wgrad_args {
+  int32_t M, N, K, accumulate;
+  int64_t lda, ldb, ldc;
+  const void* A;
+  const void* B;
+  float* C;
+  void* workspace;
+  int64_t workspace_bytes;
+} mss_wgrad_args;
+
+int64_t mss_wgrad_workspace_bytes(int32_t M, int32_t N, int32_t K);
+int mss_wgrad(const mss_wgrad_args* args, void* stream);
 
 
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------

@@ -32,7 +32,6 @@ constexpr int kBwdT = kSegSteps;  // steps per lane: the granularity of the forw
 constexpr int kBwdChunk = 64 * kBwdT;
 static_assert(kBwdChunk == kPartChunk, "the reduction's chunk is the scan's");
 constexpr int kMaxChanPerBlock = 96;  // channels one workgroup walks, at most
-constexpr int kCUs = 256;             // MI355X compute units
 
 // Waves per workgroup, one workgroup per CU: 12 (3 per SIMD, 168 VGPRs) for every state
 // count, or 16 (4 per SIMD, 128 VGPRs) when 16 waves own exactly 16 accumulator rows

@@ -42,6 +42,7 @@ hipError_t launch_ssm_step(const StepParams& p, bool zoh, bool io_bf16, bool bc_
 hipError_t launch_conv_step(const ConvStepParams& p, bool io_bf16, hipStream_t stream);
 hipError_t launch_gemv(const GemvParams& p, hipStream_t stream);
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
+hipError_t launch_wgrad(const WgradParams& p, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -731,6 +732,56 @@ int mss_proj(const mss_proj_args* a, void* stream) {
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching projection GEMM");
 }
 
+
+
+namespace {
+// The split count of a supported weight-gradient shape, 0 for shapes the kernel does not take.
+int wgrad_shape_splits(int32_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || M % mss::kWgradTile != 0 || N % mss::kWgradTile != 0 || K % 64 != 0) return 0;
+  return mss::wgrad_splits(M, N, K);
+}
+}  // namespace
+
+int64_t mss_wgrad_workspace_bytes(int32_t M, int32_t N, int32_t K) {
+  const int s = wgrad_shape_splits(M, N, K);
+  return s > 1 ? static_cast<int64_t>(s) * M * N * 4 : 0;
+}
+
+int mss_wgrad(const mss_wgrad_args* a, void* stream) {
+  if (a == nullptr || a->M <= 0 || a->N <= 0 || a->K <= 0 || !a->A || !a->B || !a->C) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->lda < a->K || a->ldb < a->K || a->ldc < a->N) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->lda % 8 != 0 || a->ldb % 8 != 0 || a->ldc % 4 != 0 || !aligned16(a->A) || !aligned16(a->B) ||
+      !aligned16(a->C))
+    return MSS_ERR_INVALID_ARGUMENT;
+  const int splits = wgrad_shape_splits(a->M, a->N, a->K);
+  if (splits == 0) return MSS_ERR_UNSUPPORTED;
+  if (static_cast<long long>(a->M) * a->lda >= (1LL << 40) || static_cast<long long>(a->N) * a->ldb >= (1LL << 40) ||
+      static_cast<long long>(a->M) * a->ldc >= (1LL << 40))
+    return MSS_ERR_UNSUPPORTED;
+  const long long ws_bytes = mss_wgrad_workspace_bytes(a->M, a->N, a->K);
+  if (ws_bytes > 0 && (!a->workspace || a->workspace_bytes < ws_bytes || !aligned16(a->workspace)))
+    return MSS_ERR_INVALID_ARGUMENT;
+  // C (float32, 2 bf16 elements per column) against the operands and the workspace.
+  if (spans_overlap(a->C, a->M, 2 * a->ldc, 2 * a->N, a->A, a->M, a->lda, a->K) ||
+      spans_overlap(a->C, a->M, 2 * a->ldc, 2 * a->N, a->B, a->N, a->ldb, a->K) ||
+      (ws_bytes > 0 && spans_overlap(a->C, a->M, 2 * a->ldc, 2 * a->N, a->workspace, 1, 0, ws_bytes / 2)))
+    return MSS_ERR_INVALID_ARGUMENT;
+  mss::WgradParams p{};
+  p.M = a->M;
+  p.N = a->N;
+  p.K = a->K;
+  p.splits = splits;
+  p.accumulate = a->accumulate != 0;
+  p.lda = a->lda;
+  p.ldb = a->ldb;
+  p.ldc = a->ldc;
+  p.A = a->A;
+  p.B = a->B;
+  p.C = a->C;
+  p.workspace = static_cast<float*>(a->workspace);
+  const hipError_t e = mss::launch_wgrad(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching weight-gradient GEMM");
+}
 
 
 namespace {

@@ -327,6 +327,8 @@ struct XentParams {
   bf16_t* dz;
 };
 
+constexpr int kCUs = 256;  // MI355X compute units
+
 // Skinny projection GEMM C[M][T] (+)= W[M][K] X[K][T], bf16 with float32 sums: K <= 128
 // takes the expand kernel (M % 16 == 0), else the reduce kernel (M <= 128, M % 16 == 0,
 // K % 64 == 0); T % 64 == 0.
@@ -340,6 +342,21 @@ struct ProjParams {
   const void* X;
   void* C;
 };
+
+// Weight-gradient GEMM C[M][N] (+)= A[M][K] B[N][K]^T, bf16 operands with K-contiguous rows,
+// float32 output; K split over `splits` workgroups per output tile, whose partial tiles
+// ([splits][M][N] float32 in `workspace`) a second kernel adds in order. M and N multiples of
+// kWgradTile, K a multiple of 64.
+constexpr int kWgradTile = 192;
+struct WgradParams {
+  int M, N, K, splits, accumulate;
+  long long lda, ldb, ldc;
+  const void* A;
+  const void* B;
+  float* C;
+  float* workspace;
+};
+int wgrad_splits(int M, int N, int K);  // the split count launch_wgrad expects
 
 struct StepParams {
   int batch, dim, dstate, delta_softplus;

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 10
+MSS_ABI_VERSION = 11
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -64,6 +64,8 @@ EXPORTED_SYMBOLS = (
     "mss_gemv_scan_step",
     "mss_norm_gemv_conv_step",
     "mss_proj",
+    "mss_wgrad_workspace_bytes",
+    "mss_wgrad",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -146,6 +148,12 @@ class GemvArgs(ctypes.Structure):
 class ProjArgs(ctypes.Structure):
     _fields_ = [("M", _i32), ("K", _i32), ("T", _i32), ("accumulate", _i32), ("w_trans", _i32), ("ldw", ctypes.c_int64),
                 ("ldx", ctypes.c_int64), ("ldc", ctypes.c_int64), ("W", _p), ("X", _p), ("C", _p)]
+
+
+class WgradArgs(ctypes.Structure):
+    _fields_ = [("M", _i32), ("N", _i32), ("K", _i32), ("accumulate", _i32), ("lda", ctypes.c_int64),
+                ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64), ("A", _p), ("B", _p), ("C", _p), ("workspace", _p),
+                ("workspace_bytes", ctypes.c_int64)]
 
 
 class ConvStepArgs(ctypes.Structure):
@@ -232,6 +240,10 @@ def register_hip_kernel(library_path=None):
     lib.mss_norm_gemv_conv_step.restype = ctypes.c_int
     lib.mss_proj.argtypes = [ctypes.POINTER(ProjArgs), _p]
     lib.mss_proj.restype = ctypes.c_int
+    lib.mss_wgrad_workspace_bytes.argtypes = [_i32, _i32, _i32]
+    lib.mss_wgrad_workspace_bytes.restype = ctypes.c_int64
+    lib.mss_wgrad.argtypes = [ctypes.POINTER(WgradArgs), _p]
+    lib.mss_wgrad.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

@@ -32,7 +32,7 @@ from . import _lib
 from .decode import (causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update, norm_gemv_conv_update,
                      selective_state_update)
 from .lm_ops import add_rmsnorm
-from .proj import proj, proj_fits
+from .proj import proj, proj_fits, wgrad, wgrad_fits
 from .selective_scan_hip import _io_tag, _ptr, _stream, selective_scan_fn
 
 __all__ = ["S6", "MambaBlock", "MambaLM", "RMSNormCM", "ShadowWeights", "GraphedTrainStep"]
@@ -53,6 +53,14 @@ def _mm_fp32(a, b):
     if _MM_FP32_OUT:
         return torch.mm(a, b, out_dtype=torch.float32)
     return torch.mm(a, b).float()
+
+
+def _wgrad_mm(dy, x):
+    """dy @ x^T in float32 for activations dy (M, T), x (N, T): the split-token matrix-core
+    kernel where the shape fits, else the library GEMM."""
+    if wgrad_fits(dy, x):
+        return wgrad(dy, x)
+    return _mm_fp32(dy, x.t())
 
 
 def _proj_mm(w, x, out=None, accumulate=False):
@@ -81,7 +89,7 @@ class _WeightMM(torch.autograd.Function):
     def backward(ctx, dy):
         x, w_act = ctx.saved_tensors
         dx = w_act.t() @ dy if ctx.needs_input_grad[0] else None
-        dw = _mm_fp32(dy, x.t()) if ctx.needs_input_grad[1] else None
+        dw = _wgrad_mm(dy, x) if ctx.needs_input_grad[1] else None
         return dx, dw, None
 
 
@@ -377,9 +385,9 @@ class _MambaMixer(torch.autograd.Function):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         ba.workspace, ba.workspace_bytes = ws.data_ptr(), ws_bytes
         _lib.check((lib.mss_cbwd if cplx else lib.mss_bwd)(ba, stream), "scan backward")
-        dw_dt = _mm_fp32(ddt, x_dbl[:r].t())
+        dw_dt = _wgrad_mm(ddt, x_dbl[:r])
         _proj_mm(w_dt_act.t(), ddt, out=dx_dbl[:r])
-        dw_x = _mm_fp32(dx_dbl, u.t())
+        dw_x = _wgrad_mm(dx_dbl, u)
         _proj_mm(w_x_act.t(), dx_dbl, out=du, accumulate=True)  # du += W_x^T dx_dbl
         dconv_w = torch.empty_like(conv_w)
         dconv_b = None if conv_b is None else torch.empty_like(conv_b)
@@ -391,7 +399,7 @@ class _MambaMixer(torch.autograd.Function):
         cws = torch.empty(cws_bytes, dtype=torch.uint8, device=dev)
         ca.workspace, ca.workspace_bytes = cws.data_ptr(), cws_bytes
         _lib.check(lib.mss_conv_bwd(ca, stream), "mss_conv_bwd")
-        dw_xz = _mm_fp32(dxz, x.t())
+        dw_xz = _wgrad_mm(dxz, x)
         dx = torch.mm(w_xz_act.t(), dxz)
         return (dx, dw_xz[:di], dw_xz[di:], dconv_w, dconv_b, dw_x, dw_dt, dA, dD, dbias,
                 None, None, None, None, None, None)

@@ -11,8 +11,13 @@ float32 sums rounded to bf16 once (mss_proj). W may be the transposed view of a 
 
 ``proj_fits`` says whether a call has a shape and layout these kernels take (rows
 contiguous, 16-byte aligned, row strides multiples of 8; the shape limits of
-include/mamba_selective_scan.h); callers use a library GEMM for the others, and for the
-weight gradients.
+include/mamba_selective_scan.h); callers use a library GEMM for the others.
+
+``wgrad(dY, X, out=None, accumulate=False) -> C`` — the weight gradient of a dense
+projection over channel-major activations, C = dY @ X^T (+ C) in float32 for dY (M, T) and
+X (N, T), bf16 with contiguous rows (mss_wgrad: the tokens split over workgroups, partial
+tiles added in a fixed order). ``wgrad_fits`` says whether the shape and layout fit (M and N
+multiples of 192, T of 64); callers use a library GEMM for the others.
 """
 from __future__ import annotations
 
@@ -21,7 +26,7 @@ import torch
 from . import _lib
 from .selective_scan_hip import _require_gpu, _stream
 
-__all__ = ["proj", "proj_fits"]
+__all__ = ["proj", "proj_fits", "wgrad", "wgrad_fits"]
 
 
 def _rows_ok(t):
@@ -64,4 +69,35 @@ def proj(W, X, out=None, accumulate=False):
     a = _lib.ProjArgs(M=M, K=K, T=T, accumulate=int(bool(accumulate)), w_trans=int(trans), ldw=Wr.stride(0),
                       ldx=X.stride(0), ldc=out.stride(0), W=Wr.data_ptr(), X=X.data_ptr(), C=out.data_ptr())
     _lib.check(lib.mss_proj(a, _stream(X)), "mss_proj")
+    return out
+
+
+def wgrad_fits(dY, X, out=None):
+    if not (_rows_ok(dY) and _rows_ok(X)) or dY.shape[1] != X.shape[1]:
+        return False
+    if out is not None and not (out.dtype == torch.float32 and out.dim() == 2 and out.stride(1) == 1
+                                and out.stride(0) % 4 == 0 and out.data_ptr() % 16 == 0):
+        return False
+    M, N, T = dY.shape[0], X.shape[0], X.shape[1]
+    return M % 192 == 0 and N % 192 == 0 and T % 64 == 0 and T > 0
+
+
+def wgrad(dY, X, out=None, accumulate=False):
+    """C = dY @ X^T (+ C when accumulate), float32 (M, N), for bf16 dY (M, T) and X (N, T) with
+    contiguous rows. Raises _lib.MSSError for shapes mss_wgrad does not take (check
+    wgrad_fits first)."""
+    _require_gpu(dY, X)
+    M, T = dY.shape
+    N = X.shape[0]
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs an output to add to")
+        out = torch.empty(M, N, dtype=torch.float32, device=X.device)
+    lib = _lib.register_hip_kernel()
+    ws_bytes = int(lib.mss_wgrad_workspace_bytes(M, N, T))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=X.device) if ws_bytes > 0 else None
+    a = _lib.WgradArgs(M=M, N=N, K=T, accumulate=int(bool(accumulate)), lda=dY.stride(0), ldb=X.stride(0),
+                       ldc=out.stride(0), A=dY.data_ptr(), B=X.data_ptr(), C=out.data_ptr(),
+                       workspace=ws.data_ptr() if ws is not None else None, workspace_bytes=ws_bytes)
+    _lib.check(lib.mss_wgrad(a, _stream(X)), "mss_wgrad")
     return out

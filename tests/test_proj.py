@@ -1,5 +1,7 @@
-"""Skinny projection GEMMs of the training step (mss_proj): the S6 input projections
-(mamba/mamba1.py:52-67, 107-124) and their input gradients on the matrix cores.
+"""Projection GEMMs of the training step: mss_proj (the S6 input projections,
+mamba/mamba1.py:52-67, 107-124, and their input gradients) and mss_wgrad (the weight
+gradients dW = dY X^T of the block's dense projections, float32, tokens split over
+workgroups) on the matrix cores.
 
 CPU: argument validation (rejected calls only, before any launch) and the shape gates.
 GPU: against float32 products computed on the CPU from the same bf16 values —
@@ -11,12 +13,17 @@ GPU: against float32 products computed on the CPU from the same bf16 values —
   * the weight passed transposed gives the same bits; strided row views (a row slice of a
     wider matrix as X or C); repeated calls bit for bit; the config-5 mixer's four products
     take these kernels.
+mss_wgrad, against float32 / float64 products on the CPU: small-integer operands give the
+exact product (and old C + product when accumulating) bit for bit, at the config-5 shapes,
+with uneven token splits, with the workgroup count not a multiple of the XCD count, and with
+one split (no partial planes); random operands within 2^-13 sum|terms| of the float64
+product; repeated calls bit for bit (fixed-order sums); strided views.
 """
 import pytest
 import torch
 
 from mamba_amd import _lib
-from mamba_amd.proj import proj, proj_fits
+from mamba_amd.proj import proj, proj_fits, wgrad, wgrad_fits
 
 
 @pytest.fixture(scope="module")
@@ -50,6 +57,46 @@ def test_fits_gates_cpu_tensors():
     w = torch.zeros(80, 1536, dtype=torch.bfloat16)
     x = torch.zeros(1536, 4096, dtype=torch.bfloat16)
     assert not proj_fits(w, x)  # not on a GPU
+
+
+def _wgrad_base(lib, **kw):
+    M, N, K = kw.get("M", 3072), kw.get("N", 768), kw.get("K", 16384)
+    base = dict(M=M, N=N, K=K, accumulate=0, lda=16384, ldb=16384, ldc=768, A=1 << 32, B=1 << 36, C=1 << 40,
+                workspace=1 << 41, workspace_bytes=int(lib.mss_wgrad_workspace_bytes(M, N, K)))
+    base.update(kw)
+    return _lib.WgradArgs(**base)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(M=0), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(A=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(C=None), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(lda=1000), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(ldc=700), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(ldc=770), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(ldb=16388), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(B=(1 << 36) + 8), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(M=3000), _lib.MSS_ERR_UNSUPPORTED), (dict(N=700), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(K=16100), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(workspace=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(workspace_bytes=1 << 20), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(C=(1 << 32) + 4096), _lib.MSS_ERR_INVALID_ARGUMENT),  # C inside A
+    (dict(C=(1 << 41) + 4096), _lib.MSS_ERR_INVALID_ARGUMENT),  # C inside the workspace
+])
+def test_wgrad_validation(lib, kw, status):
+    assert lib.mss_wgrad(_wgrad_base(lib, **kw), None) == status
+
+
+def test_wgrad_workspace_bytes(lib):
+    """splits x M x N float32 partial planes, the split count filling the 256 CUs once with
+    at least 4 k-stages of 64 per split; 0 for one split and for unsupported shapes."""
+    assert lib.mss_wgrad_workspace_bytes(3072, 768, 16384) == 4 * 3072 * 768 * 4      # 64 tiles x 4
+    assert lib.mss_wgrad_workspace_bytes(768, 1536, 16384) == 8 * 768 * 1536 * 4      # 32 tiles x 8
+    assert lib.mss_wgrad_workspace_bytes(960, 1152, 4160) == 9 * 960 * 1152 * 4       # 30 tiles x 9
+    assert lib.mss_wgrad_workspace_bytes(576, 384, 8192) == 32 * 576 * 384 * 4        # 6 tiles, 128 stages
+    assert lib.mss_wgrad_workspace_bytes(192, 1920, 320) == 0                          # 5 stages: 1 split
+    assert lib.mss_wgrad_workspace_bytes(3000, 768, 16384) == 0
+    assert lib.mss_wgrad_workspace_bytes(192, 192, 100) == 0
+
+
+def test_wgrad_fits_gates_cpu_tensors():
+    assert not wgrad_fits(torch.zeros(3072, 1024, dtype=torch.bfloat16), torch.zeros(768, 1024, dtype=torch.bfloat16))
 
 
 # ------------------------------------------------------------------------------ GPU
@@ -143,3 +190,61 @@ def test_model_projection_shapes_take_the_kernels():
     w_dt = torch.empty(di, r, dtype=torch.bfloat16, device=dev)
     assert proj_fits(w_x, u) and proj_fits(w_dt, x_dbl[:r])
     assert proj_fits(w_dt.t(), u, x_dbl[:r]) and proj_fits(w_x.t(), x_dbl, u)
+
+
+WGRAD_SHAPES = [  # (M, N, K): config-5 in_proj / out_proj gradients; uneven splits and a
+    # workgroup count that is not a multiple of 8 (960 x 1152: 30 tiles x 9 splits over 65
+    # stages); one split (direct store); tall and wide tile grids
+    (3072, 768, 16384), (768, 1536, 16384), (960, 1152, 4160), (192, 192, 64), (192, 1920, 320),
+    (576, 384, 8192), (1536, 192, 640),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", WGRAD_SHAPES)
+def test_wgrad_exact_small_integers(M, N, K):
+    gen = torch.Generator().manual_seed(M * 5 + N * 3 + K)
+    A, B = _ints((M, K), gen), _ints((N, K), gen)
+    want = A.float() @ B.float().t()  # exact: |sums| < 2^24
+    got = wgrad(A.cuda(), B.cuda())
+    assert torch.equal(got.cpu(), want)
+    old = _ints((M, N), gen, -1000, 1000).float()
+    out = old.cuda()
+    wgrad(A.cuda(), B.cuda(), out=out, accumulate=True)
+    assert torch.equal(out.cpu(), old + want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(768, 1536, 16384), (960, 1152, 4160), (192, 1920, 320)])
+def test_wgrad_random(M, N, K):
+    gen = torch.Generator().manual_seed(2000 + M + N + K)
+    A, B = _randn((M, K), gen), _randn((N, K), gen)
+    ref = A.double() @ B.double().t()
+    terms = A.double().abs() @ B.double().abs().t()
+    got = wgrad(A.cuda(), B.cuda())
+    err = (got.cpu().double() - ref).abs()
+    assert bool((err <= 2.0 ** -13 * terms).all()), float((err / terms).max())
+    again = wgrad(A.cuda(), B.cuda())
+    assert torch.equal(got, again)  # the partial tiles are added in a fixed order
+
+
+@pytest.mark.gpu
+def test_wgrad_views_and_fits():
+    """dY as a row slice of a wider matrix (the model's dxz rows), C as a column block of a
+    wider float32 matrix (ldc > N): the columns outside it untouched; the config-5 in- and
+    out-projection gradients fit the kernel, the S6 input projections' do not."""
+    gen = torch.Generator().manual_seed(9)
+    K = 1024
+    big = _ints((768, K), gen).cuda()
+    X = _ints((384, K), gen).cuda()
+    sink = torch.full((384, 384 + 64), 5.0, device="cuda")
+    wgrad(big[192:576], X, out=sink[:, :384])
+    assert torch.equal(sink[:, :384].cpu(), big[192:576].cpu().float() @ X.cpu().float().t())
+    assert bool((sink[:, 384:] == 5.0).all())
+    T = 16384
+    dxz = torch.empty(3072, T, dtype=torch.bfloat16, device="cuda")
+    x = torch.empty(768, T, dtype=torch.bfloat16, device="cuda")
+    dy = torch.empty(768, T, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(1536, T, dtype=torch.bfloat16, device="cuda")
+    assert wgrad_fits(dxz, x) and wgrad_fits(dy, y)
+    assert not wgrad_fits(torch.empty(80, T, dtype=torch.bfloat16, device="cuda"), y)
