@@ -10,10 +10,11 @@
 //                       and the dt-rank gradient W_dt^T dDelta)
 //   proj_expand_kernel  C[M][T] (+)= W[M][K] X[K][T], K <= 128 (the dt-projection, and the
 //                       x-projection's input gradient W_x^T dx_dbl added into du)
-// (The weight gradients, A B^T over the tokens, stay with the library GEMM: a kernel of
-// this family that split the tokens over workgroups and summed partial tiles in a fixed
-// order measured 23.4 / 28.8 us against the library's 22.4 / 21.7 at the config-5 shapes,
-// the short operand re-read by every output block.)
+// (These projections' weight gradients, A B^T over the tokens with an 80- or 48-wide side,
+// stay with the library GEMM: a kernel of this family that split the tokens over workgroups
+// and summed partial tiles in a fixed order measured 23.4 / 28.8 us against the library's
+// 22.4 / 21.7 at the config-5 shapes, the short operand re-read by every output block. The
+// block's wide projections' weight gradients run on mss_wgrad.hip.)
 //
 // Instruction: v_mfma_f32_16x16x16_bf16. Operand layout (lane l, element e of its 4):
 // A[i][k] at l = i + 16 (k / 4), e = k % 4; B[k][j] at l = j + 16 (k / 4), e = k % 4;
