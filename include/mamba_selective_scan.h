@@ -409,12 +409,13 @@ typedef struct mss_proj_args {
 int mss_proj(const mss_proj_args* args, void* stream);
 
 /* --- Weight-gradient GEMM of the training step (bf16 operands, float32 output). -------
- * No counterpart symbol in the reference: the gradients of its dense projections
- * (mamba/mamba1.py:272-276, 330-337) are XLA dot products.
+ * No counterpart symbol in the reference: the gradients of its block projections
+ * (mamba/mamba1.py:52-67, 107-124, 272-276, 330-337) are XLA dot products.
  *
  * mss_wgrad: C[M][N] = A[M][K] B[N][K]^T (+ C when accumulate != 0), float32, i.e.
  * dW = dY X^T over channel-major activations (rows contiguous along K, the tokens).
- * M and N multiples of 192, K a multiple of 64; A, B 16-byte aligned with lda, ldb >= K,
+ * N a multiple of 4, K a multiple of 64 (192 x 192 output tiles, partial at the edges);
+ * A, B 16-byte aligned with lda, ldb >= K,
  * multiples of 8 (elements); C 16-byte aligned with ldc >= N, a multiple of 4; C overlapping
  * neither operand nor the workspace. The tokens are split over workgroups and the partial
  * tiles added in a fixed order (results do not depend on timing): `workspace` holds

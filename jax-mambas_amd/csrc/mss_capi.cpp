@@ -737,7 +737,7 @@ int mss_proj(const mss_proj_args* a, void* stream) {
 namespace {
 // The split count of a supported weight-gradient shape, 0 for shapes the kernel does not take.
 int wgrad_shape_splits(int32_t M, int32_t N, int32_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || M % mss::kWgradTile != 0 || N % mss::kWgradTile != 0 || K % 64 != 0) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || N % 4 != 0 || K % 64 != 0) return 0;
   return mss::wgrad_splits(M, N, K);
 }
 }  // namespace

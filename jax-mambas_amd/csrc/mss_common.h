@@ -344,9 +344,9 @@ struct ProjParams {
 };
 
 // Weight-gradient GEMM C[M][N] (+)= A[M][K] B[N][K]^T, bf16 operands with K-contiguous rows,
-// float32 output; K split over `splits` workgroups per output tile, whose partial tiles
-// ([splits][M][N] float32 in `workspace`) a second kernel adds in order. M and N multiples of
-// kWgradTile, K a multiple of 64.
+// float32 output; K split over `splits` workgroups per kWgradTile-square output tile (partial
+// at the edges), whose partial tiles ([splits][M][N] float32 in `workspace`) a second kernel
+// adds in order. N a multiple of 4, K a multiple of 64.
 constexpr int kWgradTile = 192;
 struct WgradParams {
   int M, N, K, splits, accumulate;

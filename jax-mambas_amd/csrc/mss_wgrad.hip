@@ -2,7 +2,10 @@
 // with bf16 operands whose rows are contiguous along K (the tokens) and float32 output, i.e.
 // dW = dY X^T for a linear layer over channel-major activations [features][tokens]. In the
 // reference these are the gradients XLA forms for the Mamba block's dense projections
-// (mamba/mamba1.py:272-276, 330-337: in_proj over [x; z], out_proj).
+// (mamba/mamba1.py:272-276, 330-337: in_proj over [x; z], out_proj) and for the S6 input
+// projections (s_B / s_C / Linear_R stacked as one x-projection, Linear_Delta; :52-67,
+// 107-124). Tiles at the M / N edges are partial (rows past the edge read the last row and
+// their outputs are dropped).
 //
 // The output is small (at the 130M shape 3072 x 768 and 768 x 1536) and the contraction long
 // (16384 tokens), so a library tiling that gives one workgroup per output tile leaves most of
@@ -61,7 +64,8 @@ __global__ __launch_bounds__(kWgThreads) void wgrad_kernel(WgradParams p) {
   const int wt = w & 3, wk = w >> 2;  // sub-tile, half of the k steps
   const int wm = wt & 1, wn = wt >> 1;
   const int j = lane & 31, g = lane >> 5;
-  const int tiles_m = p.M / kWgTile, tiles_n = p.N / kWgTile, tiles = tiles_m * tiles_n;
+  const int tiles_m = (p.M + kWgTile - 1) / kWgTile, tiles_n = (p.N + kWgTile - 1) / kWgTile;
+  const int tiles = tiles_m * tiles_n;
   const int nwg = tiles * p.splits;
   const int id = blockIdx.x;
   const int lin = nwg % 8 == 0 ? (id & 7) * (nwg / 8) + (id >> 3) : id;
@@ -82,7 +86,8 @@ __global__ __launch_bounds__(kWgThreads) void wgrad_kernel(WgradParams p) {
   const bf16_t* __restrict__ A = static_cast<const bf16_t*>(p.A);
   const bf16_t* __restrict__ B = static_cast<const bf16_t*>(p.B);
 
-  // Stage kk: slot i * 64 + lane of each operand = row slot / 8, stored chunk slot % 8.
+  // Stage kk: slot i * 64 + lane of each operand = row slot / 8, stored chunk slot % 8. Rows
+  // past M (N) re-read the last row: finite values whose products land in discarded outputs.
   auto issue = [&](int kk, u32x4* dA, u32x4* dB) {
     const int k0 = kk * 64;
 #pragma unroll
@@ -90,7 +95,7 @@ __global__ __launch_bounds__(kWgThreads) void wgrad_kernel(WgradParams p) {
       const int i = w + kWgWaves * t;
       const int slot = i * 64 + lane;
       const int row = slot >> 3, c = (slot & 7) ^ wg_swz(row);
-      const bf16_t* src = A + static_cast<size_t>(m0 + row) * p.lda + k0 + 8 * c;
+      const bf16_t* src = A + static_cast<size_t>(min(m0 + row, p.M - 1)) * p.lda + k0 + 8 * c;
       __builtin_amdgcn_global_load_lds((gbl_void_t)src, (lds_void_t)(dA + i * 64), 16, 0, 0);
     }
 #pragma unroll
@@ -98,7 +103,7 @@ __global__ __launch_bounds__(kWgThreads) void wgrad_kernel(WgradParams p) {
       const int i = w + kWgWaves * t;
       const int slot = i * 64 + lane;
       const int row = slot >> 3, c = (slot & 7) ^ wg_swz(row);
-      const bf16_t* src = B + static_cast<size_t>(n0 + row) * p.ldb + k0 + 8 * c;
+      const bf16_t* src = B + static_cast<size_t>(min(n0 + row, p.N - 1)) * p.ldb + k0 + 8 * c;
       __builtin_amdgcn_global_load_lds((gbl_void_t)src, (lds_void_t)(dB + i * 64), 16, 0, 0);
     }
   };
@@ -200,6 +205,7 @@ __global__ __launch_bounds__(kWgThreads) void wgrad_kernel(WgradParams p) {
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * kWgSub + 32 * mt + 8 * (r >> 2) + 4 * g + (r & 3);
         const int col = n0 + wn * kWgSub + 32 * nt + j;
+        if (row >= p.M || col >= p.N) continue;
         float* dst = out + static_cast<size_t>(row) * ldo + col;
         float v = acc[mt][nt][r];
         if (direct && p.accumulate) v += *dst;
@@ -232,7 +238,7 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
 }  // namespace
 
 int wgrad_splits(int M, int N, int K) {
-  const int tiles = (M / kWgTile) * (N / kWgTile);
+  const int tiles = ((M + kWgTile - 1) / kWgTile) * ((N + kWgTile - 1) / kWgTile);
   const int ks = K / 64;
   int s = (kCUs + tiles / 2) / tiles;  // one pass of one workgroup per CU (144 KB of LDS each)
   s = s < ks / 4 ? s : ks / 4;         // at least 4 stages per split
@@ -240,7 +246,7 @@ int wgrad_splits(int M, int N, int K) {
 }
 
 hipError_t launch_wgrad(const WgradParams& p, hipStream_t stream) {
-  const int nwg = (p.M / kWgTile) * (p.N / kWgTile) * p.splits;
+  const int nwg = ((p.M + kWgTile - 1) / kWgTile) * ((p.N + kWgTile - 1) / kWgTile) * p.splits;
   hipLaunchKernelGGL(wgrad_kernel, dim3(nwg), dim3(kWgThreads), 0, stream, p);
   if (p.splits > 1) {
     const long long total = static_cast<long long>(p.M) * (p.N / 4);

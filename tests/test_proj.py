@@ -16,8 +16,9 @@ GPU: against float32 products computed on the CPU from the same bf16 values —
 mss_wgrad, against float32 / float64 products on the CPU: small-integer operands give the
 exact product (and old C + product when accumulating) bit for bit, at the config-5 shapes,
 with uneven token splits, with the workgroup count not a multiple of the XCD count, and with
-one split (no partial planes); random operands within 2^-13 sum|terms| of the float64
-product; repeated calls bit for bit (fixed-order sums); strided views.
+one split (no partial planes), with partial edge tiles (the S6 projections' 80- and 48-wide
+gradients); random operands within 2^-13 sum|terms| of the float64 product; repeated calls
+bit for bit (fixed-order sums); strided views.
 """
 import pytest
 import torch
@@ -72,7 +73,7 @@ def _wgrad_base(lib, **kw):
     (dict(C=None), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(lda=1000), _lib.MSS_ERR_INVALID_ARGUMENT),
     (dict(ldc=700), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(ldc=770), _lib.MSS_ERR_INVALID_ARGUMENT),
     (dict(ldb=16388), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(B=(1 << 36) + 8), _lib.MSS_ERR_INVALID_ARGUMENT),
-    (dict(M=3000), _lib.MSS_ERR_UNSUPPORTED), (dict(N=700), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(N=702), _lib.MSS_ERR_UNSUPPORTED),
     (dict(K=16100), _lib.MSS_ERR_UNSUPPORTED),
     (dict(workspace=None), _lib.MSS_ERR_INVALID_ARGUMENT),
     (dict(workspace_bytes=1 << 20), _lib.MSS_ERR_INVALID_ARGUMENT),
@@ -91,7 +92,10 @@ def test_wgrad_workspace_bytes(lib):
     assert lib.mss_wgrad_workspace_bytes(960, 1152, 4160) == 9 * 960 * 1152 * 4       # 30 tiles x 9
     assert lib.mss_wgrad_workspace_bytes(576, 384, 8192) == 32 * 576 * 384 * 4        # 6 tiles, 128 stages
     assert lib.mss_wgrad_workspace_bytes(192, 1920, 320) == 0                          # 5 stages: 1 split
-    assert lib.mss_wgrad_workspace_bytes(3000, 768, 16384) == 0
+    assert lib.mss_wgrad_workspace_bytes(80, 1536, 16384) == 32 * 80 * 1536 * 4       # 1 x 8 partial tiles
+    assert lib.mss_wgrad_workspace_bytes(1536, 48, 16384) == 32 * 1536 * 48 * 4
+    assert lib.mss_wgrad_workspace_bytes(3000, 768, 16384) == 4 * 3000 * 768 * 4      # 16 x 4 tiles
+    assert lib.mss_wgrad_workspace_bytes(192, 702, 16384) == 0                         # N % 4
     assert lib.mss_wgrad_workspace_bytes(192, 192, 100) == 0
 
 
@@ -192,11 +196,13 @@ def test_model_projection_shapes_take_the_kernels():
     assert proj_fits(w_dt.t(), u, x_dbl[:r]) and proj_fits(w_x.t(), x_dbl, u)
 
 
-WGRAD_SHAPES = [  # (M, N, K): config-5 in_proj / out_proj gradients; uneven splits and a
-    # workgroup count that is not a multiple of 8 (960 x 1152: 30 tiles x 9 splits over 65
-    # stages); one split (direct store); tall and wide tile grids
-    (3072, 768, 16384), (768, 1536, 16384), (960, 1152, 4160), (192, 192, 64), (192, 1920, 320),
-    (576, 384, 8192), (1536, 192, 640),
+WGRAD_SHAPES = [  # (M, N, K): config-5 in_proj / out_proj / x_proj / dt_proj gradients;
+    # uneven splits and a workgroup count that is not a multiple of 8 (960 x 1152: 30 tiles x
+    # 9 splits over 65 stages); one split (direct store); tall and wide tile grids; partial
+    # edge tiles on either side or both
+    (3072, 768, 16384), (768, 1536, 16384), (80, 1536, 16384), (1536, 48, 16384), (960, 1152, 4160),
+    (192, 192, 64), (192, 1920, 320), (576, 384, 8192), (1536, 192, 640), (100, 196, 640), (1, 4, 64),
+    (200, 388, 1024),
 ]
 
 
@@ -215,7 +221,8 @@ def test_wgrad_exact_small_integers(M, N, K):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N,K", [(768, 1536, 16384), (960, 1152, 4160), (192, 1920, 320)])
+@pytest.mark.parametrize("M,N,K", [(768, 1536, 16384), (960, 1152, 4160), (192, 1920, 320), (80, 1536, 16384),
+                                   (200, 388, 1024)])
 def test_wgrad_random(M, N, K):
     gen = torch.Generator().manual_seed(2000 + M + N + K)
     A, B = _randn((M, K), gen), _randn((N, K), gen)
@@ -232,7 +239,8 @@ def test_wgrad_random(M, N, K):
 def test_wgrad_views_and_fits():
     """dY as a row slice of a wider matrix (the model's dxz rows), C as a column block of a
     wider float32 matrix (ldc > N): the columns outside it untouched; the config-5 in- and
-    out-projection gradients fit the kernel, the S6 input projections' do not."""
+    out-projection gradients take the kernel, the S6 projections' (80 and 48 wide, faster on
+    the library GEMM) do not."""
     gen = torch.Generator().manual_seed(9)
     K = 1024
     big = _ints((768, K), gen).cuda()
@@ -246,5 +254,8 @@ def test_wgrad_views_and_fits():
     x = torch.empty(768, T, dtype=torch.bfloat16, device="cuda")
     dy = torch.empty(768, T, dtype=torch.bfloat16, device="cuda")
     y = torch.empty(1536, T, dtype=torch.bfloat16, device="cuda")
+    u = torch.empty(1536, T, dtype=torch.bfloat16, device="cuda")
+    dx_dbl = torch.empty(80, T, dtype=torch.bfloat16, device="cuda")
     assert wgrad_fits(dxz, x) and wgrad_fits(dy, y)
-    assert not wgrad_fits(torch.empty(80, T, dtype=torch.bfloat16, device="cuda"), y)
+    assert not wgrad_fits(dx_dbl, u) and not wgrad_fits(u, dx_dbl[:48])
+    assert not wgrad_fits(dxz, torch.empty(462, T, dtype=torch.bfloat16, device="cuda"))  # N % 4
