@@ -178,7 +178,7 @@ def test_model_matches_oracle_on_gpu(euler, complex_ssm):
         scale = float(v.grad.abs().max())
         err = float((got - v.grad).abs().max())
         print(f"  grad {k:28s} max|g|={scale:.3e} max_err={err:.3e}", flush=True)
-        assert err <= 1e-3 * scale + 1e-7, k
+        assert err <= 1e-4 * scale + 1e-7, k  # measured <= 7e-6 of scale
 
 
 @pytest.mark.gpu
@@ -283,9 +283,10 @@ def test_c5_widths_one_layer_matches_oracle(act):
     1536, dt_rank 48, N 16, vocab 50280, B 8, L 2048): logits, loss and every parameter
     gradient against the float64 oracle model (sequential-scan option) on the CPU with the
     same weights. The layer's scan runs the 16-wave backward plan of every config-5 layer.
-    f32 activations: the config-1 bars (logits 1e-4, gradients 1e-3 of each tensor's scale);
+    f32 activations: the config-1 bars (logits 1e-4, gradients 1e-4 of each tensor's scale);
     bf16 activations (config 5's dtype: bf16 GEMM weights and activations, fp32 scan
-    accumulation, fp32 master gradients): logits 1e-2 and gradients 3e-2 of scale."""
+    accumulation, fp32 master gradients): logits 1e-2 and gradients 2e-2 of scale (measured:
+    at most 7e-6 and 6.2e-3)."""
     print(f"case c5 widths one layer act={act}", flush=True)
     cfg = C5
     st = _lib.Strides(io_batch=cfg["length"], io_dim=cfg["batch"] * cfg["length"], bc_batch=cfg["length"],
@@ -316,7 +317,7 @@ def test_c5_widths_one_layer_matches_oracle(act):
     err, scale = _max_err_over_scale(logits, ref_logits.detach())
     print(f"  logits max_err={err:.3e} max|ref|={scale:.3e} loss {loss.item():.6f} vs {ref_loss.item():.6f}",
           flush=True)
-    lt, gt = (1e-4, 1e-3) if act == "f32" else (1e-2, 3e-2)
+    lt, gt = (1e-4, 1e-4) if act == "f32" else (1e-2, 2e-2)
     assert err <= lt * scale + (1e-4 if act == "f32" else 0.0)
     assert abs(loss.item() - ref_loss.item()) <= (1e-5 if act == "f32" else 2e-3) * abs(ref_loss.item())
     for k, v in p.items():
