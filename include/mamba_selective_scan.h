@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 11
+#define MSS_ABI_VERSION 12
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -61,6 +61,7 @@ extern "C" {
 #define MSS_REF_CHUNK 2048   /* step granularity of the reference's chunk_states */
 #define MSS_NOALLOC_SCRATCH_BYTES (128u << 20) /* fixed per-device scratch of mss_bwd_noalloc */
 #define MSS_NORM_GEMV_MAX_FEATURES 1024 /* largest norm->features of mss_norm_gemv_conv_step */
+#define MSS_XENT_FUSED_MAX_VOCAB 65536 /* largest vocab of mss_xent_fwd_grad */
 
 typedef enum mss_status {
   MSS_OK = 0,
@@ -386,6 +387,16 @@ typedef struct mss_xent_args {
 
 int mss_xent_fwd(const mss_xent_args* args, void* stream);
 int mss_xent_bwd(const mss_xent_args* args, void* stream);
+
+/* Forward and backward in one pass over the logits (each row read once), for a loss that
+ * will be differentiated: loss and lse as mss_xent_fwd (the row's float32 partial sums
+ * merged in another fixed order, so within a few units of the last place of its lse), and
+ * dlogits = (*grad_scale) * (softmax - onehot) as mss_xent_bwd computes it from that lse. vocab % 8 == 0 and vocab <= MSS_XENT_FUSED_MAX_VOCAB, logits and dlogits 16-byte aligned and not
+ * overlapping; MSS_ERR_UNSUPPORTED for other shapes.
+ * mss_xent_rescale multiplies n bf16 values by *factor (a device scalar, e.g. the upstream
+ * gradient of the loss), rounding once, and does nothing when *factor == 1. */
+int mss_xent_fwd_grad(const mss_xent_args* args, void* stream);
+int mss_xent_rescale(void* dlogits, int64_t n, const float* factor, void* stream);
 
 /* --- Skinny projection GEMMs of the training step (bf16, float32 sums). ------------
  * No counterpart symbol in the reference: its S6 input projections (s_B, s_C, Linear_R:

@@ -38,6 +38,8 @@ hipError_t launch_norm_fwd(const NormParams& p, bool io_bf16, hipStream_t stream
 hipError_t launch_norm_bwd(const NormParams& p, bool io_bf16, float* dw, hipStream_t stream);
 int norm_blocks(int tokens);
 hipError_t launch_xent(const XentParams& p, bool bwd, bool vec, hipStream_t stream);
+hipError_t launch_xent_fused(const XentParams& p, hipStream_t stream);
+hipError_t launch_xent_rescale(bf16_t* dz, long long n, const float* factor, hipStream_t stream);
 hipError_t launch_ssm_step(const StepParams& p, bool zoh, bool io_bf16, bool bc_bf16, hipStream_t stream);
 hipError_t launch_conv_step(const ConvStepParams& p, bool io_bf16, hipStream_t stream);
 hipError_t launch_gemv(const GemvParams& p, hipStream_t stream);
@@ -656,6 +658,11 @@ int mss_norm_bwd(const mss_norm_args* args, void* stream) {
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching rmsnorm backward");
 }
 
+namespace {
+bool spans_overlap(const void* a, long long rows_a, long long ld_a, long long cols_a, const void* b,
+                   long long rows_b, long long ld_b, long long cols_b);
+}  // namespace
+
 static int validate_xent(const mss_xent_args* a, bool bwd) {
   if (a == nullptr || a->rows <= 0 || a->vocab <= 0) return MSS_ERR_INVALID_ARGUMENT;
   if (!a->logits || !a->targets || !a->lse) return MSS_ERR_INVALID_ARGUMENT;
@@ -687,6 +694,36 @@ int mss_xent_fwd(const mss_xent_args* args, void* stream) {
 int mss_xent_bwd(const mss_xent_args* args, void* stream) {
   const int s = validate_xent(args, true);
   return s != MSS_OK ? s : run_xent(args, true, static_cast<hipStream_t>(stream));
+}
+
+int mss_xent_fwd_grad(const mss_xent_args* a, void* stream) {
+  if (a == nullptr || a->rows <= 0 || a->vocab <= 0 || !a->logits || !a->targets || !a->lse || !a->loss ||
+      !a->grad_scale || !a->dlogits)
+    return MSS_ERR_INVALID_ARGUMENT;
+  static_assert(mss::kXentFusedMaxVocab == MSS_XENT_FUSED_MAX_VOCAB, "header and kernel disagree");
+  if (a->vocab % 8 != 0 || a->vocab > MSS_XENT_FUSED_MAX_VOCAB || !aligned16(a->logits) || !aligned16(a->dlogits))
+    return MSS_ERR_UNSUPPORTED;
+  const long long n = static_cast<long long>(a->rows) * a->vocab;
+  if (spans_overlap(a->logits, 1, 0, n, a->dlogits, 1, 0, n)) return MSS_ERR_INVALID_ARGUMENT;
+  mss::XentParams p{};
+  p.rows = a->rows;
+  p.vocab = a->vocab;
+  p.z = static_cast<const mss::bf16_t*>(a->logits);
+  p.target = reinterpret_cast<const long long*>(a->targets);
+  p.loss = a->loss;
+  p.lse = a->lse;
+  p.grad_scale = a->grad_scale;
+  p.dz = static_cast<mss::bf16_t*>(a->dlogits);
+  const hipError_t e = mss::launch_xent_fused(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching cross-entropy forward + gradient");
+}
+
+int mss_xent_rescale(void* dlogits, int64_t n, const float* factor, void* stream) {
+  if (!dlogits || !factor || n < 0) return MSS_ERR_INVALID_ARGUMENT;
+  if (n == 0) return MSS_OK;
+  const hipError_t e = mss::launch_xent_rescale(static_cast<mss::bf16_t*>(dlogits), n, factor,
+                                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching gradient rescale");
 }
 
 namespace {

@@ -317,6 +317,7 @@ struct NormParams {
   float* dw_part;       // [n_blocks][features]
 };
 
+constexpr int kXentFusedMaxVocab = 65536;  // rows the fused forward + gradient holds in registers
 struct XentParams {
   int rows, vocab;
   const bf16_t* z;

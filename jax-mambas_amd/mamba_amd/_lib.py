@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 11
+MSS_ABI_VERSION = 12
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -30,6 +30,7 @@ MSS_MAX_DSTATE_WIDE = 256  # float32 real-A scans (backward over groups of MSS_M
 MSS_SEG_STEPS = 8
 MSS_REF_CHUNK = 2048
 MSS_NORM_GEMV_MAX_FEATURES = 1024
+MSS_XENT_FUSED_MAX_VOCAB = 65536
 
 # Every symbol include/mamba_selective_scan.h declares.
 EXPORTED_SYMBOLS = (
@@ -56,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "mss_norm_bwd",
     "mss_xent_fwd",
     "mss_xent_bwd",
+    "mss_xent_fwd_grad",
+    "mss_xent_rescale",
     "mss_scan_step",
     "mss_cscan_step",
     "mss_conv_step",
@@ -221,9 +224,11 @@ def register_hip_kernel(library_path=None):
         getattr(lib, name).restype = ctypes.c_int
     lib.mss_norm_bwd_workspace_bytes.argtypes = [ctypes.POINTER(NormArgs)]
     lib.mss_norm_bwd_workspace_bytes.restype = ctypes.c_size_t
-    for name in ("mss_xent_fwd", "mss_xent_bwd"):
+    for name in ("mss_xent_fwd", "mss_xent_bwd", "mss_xent_fwd_grad"):
         getattr(lib, name).argtypes = [ctypes.POINTER(XentArgs), _p]
         getattr(lib, name).restype = ctypes.c_int
+    lib.mss_xent_rescale.argtypes = [_p, ctypes.c_int64, _p, _p]
+    lib.mss_xent_rescale.restype = ctypes.c_int
     for name in ("mss_scan_step", "mss_cscan_step"):
         getattr(lib, name).argtypes = [ctypes.POINTER(StepArgs), _p]
         getattr(lib, name).restype = ctypes.c_int

@@ -106,10 +106,51 @@ class _CrossEntropy(torch.autograd.Function):
         return dlogits, None
 
 
+class _CrossEntropyFused(torch.autograd.Function):
+    """The loss and its gradient for the mean in one pass over the logits
+    (mss_xent_fwd_grad); the backward only multiplies by the upstream gradient, and skips
+    even that when it is 1 (mss_xent_rescale checks on the device). The logits are not kept."""
+
+    @staticmethod
+    def forward(ctx, logits, targets):
+        lib = _lib.register_hip_kernel()
+        rows, vocab = logits.shape
+        loss = torch.empty(rows, dtype=torch.float32, device=logits.device)
+        lse = torch.empty(rows, dtype=torch.float32, device=logits.device)
+        scale = torch.full((1,), 1.0 / rows, dtype=torch.float32, device=logits.device)
+        dlogits = torch.empty_like(logits)
+        a = _lib.XentArgs(rows=rows, vocab=vocab, logits=logits.data_ptr(), targets=targets.data_ptr(),
+                          loss=loss.data_ptr(), lse=lse.data_ptr(), grad_scale=scale.data_ptr(),
+                          dlogits=dlogits.data_ptr())
+        _lib.check(lib.mss_xent_fwd_grad(a, _stream(logits)), "mss_xent_fwd_grad")
+        ctx.save_for_backward(dlogits)
+        return loss.mean()
+
+    @staticmethod
+    def backward(ctx, grad):
+        lib = _lib.register_hip_kernel()
+        (dlogits,) = ctx.saved_tensors
+        factor = grad.float().reshape(1).contiguous()
+        _lib.check(lib.mss_xent_rescale(dlogits.data_ptr(), dlogits.numel(), factor.data_ptr(), _stream(dlogits)),
+                   "mss_xent_rescale")
+        return dlogits, None
+
+
+def _fused_fits(logits):
+    return (logits.shape[1] % 8 == 0 and logits.shape[1] <= _lib.MSS_XENT_FUSED_MAX_VOCAB
+            and logits.data_ptr() % 16 == 0)
+
+
 def cross_entropy(logits, targets):
+    """Mean cross-entropy of bf16 (rows, vocab) logits against int64 targets. When the
+    result will be differentiated (grad enabled, logits requiring grad) and the row fits,
+    the loss and its gradient come from one pass over the logits."""
     if logits.dtype != torch.bfloat16 or logits.ndim != 2:
         raise TypeError("logits must be a bfloat16 (rows, vocab) matrix")
     if targets.dtype != torch.int64 or tuple(targets.shape) != (logits.shape[0],):
         raise ValueError(f"targets must be int64 with shape ({logits.shape[0]},)")
     _require_gpu(logits, targets)
-    return _CrossEntropy.apply(logits.contiguous(), targets.contiguous())
+    logits, targets = logits.contiguous(), targets.contiguous()
+    if torch.is_grad_enabled() and logits.requires_grad and _fused_fits(logits):
+        return _CrossEntropyFused.apply(logits, targets)
+    return _CrossEntropy.apply(logits, targets)

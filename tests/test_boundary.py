@@ -47,7 +47,7 @@ def test_library_exports_every_header_symbol(lib):
     version = int(re.search(r"#define MSS_ABI_VERSION (\d+)", header).group(1))
     assert lib.mss_abi_version() == version == _lib.MSS_ABI_VERSION
     for name in ("MSS_MAX_DSTATE", "MSS_MAX_DSTATE_WIDE", "MSS_SEG_STEPS", "MSS_REF_CHUNK",
-                 "MSS_NORM_GEMV_MAX_FEATURES"):
+                 "MSS_NORM_GEMV_MAX_FEATURES", "MSS_XENT_FUSED_MAX_VOCAB"):
         value = int(re.search(rf"#define {name} (\d+)", header).group(1))
         assert getattr(_lib, name) == value, name
 

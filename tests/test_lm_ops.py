@@ -4,7 +4,9 @@ RMSNorm follows mamba/mamba1.py:300-337 (nnx.RMSNorm(epsilon=1e-5) before each b
 block output added back); the loss is the training step's softmax cross-entropy
 (experiments/mamba_inductionheads.py:129-136). CPU: argument validation. GPU: values and
 gradients against float64 references on the same inputs — the oracle's rmsnorm
-(oracle/mamba1_torch.py, pinned against torch.rms_norm) and torch's cross_entropy.
+(oracle/mamba1_torch.py, pinned against torch.rms_norm) and torch's cross_entropy; the
+one-pass loss + gradient (mss_xent_fwd_grad, taken when the loss will be differentiated)
+against the two-pass path: losses within float32 rounding, gradients within one bf16 step.
 fp32 activations within rtol 1e-4 / atol 1e-5 (the dweight sums over tokens on the
 tensor's scale); bf16 within 2e-2.
 """
@@ -14,7 +16,7 @@ import torch
 import torch.nn.functional as F
 
 from mamba_amd import _lib
-from mamba_amd.lm_ops import add_rmsnorm, cross_entropy
+from mamba_amd.lm_ops import _CrossEntropy, add_rmsnorm, cross_entropy
 from oracle import mamba1_torch as ref
 
 
@@ -45,6 +47,21 @@ def test_xent_validation(lib, kw):
     assert lib.mss_xent_fwd(_lib.XentArgs(**base), None) == _lib.MSS_ERR_INVALID_ARGUMENT
     assert lib.mss_xent_bwd(_lib.XentArgs(rows=4, vocab=10, logits=1, targets=1, lse=1), None) == \
         _lib.MSS_ERR_INVALID_ARGUMENT  # no grad_scale / dlogits
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(dlogits=None), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(grad_scale=None), _lib.MSS_ERR_INVALID_ARGUMENT),
+    (dict(loss=None), _lib.MSS_ERR_INVALID_ARGUMENT), (dict(vocab=1003), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(vocab=65544), _lib.MSS_ERR_UNSUPPORTED), (dict(logits=(1 << 32) + 8), _lib.MSS_ERR_UNSUPPORTED),
+    (dict(dlogits=(1 << 32) + 64), _lib.MSS_ERR_INVALID_ARGUMENT),  # overlaps the logits
+])
+def test_xent_fused_validation(lib, kw, status):
+    base = dict(rows=4, vocab=1000, logits=1 << 32, targets=1 << 36, loss=1 << 37, lse=1 << 38, grad_scale=1 << 39,
+                dlogits=1 << 40)
+    base.update(kw)
+    assert lib.mss_xent_fwd_grad(_lib.XentArgs(**base), None) == status
+    assert lib.mss_xent_rescale(None, 10, 1 << 39, None) == _lib.MSS_ERR_INVALID_ARGUMENT
+    assert lib.mss_xent_rescale(1 << 40, 10, None, None) == _lib.MSS_ERR_INVALID_ARGUMENT
 
 
 def test_python_errors():
@@ -128,5 +145,38 @@ def test_cross_entropy(vocab):
 @pytest.mark.gpu
 def test_cross_entropy_bad_target_is_nan():
     z = torch.randn(4, 64, dtype=torch.bfloat16, device="cuda")
+    loss = cross_entropy(z, torch.tensor([0, 1, 64, 2], device="cuda"))
+    assert torch.isnan(loss).item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vocab,rows", [(50280, 64), (1000, 37), (65536, 5), (8, 3)])
+def test_cross_entropy_one_pass_matches_two_pass(vocab, rows):
+    """The one-pass loss + gradient (a loss that will be differentiated, upstream gradient 1:
+    the backward leaves the stored gradient as it is) against the two-pass kernels on the same
+    logits: losses within float32 rounding of the row sums, gradients within one bf16 step of
+    the value (both are one rounding of the same softmax); against float64 torch as above."""
+    print(f"case cross_entropy one pass vocab={vocab} rows={rows}", flush=True)
+    g = torch.Generator().manual_seed(vocab + rows)
+    z = (3 * torch.randn(rows, vocab, generator=g)).to(torch.bfloat16).cuda()
+    tg = torch.randint(0, vocab, (rows,), generator=g).cuda()
+    z1 = z.clone().requires_grad_(True)
+    l1 = cross_entropy(z1, tg)  # one pass
+    l1.backward()
+    z2 = z.clone().requires_grad_(True)
+    l2 = _CrossEntropy.apply(z2, tg)  # two passes
+    l2.backward()
+    torch.cuda.synchronize()
+    assert abs(l1.item() - l2.item()) <= 1e-6 * abs(l2.item())
+    d1, d2 = z1.grad.float(), z2.grad.float()
+    assert bool(((d1 - d2).abs() <= 2.0 ** -7 * d2.abs() + 1e-12).all())
+    zr = z.cpu().double().requires_grad_(True)
+    F.cross_entropy(zr, tg.cpu()).backward()
+    _bound_check("dlogits", d1, zr.grad, 1e-2, 1e-5 / rows)
+
+
+@pytest.mark.gpu
+def test_cross_entropy_one_pass_bad_target_is_nan():
+    z = torch.randn(4, 64, dtype=torch.bfloat16, device="cuda", requires_grad=True)
     loss = cross_entropy(z, torch.tensor([0, 1, 64, 2], device="cuda"))
     assert torch.isnan(loss).item()
