@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 12
+#define MSS_ABI_VERSION 13
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -444,6 +444,27 @@ typedef struct mss_wgrad_args {
 
 int64_t mss_wgrad_workspace_bytes(int32_t M, int32_t N, int32_t K);
 int mss_wgrad(const mss_wgrad_args* args, void* stream);
+
+/* --- bf16 shadows of float32 master weights, refreshed once per training step. --------
+ * No counterpart symbol in the reference (its parameters are used in their own dtype).
+ * For each entry: dst = bf16(src) (round to nearest even) when dst is not NULL, and
+ * dst_t[c * ld_t + r] = bf16(src[r][c]) when dst_t is not NULL (the transposed copy the
+ * input-gradient GEMMs W^T dY read as a contiguous operand). src is [rows][cols] float32
+ * with rows contiguous, dst [rows][cols] bf16. The table lives in DEVICE memory (built once,
+ * read by every refresh, e.g. each replay of a captured step); entries are 64 x 64 tiles
+ * numbered consecutively: entry i covers tiles [tile0_i, tile0_i + ceil(rows/64) *
+ * ceil(cols/64)), tile0 increasing from 0, n_tiles the total. The table is not checked
+ * here (it is device memory); one launch refreshes every entry. */
+typedef struct mss_shadow_entry {
+  const float* src;
+  void* dst;
+  void* dst_t;
+  int32_t rows, cols;
+  int64_t ld_t;
+  int64_t tile0;
+} mss_shadow_entry;
+
+int mss_shadow_refresh(const mss_shadow_entry* entries, int32_t n_entries, int64_t n_tiles, void* stream);
 
 
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------

@@ -11,6 +11,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <cstddef>
 #include <mutex>
 #include <string>
 
@@ -45,6 +46,7 @@ hipError_t launch_conv_step(const ConvStepParams& p, bool io_bf16, hipStream_t s
 hipError_t launch_gemv(const GemvParams& p, hipStream_t stream);
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 hipError_t launch_wgrad(const WgradParams& p, hipStream_t stream);
+hipError_t launch_shadow_refresh(const ShadowParams& p, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -818,6 +820,22 @@ int mss_wgrad(const mss_wgrad_args* a, void* stream) {
   p.workspace = static_cast<float*>(a->workspace);
   const hipError_t e = mss::launch_wgrad(p, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching weight-gradient GEMM");
+}
+
+
+static_assert(sizeof(mss_shadow_entry) == sizeof(mss::ShadowEntry) &&
+                  offsetof(mss_shadow_entry, ld_t) == offsetof(mss::ShadowEntry, ld_t) &&
+                  offsetof(mss_shadow_entry, tile0) == offsetof(mss::ShadowEntry, tile0),
+              "public and kernel shadow entries share one layout");
+
+int mss_shadow_refresh(const mss_shadow_entry* entries, int32_t n_entries, int64_t n_tiles, void* stream) {
+  if (!entries || n_entries <= 0 || n_tiles <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  mss::ShadowParams p{};
+  p.entries = reinterpret_cast<const mss::ShadowEntry*>(entries);
+  p.n_entries = n_entries;
+  p.n_tiles = n_tiles;
+  const hipError_t e = mss::launch_shadow_refresh(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching shadow refresh");
 }
 
 

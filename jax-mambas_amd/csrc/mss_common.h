@@ -359,6 +359,21 @@ struct WgradParams {
 };
 int wgrad_splits(int M, int N, int K);  // the split count launch_wgrad expects
 
+// bf16 shadows of float32 weights (layout of mss_shadow_entry in the public header).
+struct ShadowEntry {
+  const float* src;
+  bf16_t* dst;
+  bf16_t* dst_t;
+  int rows, cols;
+  long long ld_t;
+  long long tile0;
+};
+struct ShadowParams {
+  const ShadowEntry* entries;  // device memory
+  int n_entries;
+  long long n_tiles;
+};
+
 struct StepParams {
   int batch, dim, dstate, delta_softplus;
   long long io_sb, io_sd, bc_sb, bc_sn;

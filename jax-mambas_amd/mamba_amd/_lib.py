@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 12
+MSS_ABI_VERSION = 13
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -69,6 +69,7 @@ EXPORTED_SYMBOLS = (
     "mss_proj",
     "mss_wgrad_workspace_bytes",
     "mss_wgrad",
+    "mss_shadow_refresh",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -157,6 +158,11 @@ class WgradArgs(ctypes.Structure):
     _fields_ = [("M", _i32), ("N", _i32), ("K", _i32), ("accumulate", _i32), ("lda", ctypes.c_int64),
                 ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64), ("A", _p), ("B", _p), ("C", _p), ("workspace", _p),
                 ("workspace_bytes", ctypes.c_int64)]
+
+
+class ShadowEntry(ctypes.Structure):
+    _fields_ = [("src", _p), ("dst", _p), ("dst_t", _p), ("rows", _i32), ("cols", _i32), ("ld_t", ctypes.c_int64),
+                ("tile0", ctypes.c_int64)]
 
 
 class ConvStepArgs(ctypes.Structure):
@@ -249,6 +255,8 @@ def register_hip_kernel(library_path=None):
     lib.mss_wgrad_workspace_bytes.restype = ctypes.c_int64
     lib.mss_wgrad.argtypes = [ctypes.POINTER(WgradArgs), _p]
     lib.mss_wgrad.restype = ctypes.c_int
+    lib.mss_shadow_refresh.argtypes = [_p, _i32, ctypes.c_int64, _p]
+    lib.mss_shadow_refresh.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

@@ -78,19 +78,22 @@ def _proj_mm(w, x, out=None, accumulate=False):
 
 class _WeightMM(torch.autograd.Function):
     """y = W_act @ x with a low-precision shadow W_act of the float32 master weight W:
-    dx = W_act^T dy; dW = dy x^T, produced in float32 for the master weight."""
+    dx = W_act^T dy (from the contiguous transposed shadow W_act_t when given); dW = dy x^T,
+    produced in float32 for the master weight."""
 
     @staticmethod
-    def forward(ctx, x, w, w_act):
-        ctx.save_for_backward(x, w_act)
+    def forward(ctx, x, w, w_act, w_act_t=None):
+        ctx.save_for_backward(x, w_act, w_act_t)
         return w_act @ x
 
     @staticmethod
     def backward(ctx, dy):
-        x, w_act = ctx.saved_tensors
-        dx = w_act.t() @ dy if ctx.needs_input_grad[0] else None
+        x, w_act, w_act_t = ctx.saved_tensors
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = w_act_t @ dy if w_act_t is not None else w_act.t() @ dy
         dw = _wgrad_mm(dy, x) if ctx.needs_input_grad[1] else None
-        return dx, dw, None
+        return dx, dw, None, None
 
 
 class _TiedHeadMM(torch.autograd.Function):
@@ -111,30 +114,90 @@ class _TiedHeadMM(torch.autograd.Function):
 
 
 class ShadowWeights:
-    """Low-precision copies of float32 weights, refreshed together in one multi-tensor
-    copy per step (instead of one cast per weight per use, plus one per gradient). The
-    copies are views of one buffer in the order given (offsets padded to 64 elements), so
-    consecutive weights with the same column count can be used as one stacked matrix."""
+    """Low-precision copies of float32 weights, refreshed together once per step (instead of
+    one cast per weight per use, plus one per gradient). The copies are views of one buffer
+    in the order given (offsets padded to 64 elements), so consecutive weights with the same
+    column count can be used as one stacked matrix. `transposed` lists groups of such
+    consecutive weights whose stacked matrix is also kept transposed and contiguous (the
+    operand layout the input-gradient GEMMs W^T dY run fastest on). In bf16 on the GPU the
+    refresh is one HIP launch over a device table (mss_shadow_refresh) writing both copies."""
 
-    def __init__(self, params):
+    def __init__(self, params, transposed=()):
         self.params = list(params)
+        self.groups = [tuple(g) for g in transposed]
         self.bufs = None
         self.flat = None
+        self.tflat = None
         self.offsets = {}
         self.by_id = {}
+        self.t_by_key = {}
+        self._table = None   # (device entry table, n_entries, n_tiles, master pointers)
+
+    def _layout(self, dtype):
+        offs, off = [], 0
+        for p in self.params:
+            offs.append(off)
+            off += (p.numel() + 63) // 64 * 64
+        dev = self.params[0].device
+        self.flat = torch.empty(off, dtype=dtype, device=dev)
+        self.bufs = [self.flat[o:o + p.numel()].view(p.shape) for o, p in zip(offs, self.params)]
+        self.by_id = {id(p): b for p, b in zip(self.params, self.bufs)}
+        self.offsets = {id(p): o for p, o in zip(self.params, offs)}
+        toff, self._tslot = 0, {}   # id(w) -> (offset of its group, column offset, group rows)
+        gspec = []
+        for g in self.groups:
+            cols, rows = g[0].shape[1], sum(w.shape[0] for w in g)
+            gspec.append((toff, cols, rows))
+            c = 0
+            for w in g:
+                self._tslot[id(w)] = (toff, c, rows)
+                c += w.shape[0]
+            toff += (cols * rows + 63) // 64 * 64
+        self.tflat = torch.empty(max(toff, 1), dtype=dtype, device=dev)
+        self.t_by_key = {tuple(id(w) for w in g): self.tflat[o:o + c * r].view(c, r)
+                         for g, (o, c, r) in zip(self.groups, gspec)}
+        self._table = None
+
+    def _native_table(self):
+        """The device table of mss_shadow_refresh, rebuilt when a master moved."""
+        ptrs = tuple(p.data_ptr() for p in self.params)
+        if self._table is not None and self._table[3] == ptrs:
+            return self._table
+        entries, tile0 = [], 0
+        esz = self.flat.element_size()
+        for p, b in zip(self.params, self.bufs):
+            rows, cols = (p.shape[0], p.shape[1]) if p.dim() == 2 else (1, p.numel())
+            dst_t, ld_t = None, 0
+            if id(p) in self._tslot:
+                o, c, r = self._tslot[id(p)]
+                dst_t, ld_t = self.tflat.data_ptr() + (o + c) * esz, r
+            entries.append(_lib.ShadowEntry(src=p.data_ptr(), dst=b.data_ptr(), dst_t=dst_t, rows=rows, cols=cols,
+                                            ld_t=ld_t, tile0=tile0))
+            tile0 += ((rows + 63) // 64) * ((cols + 63) // 64)
+        raw = (_lib.ShadowEntry * len(entries))(*entries)
+        table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.flat.device)
+        self._table = (table, len(entries), tile0, ptrs)
+        return self._table
 
     def refresh(self, dtype):
         if self.bufs is None or self.flat.dtype != dtype:
-            offs, off = [], 0
-            for p in self.params:
-                offs.append(off)
-                off += (p.numel() + 63) // 64 * 64
-            self.flat = torch.empty(off, dtype=dtype, device=self.params[0].device)
-            self.bufs = [self.flat[o:o + p.numel()].view(p.shape) for o, p in zip(offs, self.params)]
-            self.by_id = {id(p): b for p, b in zip(self.params, self.bufs)}
-            self.offsets = {id(p): o for p, o in zip(self.params, offs)}
+            self._layout(dtype)
+        native = (dtype == torch.bfloat16 and self.flat.is_cuda
+                  and all(p.dtype == torch.float32 and p.is_contiguous() for p in self.params))
         with torch.no_grad():
+            if native:
+                table, n, tiles, _ = self._native_table()
+                lib = _lib.register_hip_kernel()
+                _lib.check(lib.mss_shadow_refresh(table.data_ptr(), n, tiles, _stream(self.flat)),
+                           "mss_shadow_refresh")
+                return
             torch._foreach_copy_(self.bufs, [p.detach() for p in self.params])
+            for g in self.groups:
+                self.t_by_key[tuple(id(w) for w in g)].copy_(torch.cat([w.detach() for w in g]).t())
+
+    def stacked_t(self, *ws):
+        """The contiguous transpose of the stacked shadows of ws, when kept, else None."""
+        return self.t_by_key.get(tuple(id(w) for w in ws)) if self.t_by_key else None
 
     def stacked(self, *ws):
         """The shadows of ws as one (sum of rows, cols) matrix when they lie back to back,
@@ -166,10 +229,11 @@ class ShadowWeights:
         return self.mm(w, x)
 
     def mm(self, w, x):
-        """w @ x: plain autograd in float32, else through the shadow of w."""
+        """w @ x: plain autograd in float32, else through the shadow of w (and its transposed
+        shadow for the input gradient, when kept)."""
         if x.dtype == torch.float32 or not self.by_id:
             return w.to(x.dtype) @ x
-        return _WeightMM.apply(x, w, self.by_id[id(w)])
+        return _WeightMM.apply(x, w, self.by_id[id(w)], self.stacked_t(w))
 
     def head(self, x, e):
         if x.dtype == torch.float32 or not self.by_id:
@@ -310,7 +374,7 @@ class _MambaMixer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w_in, w_z, conv_w, conv_b, w_x, w_dt, A, D, dt_bias, w_xz_act, w_x_act, w_dt_act,
-                batch, seq_lens, zoh):
+                batch, seq_lens, zoh, w_xz_t=None):
         lib = _lib.register_hip_kernel()
         di, T = w_in.shape[0], x.shape[1]
         r = w_dt.shape[1]
@@ -345,7 +409,7 @@ class _MambaMixer(torch.autograd.Function):
                           last_state=rv(last), carries=rv(carries), y_pre=y_pre.data_ptr(), strides=st)
         _lib.check((lib.mss_cfwd if cplx else lib.mss_fwd)(fa, stream), "scan forward")
         ctx.save_for_backward(x, xz, u, x_dbl, dt, carries, y_pre, A, D, dt_bias, conv_w, conv_b,
-                              w_xz_act, w_x_act, w_dt_act, seq_lens)
+                              w_xz_act, w_x_act, w_dt_act, seq_lens, w_xz_t)
         ctx.batch, ctx.zoh, ctx.dims = batch, zoh, (di, r, n, L)
         ctx.mark_non_differentiable(last, xz)
         ctx.set_materialize_grads(False)  # no zero-filled gradients for last / xz
@@ -355,7 +419,7 @@ class _MambaMixer(torch.autograd.Function):
     def backward(ctx, dy, _dlast, _dxz):
         lib = _lib.register_hip_kernel()
         (x, xz, u, x_dbl, dt, carries, y_pre, A, D, dt_bias, conv_w, conv_b, w_xz_act, w_x_act, w_dt_act,
-         seq_lens) = ctx.saved_tensors
+         seq_lens, w_xz_t) = ctx.saved_tensors
         di, r, n, L = ctx.dims
         batch = ctx.batch
         T = x.shape[1]
@@ -400,9 +464,9 @@ class _MambaMixer(torch.autograd.Function):
         ca.workspace, ca.workspace_bytes = cws.data_ptr(), cws_bytes
         _lib.check(lib.mss_conv_bwd(ca, stream), "mss_conv_bwd")
         dw_xz = _wgrad_mm(dxz, x)
-        dx = torch.mm(w_xz_act.t(), dxz)
+        dx = torch.mm(w_xz_t if w_xz_t is not None else w_xz_act.t(), dxz)
         return (dx, dw_xz[:di], dw_xz[di:], dconv_w, dconv_b, dw_x, dw_dt, dA, dD, dbias,
-                None, None, None, None, None, None)
+                None, None, None, None, None, None, None)
 
 
 class MambaBlock(nn.Module):
@@ -439,14 +503,17 @@ class MambaBlock(nn.Module):
         h, x = self.norm(h, delta, act_dtype)
         s6 = self.s6
         w_xz = weights.stacked(self.in_proj, self.z_proj)
+        w_xz_t = None
         if w_xz is None or w_xz.dtype != act_dtype:
             w_xz = torch.cat([self.in_proj.detach(), self.z_proj.detach()]).to(act_dtype)
+        else:
+            w_xz_t = weights.stacked_t(self.in_proj, self.z_proj)
         A = s6.a_matrix() if A is None else A
         y, last, xz = _MambaMixer.apply(
             x, self.in_proj, self.z_proj, self.conv_weight, self.conv_bias, s6.x_proj, s6.dt_proj, A,
             None if s6.D is None else s6.D.float(), s6.dt_bias.float(), w_xz,
             weights.act(s6.x_proj, act_dtype), weights.act(s6.dt_proj, act_dtype), batch, seq_lens,
-            s6.discretization == "zoh")
+            s6.discretization == "zoh", w_xz_t)
         if not torch.is_grad_enabled():  # inference: keep the decode caches of this prompt
             xin = xz[:self.in_proj.shape[0]]
             k = self.conv_weight.shape[1]
@@ -489,7 +556,8 @@ class MambaLM(nn.Module):
                        device=device)
             for _ in range(n_layers))
         self.final_norm = RMSNormCM(d_model, device=device)
-        self._shadows = ShadowWeights([self.embedding] + [w for b in self.blocks for w in b.gemm_weights()])
+        self._shadows = ShadowWeights([self.embedding] + [w for b in self.blocks for w in b.gemm_weights()],
+                                      transposed=[g for b in self.blocks for g in ((b.in_proj, b.z_proj), (b.out_proj,))])
 
     def forward(self, tokens, seq_lens=None, act_dtype=torch.bfloat16, shadow_weights=True):
         """tokens (B, L) int64 -> logits (B*L, vocab) in act_dtype (rows in (b, t) order).
