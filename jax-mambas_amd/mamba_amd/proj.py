@@ -79,10 +79,10 @@ def wgrad_fits(dY, X, out=None):
                                 and out.stride(0) % 4 == 0 and out.data_ptr() % 16 == 0):
         return False
     M, (N, T) = dY.shape[0], X.shape
-    # The kernel takes any M and N % 4 == 0 (partial edge tiles); below one 192-wide tile on
-    # either side most of each tile's products are discarded and the library GEMM is faster
-    # (config-5 x_proj / dt_proj gradients, 80 x 1536 and 1536 x 48: 31.5 / 28.8 us against
-    # 21.5 / 21.1, MI355X), so those stay with it.
+    # The kernel takes any M and N % 4 == 0 (96 x 96 tiles when a side is below 192); for the
+    # config-5 S6 projections' gradients (80 x 1536 and 1536 x 48 over 16384 tokens) the
+    # library GEMM stays faster (kernel + sums 27.5-28.5 us against 21.5, MI355X), so
+    # shapes with a side below 192 are left to it.
     return N % 4 == 0 and T % 64 == 0 and T > 0 and M >= 192 and N >= 192
 
 

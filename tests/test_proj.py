@@ -16,8 +16,8 @@ GPU: against float32 products computed on the CPU from the same bf16 values —
 mss_wgrad, against float32 / float64 products on the CPU: small-integer operands give the
 exact product (and old C + product when accumulating) bit for bit, at the config-5 shapes,
 with uneven token splits, with the workgroup count not a multiple of the XCD count, and with
-one split (no partial planes), with partial edge tiles (the S6 projections' 80- and 48-wide
-gradients); random operands within 2^-13 sum|terms| of the float64 product; repeated calls
+one split (no partial planes), with partial edge tiles, on 96 x 96 tiles (a side below 192:
+the S6 projections' 80- and 48-wide gradients); random operands within 2^-13 sum|terms| of the float64 product; repeated calls
 bit for bit (fixed-order sums); strided views.
 """
 import pytest
@@ -86,14 +86,18 @@ def test_wgrad_validation(lib, kw, status):
 
 def test_wgrad_workspace_bytes(lib):
     """splits x M x N float32 partial planes, the split count filling the 256 CUs once with
-    at least 4 k-stages of 64 per split; 0 for one split and for unsupported shapes."""
+    at least 4 k-stages per split (192 x 192 tiles with 64-deep stages; 96 x 96 when a side is
+    below 192, with 128-deep stages when K allows); 0 for one split and for unsupported shapes."""
     assert lib.mss_wgrad_workspace_bytes(3072, 768, 16384) == 4 * 3072 * 768 * 4      # 64 tiles x 4
     assert lib.mss_wgrad_workspace_bytes(768, 1536, 16384) == 8 * 768 * 1536 * 4      # 32 tiles x 8
     assert lib.mss_wgrad_workspace_bytes(960, 1152, 4160) == 9 * 960 * 1152 * 4       # 30 tiles x 9
     assert lib.mss_wgrad_workspace_bytes(576, 384, 8192) == 32 * 576 * 384 * 4        # 6 tiles, 128 stages
     assert lib.mss_wgrad_workspace_bytes(192, 1920, 320) == 0                          # 5 stages: 1 split
-    assert lib.mss_wgrad_workspace_bytes(80, 1536, 16384) == 32 * 80 * 1536 * 4       # 1 x 8 partial tiles
-    assert lib.mss_wgrad_workspace_bytes(1536, 48, 16384) == 32 * 1536 * 48 * 4
+    # a side below 192: 96 x 96 tiles
+    assert lib.mss_wgrad_workspace_bytes(80, 1536, 16384) == 16 * 80 * 1536 * 4       # 1 x 16 partial tiles
+    assert lib.mss_wgrad_workspace_bytes(1536, 48, 16384) == 16 * 1536 * 48 * 4      # 16 x 1
+    assert lib.mss_wgrad_workspace_bytes(150, 1000, 4096) == 8 * 150 * 1000 * 4       # 2 x 11, 32 stages of 128
+    assert lib.mss_wgrad_workspace_bytes(100, 196, 576) == 2 * 100 * 196 * 4          # 9 stages of 64
     assert lib.mss_wgrad_workspace_bytes(3000, 768, 16384) == 4 * 3000 * 768 * 4      # 16 x 4 tiles
     assert lib.mss_wgrad_workspace_bytes(192, 702, 16384) == 0                         # N % 4
     assert lib.mss_wgrad_workspace_bytes(192, 192, 100) == 0
@@ -202,7 +206,7 @@ WGRAD_SHAPES = [  # (M, N, K): config-5 in_proj / out_proj / x_proj / dt_proj gr
     # edge tiles on either side or both
     (3072, 768, 16384), (768, 1536, 16384), (80, 1536, 16384), (1536, 48, 16384), (960, 1152, 4160),
     (192, 192, 64), (192, 1920, 320), (576, 384, 8192), (1536, 192, 640), (100, 196, 640), (1, 4, 64),
-    (200, 388, 1024),
+    (200, 388, 1024), (150, 1000, 4096), (100, 196, 576),
 ]
 
 
@@ -222,7 +226,7 @@ def test_wgrad_exact_small_integers(M, N, K):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K", [(768, 1536, 16384), (960, 1152, 4160), (192, 1920, 320), (80, 1536, 16384),
-                                   (200, 388, 1024)])
+                                   (200, 388, 1024), (1536, 48, 16384), (150, 1000, 4096)])
 def test_wgrad_random(M, N, K):
     gen = torch.Generator().manual_seed(2000 + M + N + K)
     A, B = _randn((M, K), gen), _randn((N, K), gen)
