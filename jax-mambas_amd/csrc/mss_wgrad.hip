@@ -302,10 +302,10 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
 
 }  // namespace
 
-int wgrad_tile(int M, int N) { return M >= kWgradTile && N >= kWgradTile ? kWgradTile : kWgSub; }
+static int wgrad_tile(int M, int N) { return M >= kWgradTile && N >= kWgradTile ? kWgradTile : kWgSub; }
 // Stage depth: 128 k (256-byte row pieces, fewer DRAM page visits) for the 96 x 96 tiles of the
 // skinny, memory-bound shapes when K allows, else 64.
-int wgrad_bk(int M, int N, int K) { return wgrad_tile(M, N) == kWgSub && K % 128 == 0 ? 128 : 64; }
+static int wgrad_bk(int M, int N, int K) { return wgrad_tile(M, N) == kWgSub && K % 128 == 0 ? 128 : 64; }
 
 int wgrad_splits(int M, int N, int K) {
   const int t = wgrad_tile(M, N);
