@@ -189,64 +189,97 @@ __global__ __launch_bounds__((kMB + 2) * 64) void proj_reduce_kernel(ProjParams 
 
 // ---------------------------------------------------------------------------------------
 // C[M][T] (+)= W[M][K] X[K][T] for K = 16 kKB <= 128 and M % 16 == 0. A workgroup of 4 waves
-// covers 64 tokens x 128 rows, each wave two 16-row tiles; every operand is loaded before
-// the first product (K is short), X transposed in registers. kTrans: the weight given as
-// W^T [K][M], its 4 k of a row read as four 2-byte loads (the weight is small and cached).
+// covers 64 tokens x kExpandTiles 16-row tiles: each wave loads the 64-token X block once
+// (transposed in registers into the B operands of all of K) and walks the workgroup's tiles
+// w, w + 4, ..., loading the next tile's W rows (and, accumulating, the C values to add to)
+// while it computes and stores the current one, so the output streams out without a wait
+// on a fresh X block per tile. kTrans: the weight given as W^T [K][M], its 4 k of a row
+// read as four 2-byte loads (the weight is small and cached).
+constexpr int kExpandWaveTiles = 6;  // 16-row tiles per wave
+constexpr int kExpandCAhead = 6;     // accumulating: tiles whose C values are loaded ahead
+constexpr int kExpandTiles = 4 * kExpandWaveTiles;
+
 template <int kKB, bool kTrans>
+__device__ __forceinline__ void expand_load_w(const bf16_t* __restrict__ W, long long ldw, int row, int g,
+                                              uint2 (&wr)[kKB]) {
+#pragma unroll
+  for (int kb = 0; kb < kKB; ++kb) {
+    if constexpr (kTrans) {
+      const uint16_t* src = reinterpret_cast<const uint16_t*>(W) + static_cast<size_t>(16 * kb + 4 * g) * ldw + row;
+      wr[kb].x = static_cast<uint32_t>(src[0]) | (static_cast<uint32_t>(src[ldw]) << 16);
+      wr[kb].y = static_cast<uint32_t>(src[2 * ldw]) | (static_cast<uint32_t>(src[3 * ldw]) << 16);
+    } else {
+      wr[kb] = *reinterpret_cast<const uint2*>(W + static_cast<size_t>(row) * ldw + 16 * kb + 4 * g);
+    }
+  }
+}
+
+template <int kKB, bool kTrans, bool kAcc>
 __global__ __launch_bounds__(256) void proj_expand_kernel(ProjParams p) {
+  constexpr int kWT = kExpandWaveTiles;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int T0 = blockIdx.x * 64;
-  const int mt0 = (blockIdx.y * 4 + w) * 2;  // the wave's first 16-row tile
   const int n_mt = p.M / 16;
+  const int mt0 = blockIdx.y * kExpandTiles + w;  // the wave's tiles: mt0 + 4 i
   if (mt0 >= n_mt) return;
-  const bool two = mt0 + 1 < n_mt;
+  const int n_t = min(kWT, (n_mt - mt0 + 3) / 4);  // wave-uniform
   const bf16_t* __restrict__ X = static_cast<const bf16_t*>(p.X);
   const bf16_t* __restrict__ W = static_cast<const bf16_t*>(p.W);
-  uint2 xr[kKB][4], wr[kKB][2];
+  bf16_t* __restrict__ C = static_cast<bf16_t*>(p.C) + T0 + 4 * j;
+  auto crow = [&](int i, int e) { return C + static_cast<size_t>(16 * (mt0 + 4 * i) + 4 * g + e) * p.ldc; };
+  uint2 cr[kAcc ? kWT : 1][4];
+  if constexpr (kAcc) {
 #pragma unroll
-  for (int kb = 0; kb < kKB; ++kb) {
+    for (int i = 0; i < kExpandCAhead && i < kWT; ++i)
+      if (i < n_t)
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      xr[kb][e] = *reinterpret_cast<const uint2*>(X + static_cast<size_t>(16 * kb + 4 * g + e) * p.ldx + T0 + 4 * j);
+        for (int e = 0; e < 4; ++e) cr[i][e] = *reinterpret_cast<const uint2*>(crow(i, e));
+  }
+  pbf16x4 bo[kKB][4];
+  {
+    uint2 xr[kKB][4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int row = 16 * (two ? mt0 + t : mt0) + j;
-      if constexpr (kTrans) {
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(W) + static_cast<size_t>(16 * kb + 4 * g) * p.ldw + row;
-        wr[kb][t].x = static_cast<uint32_t>(src[0]) | (static_cast<uint32_t>(src[p.ldw]) << 16);
-        wr[kb][t].y = static_cast<uint32_t>(src[2 * p.ldw]) | (static_cast<uint32_t>(src[3 * p.ldw]) << 16);
-      } else {
-        wr[kb][t] = *reinterpret_cast<const uint2*>(W + static_cast<size_t>(row) * p.ldw + 16 * kb + 4 * g);
+    for (int kb = 0; kb < kKB; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xr[kb][e] = *reinterpret_cast<const uint2*>(X + static_cast<size_t>(16 * kb + 4 * g + e) * p.ldx + T0 + 4 * j);
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) transpose_4x4(xr[kb], bo[kb]);
+  }
+  uint2 wr[2][kKB];
+  expand_load_w<kKB, kTrans>(W, p.ldw, 16 * mt0 + j, g, wr[0]);
+#pragma unroll
+  for (int i = 0; i < kWT; ++i) {
+    if (i >= n_t) break;
+    if (i + 1 < n_t) expand_load_w<kKB, kTrans>(W, p.ldw, 16 * (mt0 + 4 * (i + 1)) + j, g, wr[(i + 1) & 1]);
+    if (kAcc && i + kExpandCAhead < kWT && i + kExpandCAhead < n_t) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cr[i + kExpandCAhead][e] = *reinterpret_cast<const uint2*>(crow(i + kExpandCAhead, e));
+    }
+    pf32x4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = pf32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      const pbf16x4 ao = pbf16x4_of(wr[i & 1][kb].x, wr[i & 1][kb].y);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = mfma16(ao, bo[kb][c], acc[c]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {  // row 16 (mt0 + 4 i) + 4 g + e, tokens 4 j .. 4 j + 3
+      float v[4] = {acc[0][e], acc[1][e], acc[2][e], acc[3][e]};
+      if constexpr (kAcc) {
+        v[0] += __uint_as_float(cr[i][e].x << 16);
+        v[1] += __uint_as_float(cr[i][e].x & 0xffff0000u);
+        v[2] += __uint_as_float(cr[i][e].y << 16);
+        v[3] += __uint_as_float(cr[i][e].y & 0xffff0000u);
       }
+      const uint2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      *reinterpret_cast<uint2*>(crow(i, e)) = o;
     }
-  }
-  pf32x4 acc[2][4];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[t][c] = pf32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int kb = 0; kb < kKB; ++kb) {
-    pbf16x4 bo[4];
-    transpose_4x4(xr[kb], bo);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const pbf16x4 ao = pbf16x4_of(wr[kb][t].x, wr[kb][t].y);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[t][c] = mfma16(ao, bo[c], acc[t][c]);
-    }
-  }
-  bf16_t* __restrict__ C = static_cast<bf16_t*>(p.C);
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if (t == 1 && !two) break;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      store_row4(C + static_cast<size_t>(16 * (mt0 + t) + 4 * g + e) * p.ldc + T0 + 4 * j, acc[t], e,
-                 p.accumulate != 0);
   }
 }
 
@@ -261,11 +294,16 @@ static void launch_reduce_t(const ProjParams& p, hipStream_t stream) {
 
 template <int kKB>
 static void launch_expand_t(const ProjParams& p, hipStream_t stream) {
-  const dim3 grid(p.T / 64, (p.M / 16 + 7) / 8);
-  if (p.w_trans)
-    hipLaunchKernelGGL((proj_expand_kernel<kKB, true>), grid, dim3(256), 0, stream, p);
+  const dim3 grid(p.T / 64, (p.M / 16 + kExpandTiles - 1) / kExpandTiles);
+  const bool acc = p.accumulate != 0;
+  if (p.w_trans && acc)
+    hipLaunchKernelGGL((proj_expand_kernel<kKB, true, true>), grid, dim3(256), 0, stream, p);
+  else if (p.w_trans)
+    hipLaunchKernelGGL((proj_expand_kernel<kKB, true, false>), grid, dim3(256), 0, stream, p);
+  else if (acc)
+    hipLaunchKernelGGL((proj_expand_kernel<kKB, false, true>), grid, dim3(256), 0, stream, p);
   else
-    hipLaunchKernelGGL((proj_expand_kernel<kKB, false>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((proj_expand_kernel<kKB, false, false>), grid, dim3(256), 0, stream, p);
 }
 
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream) {
