@@ -506,18 +506,20 @@ def run_train_c5(torch, steps, warmup, graph=True):
     """Config 5: one training step of the Mamba-1 130M-shape LM (random init, uniform random
     tokens): bf16 activations with fp32 master weights and residual stream, forward,
     cross-entropy (fp32 math on bf16 logits, HIP kernel) over all next-token positions,
-    backward (HIP scan, conv, norm and loss backward inside), fused AdamW step. Timed with
+    backward (HIP scan, conv, norm and loss backward inside), AdamW step (mss_adamw, which also
+    writes the bf16 copies of the GEMM weights the next forward reads). Timed with
     events on the current stream around exactly `steps` steps: first eagerly, then (graph)
     as one captured HIP graph replayed per step; `value` is the faster of the two (`launch`)."""
     from mamba_amd.lm_ops import cross_entropy
     from mamba_amd.mamba1 import GraphedTrainStep, MambaLM
+    from mamba_amd.optim import AdamW
 
     torch.manual_seed(0)
     m = C5_MODEL
     model = MambaLM(m["vocab"], m["d_model"], m["n_layers"], m["expand"], m["d_state"], m["dt_rank"],
                     m["d_conv"], device="cuda")
     n_params = sum(p.numel() for p in model.parameters())
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True, capturable=True)
+    opt = AdamW(model.parameters(), lr=1e-4, shadows=model.shadow_weights)
     gen = torch.Generator(device="cuda").manual_seed(0)
     tokens = torch.randint(0, m["vocab"], (C5_BATCH, C5_LENGTH + 1), device="cuda", generator=gen)
     inp = tokens[:, :-1].contiguous()
@@ -577,7 +579,7 @@ def run_train_c5(torch, steps, warmup, graph=True):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"model": "Mamba-1 130M shape", "params_m": round(n_params / 1e6, 2), **m,
-                   "global_batch": C5_BATCH, "seq_len": C5_LENGTH, "optimizer": "AdamW (fused)",
+                   "global_batch": C5_BATCH, "seq_len": C5_LENGTH, "optimizer": "AdamW (mss_adamw: one launch per step, writes the bf16 weight shadows)",
                    "parallelism": "none (1 GPU)"},
     }
 

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 13
+#define MSS_ABI_VERSION 14
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -465,6 +465,43 @@ typedef struct mss_shadow_entry {
 } mss_shadow_entry;
 
 int mss_shadow_refresh(const mss_shadow_entry* entries, int32_t n_entries, int64_t n_tiles, void* stream);
+
+/* --- AdamW over float32 master weights, writing their bf16 shadows. --------------------
+ * No counterpart symbol in the reference (its training step leaves the optimizer to the
+ * caller: optax, experiments/mamba_inductionheads.py:126-139). Updates every entry in float32,
+ * with decoupled weight decay (Loshchilov & Hutter) and bias-corrected moments:
+ *   p <- p (1 - lr wd);  m <- m + (1 - beta1)(g - m);  v <- beta2 v + (1 - beta2) g^2;
+ *   p <- p - lr / (1 - beta1^t) * m / (sqrt(v) / sqrt(1 - beta2^t) + eps),
+ * t the float32 at the entry's `step` (device memory; the caller advances it before the call,
+ * so a captured step replays with the right count). Then shadow = bf16(p) where shadow is not
+ * NULL, and shadow_t[c * ld_t + r] = bf16(p[r][c]) where shadow_t is not NULL (as
+ * mss_shadow_refresh). The entry array is HOST memory, read during the call: entries travel
+ * to the GPU as kernel arguments, up to 40 per launch, so nothing is allocated or copied
+ * and a captured call replays as it was made. Per entry: param, grad, exp_avg, exp_avg_sq
+ * (numel float32 each) 16-byte aligned, shadow (bf16) 8-byte aligned; with shadow_t, the
+ * parameter is [rows][cols] (rows * cols == numel, cols a multiple of 4) and shadow_t
+ * 16-byte aligned with ld_t >= rows a multiple of 8. MSS_ERR_INVALID_ARGUMENT otherwise,
+ * before any launch. Entries must not overlap one another. */
+typedef struct mss_adamw_entry {
+  float* param;
+  const float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  const float* step;
+  void* shadow;
+  void* shadow_t;
+  int32_t rows, cols;
+  int64_t ld_t;
+  int64_t numel;
+} mss_adamw_entry;
+
+typedef struct mss_adamw_args {
+  const mss_adamw_entry* entries;
+  int32_t n_entries;
+  float lr, beta1, beta2, eps, weight_decay;
+} mss_adamw_args;
+
+int mss_adamw(const mss_adamw_args* args, void* stream);
 
 
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------

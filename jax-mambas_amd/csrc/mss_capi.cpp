@@ -11,7 +11,9 @@
 
 #include <cstdint>
 #include <cstring>
+#include <cmath>
 #include <cstddef>
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -47,6 +49,7 @@ hipError_t launch_gemv(const GemvParams& p, hipStream_t stream);
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 hipError_t launch_wgrad(const WgradParams& p, hipStream_t stream);
 hipError_t launch_shadow_refresh(const ShadowParams& p, hipStream_t stream);
+hipError_t launch_adamw(const AdamWParams& p, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -836,6 +839,62 @@ int mss_shadow_refresh(const mss_shadow_entry* entries, int32_t n_entries, int64
   p.n_tiles = n_tiles;
   const hipError_t e = mss::launch_shadow_refresh(p, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MSS_OK : hip_fail(e, "launching shadow refresh");
+}
+
+static_assert(sizeof(mss_adamw_entry) == sizeof(mss::AdamWEntry) &&
+                  offsetof(mss_adamw_entry, step) == offsetof(mss::AdamWEntry, step) &&
+                  offsetof(mss_adamw_entry, shadow_t) == offsetof(mss::AdamWEntry, shadow_t) &&
+                  offsetof(mss_adamw_entry, rows) == offsetof(mss::AdamWEntry, rows) &&
+                  offsetof(mss_adamw_entry, numel) == offsetof(mss::AdamWEntry, numel),
+              "public and kernel AdamW entries share one layout");
+
+namespace {
+// Work units of a valid entry (flat 4096-element runs, or 64 x 64 tiles with a transposed
+// shadow), 0 for an invalid one.
+long long adamw_units(const mss_adamw_entry& e) {
+  if (!e.param || !e.grad || !e.exp_avg || !e.exp_avg_sq || !e.step || e.numel <= 0 || e.numel >= (1LL << 40))
+    return 0;
+  if (!aligned16(e.param) || !aligned16(e.grad) || !aligned16(e.exp_avg) || !aligned16(e.exp_avg_sq) ||
+      (e.shadow && !aligned8(e.shadow)))
+    return 0;
+  if (!e.shadow_t) return (e.numel + mss::kAdamWUnit - 1) / mss::kAdamWUnit;
+  if (e.rows <= 0 || e.cols <= 0 || e.cols % 4 != 0 || static_cast<long long>(e.rows) * e.cols != e.numel ||
+      e.ld_t < e.rows || e.ld_t % 8 != 0 || !aligned16(e.shadow_t))
+    return 0;
+  return static_cast<long long>((e.rows + 63) / 64) * ((e.cols + 63) / 64);
+}
+}  // namespace
+
+int mss_adamw(const mss_adamw_args* a, void* stream) {
+  if (!a || !a->entries || a->n_entries <= 0) return MSS_ERR_INVALID_ARGUMENT;
+  const bool finite = std::isfinite(a->lr) && std::isfinite(a->beta1) && std::isfinite(a->beta2) &&
+                      std::isfinite(a->eps) && std::isfinite(a->weight_decay);
+  if (!finite || a->lr < 0.f || a->beta1 < 0.f || a->beta1 >= 1.f || a->beta2 < 0.f || a->beta2 >= 1.f ||
+      a->eps <= 0.f || a->weight_decay < 0.f)
+    return MSS_ERR_INVALID_ARGUMENT;
+  for (int32_t i = 0; i < a->n_entries; ++i)
+    if (adamw_units(a->entries[i]) == 0) return MSS_ERR_INVALID_ARGUMENT;
+  // Launches of up to kAdamWMaxEntries entries each, in order.
+  for (int32_t i0 = 0; i0 < a->n_entries; i0 += mss::kAdamWMaxEntries) {
+    mss::AdamWParams p{};
+    p.n = std::min(mss::kAdamWMaxEntries, a->n_entries - i0);
+    p.lr = a->lr;
+    p.beta1 = a->beta1;
+    p.beta2 = a->beta2;
+    p.eps = a->eps;
+    p.weight_decay = a->weight_decay;
+    long long u = 0;
+    for (int k = 0; k < p.n; ++k) {
+      std::memcpy(&p.e[k], &a->entries[i0 + k], sizeof(mss::AdamWEntry));
+      p.unit0[k] = u;
+      u += adamw_units(a->entries[i0 + k]);
+    }
+    p.unit0[p.n] = u;
+    if (u >= (1LL << 31)) return MSS_ERR_UNSUPPORTED;
+    const hipError_t e = mss::launch_adamw(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "launching AdamW");
+  }
+  return MSS_OK;
 }
 
 

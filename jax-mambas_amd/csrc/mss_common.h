@@ -374,6 +374,30 @@ struct ShadowParams {
   long long n_tiles;
 };
 
+// AdamW over float32 masters with bf16 shadows (layout of mss_adamw_entry in the public
+// header). A launch takes up to kAdamWMaxEntries entries by value in its arguments (so a
+// captured launch needs no table in device memory); unit0[i] is entry i's first work unit.
+struct AdamWEntry {
+  float* param;
+  const float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  const float* step;  // the step number of this update (1 on the first)
+  bf16_t* shadow;     // may be null
+  bf16_t* shadow_t;   // may be null: then flat 4096-element units, else 64 x 64 tiles
+  int rows, cols;
+  long long ld_t;
+  long long numel;
+};
+constexpr int kAdamWMaxEntries = 40;
+constexpr int kAdamWUnit = 4096;
+struct AdamWParams {
+  AdamWEntry e[kAdamWMaxEntries];
+  long long unit0[kAdamWMaxEntries + 1];
+  int n;
+  float lr, beta1, beta2, eps, weight_decay;
+};
+
 struct StepParams {
   int batch, dim, dstate, delta_softplus;
   long long io_sb, io_sd, bc_sb, bc_sn;

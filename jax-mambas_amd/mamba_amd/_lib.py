@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 13
+MSS_ABI_VERSION = 14
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -70,6 +70,7 @@ EXPORTED_SYMBOLS = (
     "mss_wgrad_workspace_bytes",
     "mss_wgrad",
     "mss_shadow_refresh",
+    "mss_adamw",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -165,6 +166,16 @@ class ShadowEntry(ctypes.Structure):
                 ("tile0", ctypes.c_int64)]
 
 
+class AdamWEntry(ctypes.Structure):
+    _fields_ = [("param", _p), ("grad", _p), ("exp_avg", _p), ("exp_avg_sq", _p), ("step", _p), ("shadow", _p),
+                ("shadow_t", _p), ("rows", _i32), ("cols", _i32), ("ld_t", ctypes.c_int64), ("numel", ctypes.c_int64)]
+
+
+class AdamWArgs(ctypes.Structure):
+    _fields_ = [("entries", _p), ("n_entries", _i32), ("lr", ctypes.c_float), ("beta1", ctypes.c_float),
+                ("beta2", ctypes.c_float), ("eps", ctypes.c_float), ("weight_decay", ctypes.c_float)]
+
+
 class ConvStepArgs(ctypes.Structure):
     _fields_ = [
         ("batch", _i32), ("dim", _i32), ("width", _i32), ("io_dtype", _i32), ("activation", _i32),
@@ -257,6 +268,8 @@ def register_hip_kernel(library_path=None):
     lib.mss_wgrad.restype = ctypes.c_int
     lib.mss_shadow_refresh.argtypes = [_p, _i32, ctypes.c_int64, _p]
     lib.mss_shadow_refresh.restype = ctypes.c_int
+    lib.mss_adamw.argtypes = [ctypes.POINTER(AdamWArgs), _p]
+    lib.mss_adamw.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

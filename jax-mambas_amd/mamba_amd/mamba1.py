@@ -132,6 +132,7 @@ class ShadowWeights:
         self.by_id = {}
         self.t_by_key = {}
         self._table = None   # (device entry table, n_entries, n_tiles, master pointers)
+        self._current = None  # the masters' (pointer, version) when the copies last matched them
 
     def _layout(self, dtype):
         offs, off = [], 0
@@ -179,9 +180,36 @@ class ShadowWeights:
         self._table = (table, len(entries), tile0, ptrs)
         return self._table
 
+    def _token(self):
+        return tuple((p.data_ptr(), p._version) for p in self.params)
+
+    def is_current(self):
+        """Whether the copies match the masters: nothing replaced or changed a master in place
+        (autograd's version counters) since they were last written."""
+        return self._current is not None and self._current == self._token()
+
+    def mark_current(self):
+        """Records that the copies match the masters as they are now (called by whatever wrote
+        both, e.g. mamba_amd.optim.AdamW after its update)."""
+        self._current = self._token()
+
+    def targets(self, p):
+        """(shadow, transposed shadow or None, ld_t) of master p in the bf16 layout, else None."""
+        if self.bufs is None or self.flat.dtype != torch.bfloat16 or id(p) not in self.by_id:
+            return None
+        dst_t, ld_t = None, 0
+        if id(p) in self._tslot:
+            o, c, r = self._tslot[id(p)]
+            dst_t, ld_t = self.tflat[o + c:], r
+        return self.by_id[id(p)], dst_t, ld_t
+
     def refresh(self, dtype):
+        """Writes the copies from the masters, unless they already match them."""
         if self.bufs is None or self.flat.dtype != dtype:
             self._layout(dtype)
+            self._current = None
+        if self.is_current():
+            return
         native = (dtype == torch.bfloat16 and self.flat.is_cuda
                   and all(p.dtype == torch.float32 and p.is_contiguous() for p in self.params))
         with torch.no_grad():
@@ -190,10 +218,11 @@ class ShadowWeights:
                 lib = _lib.register_hip_kernel()
                 _lib.check(lib.mss_shadow_refresh(table.data_ptr(), n, tiles, _stream(self.flat)),
                            "mss_shadow_refresh")
-                return
-            torch._foreach_copy_(self.bufs, [p.detach() for p in self.params])
-            for g in self.groups:
-                self.t_by_key[tuple(id(w) for w in g)].copy_(torch.cat([w.detach() for w in g]).t())
+            else:
+                torch._foreach_copy_(self.bufs, [p.detach() for p in self.params])
+                for g in self.groups:
+                    self.t_by_key[tuple(id(w) for w in g)].copy_(torch.cat([w.detach() for w in g]).t())
+        self.mark_current()
 
     def stacked_t(self, *ws):
         """The contiguous transpose of the stacked shadows of ws, when kept, else None."""
@@ -559,10 +588,16 @@ class MambaLM(nn.Module):
         self._shadows = ShadowWeights([self.embedding] + [w for b in self.blocks for w in b.gemm_weights()],
                                       transposed=[g for b in self.blocks for g in ((b.in_proj, b.z_proj), (b.out_proj,))])
 
+    @property
+    def shadow_weights(self):
+        """The bf16 copies of the GEMM weights (ShadowWeights), e.g. for mamba_amd.optim.AdamW
+        to write with its update."""
+        return self._shadows
+
     def forward(self, tokens, seq_lens=None, act_dtype=torch.bfloat16, shadow_weights=True):
         """tokens (B, L) int64 -> logits (B*L, vocab) in act_dtype (rows in (b, t) order).
-        Low-precision GEMM weights are refreshed from the float32 masters once per call
-        (shadow_weights=False casts each weight at its use instead)."""
+        Low-precision GEMM weights are refreshed from the float32 masters once per call unless
+        they already match them (shadow_weights=False casts each weight at its use instead)."""
         batch = tokens.shape[0]
         weights = _PLAIN
         if act_dtype != torch.float32 and shadow_weights:

@@ -13,6 +13,7 @@ import torch.nn.functional as F
 
 from mamba_amd import _lib
 from mamba_amd.mamba1 import GraphedTrainStep, MambaLM
+from mamba_amd.optim import AdamW
 from oracle import mamba1_torch as ref
 from oracle import cscan64, scan64
 
@@ -211,11 +212,14 @@ def test_bf16_shadow_weights_match_per_use_casts():
 
 
 @pytest.mark.gpu
-def test_graphed_train_step_matches_eager():
+@pytest.mark.parametrize("opt", ["torch", "mss"])
+def test_graphed_train_step_matches_eager(opt):
     """The HIP-graph training step against eager steps from the same initial weights: the
     loss of every replay and the final weights agree (replays are checked one by one, with
-    eager work and synchronisations between them)."""
-    print("case graphed train step", flush=True)
+    eager work and synchronisations between them). With torch's fused AdamW, and with
+    mss_adamw (mamba_amd.optim.AdamW), which writes the bf16 shadows itself, so neither the
+    eager forwards after the first nor the captured one refresh them."""
+    print(f"case graphed train step opt={opt}", flush=True)
     from mamba_amd.lm_ops import cross_entropy
 
     cfg = dict(C1, vocab=256)
@@ -227,6 +231,8 @@ def test_graphed_train_step_matches_eager():
         torch.manual_seed(4)
         m = MambaLM(cfg["vocab"], cfg["d_model"], cfg["n_layers"], cfg["expand"], cfg["d_state"], None,
                     cfg["d_conv"], device="cuda")
+        if opt == "mss":
+            return m, AdamW(m.parameters(), lr=1e-3, shadows=m.shadow_weights)
         return m, torch.optim.AdamW(m.parameters(), lr=1e-3, fused=True, capturable=True)
 
     warm, steps = 3, 4
@@ -331,7 +337,8 @@ def test_c5_widths_one_layer_matches_oracle(act):
 @pytest.mark.gpu
 @pytest.mark.slow
 def test_c5_full_train_step_graph_matches_eager():
-    """The config-5 training step (24 layers, bf16, AdamW) at its workload: every eager step
+    """The config-5 training step (24 layers, bf16, mss_adamw writing the bf16 shadows) at its
+    workload, as the benchmark runs it: every eager step
     has a finite loss and finite, nonzero gradients, and the HIP-graph step replays the same
     losses and ends at the same weights as the eager steps (replays checked one by one)."""
     print("case c5 full train step graph vs eager", flush=True)
@@ -346,7 +353,7 @@ def test_c5_full_train_step_graph_matches_eager():
         torch.manual_seed(7)
         m = MambaLM(cfg["vocab"], cfg["d_model"], cfg["n_layers"], cfg["expand"], cfg["d_state"], cfg["dt_rank"],
                     cfg["d_conv"], device="cuda")
-        return m, torch.optim.AdamW(m.parameters(), lr=1e-3, fused=True, capturable=True)
+        return m, AdamW(m.parameters(), lr=1e-3, shadows=m.shadow_weights)
 
     warm, steps = 3, 3
     m_e, o_e = make()
