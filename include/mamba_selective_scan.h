@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 14
+#define MSS_ABI_VERSION 15
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -502,6 +502,24 @@ typedef struct mss_adamw_args {
 } mss_adamw_args;
 
 int mss_adamw(const mss_adamw_args* args, void* stream);
+
+/* --- Token embedding into a channel-major stream, and its gradient. -------------------
+ * Replace the XLA gather of the reference LM's input embedding (nnx.Embed,
+ * mamba/mamba1.py:378-380) and its scatter-add gradient, for a stream kept as [D][T].
+ * mss_embed_cm: h[f * ldh + t] = E[tokens[t] * D + f] for t < T, f < D (float32; E [V][D]
+ * rows contiguous, ldh >= T); a token outside [0, V) gives a column of NaN (nothing is read
+ * for it). h must not overlap E or tokens.
+ * mss_embed_cm_backward: dE[v * D + f] += sum of dh[f * ldh + t] over t with tokens[t] == v,
+ * given the tokens sorted stably (sorted_tokens ascending, order[i] the position of
+ * sorted_tokens[i]; e.g. a stable sort's values and indices). Each row of dE is updated by
+ * one workgroup, the run's terms added in a fixed association: the result does not depend on
+ * timing. Tokens outside [0, V) are skipped. D a multiple of 4 and at most 1024, and at most
+ * 2^24 tiles of 64 x 64 in both calls (MSS_ERR_UNSUPPORTED otherwise); dE and workspace 16-byte aligned, workspace >= 4 * T * D
+ * bytes (dh transposed token-major); dE overlapping neither dh nor the workspace. */
+int mss_embed_cm(const int64_t* tokens, int64_t T, const float* E, int32_t V, int32_t D, float* h, int64_t ldh,
+                 void* stream);
+int mss_embed_cm_backward(const float* dh, int64_t ldh, const int64_t* sorted_tokens, const int64_t* order, int64_t T,
+                          int32_t V, int32_t D, float* dE, void* workspace, int64_t workspace_bytes, void* stream);
 
 
 /* --- Reference-compatible entry points (float32, no fusions). ---------------------

@@ -15,7 +15,7 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "build"
 LIB_NAME = "libmamba_selective_scan_hip.so"
 SOURCES = ["mss_fwd.hip", "mss_fwd_bf16.hip", "mss_bwd.hip", "mss_conv.hip", "mss_norm.hip", "mss_xent.hip", "mss_step.hip", "mss_complex.hip", "mss_gemv.hip", "mss_proj.hip",
-           "mss_wgrad.hip", "mss_shadow.hip", "mss_adamw.hip", "mss_capi.cpp"]
+           "mss_wgrad.hip", "mss_shadow.hip", "mss_adamw.hip", "mss_embed.hip", "mss_capi.cpp"]
 ARCH = os.environ.get("MSS_OFFLOAD_ARCH", "gfx950")
 # Per-source machine-scheduler choice (MI355X, 11 interleaved trials, bit-identical outputs):
 # the backward scan and the bf16-I/O forward compiled with the ILP-maximising strategy run

@@ -50,6 +50,8 @@ hipError_t launch_proj(const ProjParams& p, hipStream_t stream);
 hipError_t launch_wgrad(const WgradParams& p, hipStream_t stream);
 hipError_t launch_shadow_refresh(const ShadowParams& p, hipStream_t stream);
 hipError_t launch_adamw(const AdamWParams& p, hipStream_t stream);
+hipError_t launch_embed_cm(const EmbedParams& p, hipStream_t stream);
+hipError_t launch_embed_cm_backward(const EmbedParams& p, hipStream_t stream);
 }  // namespace mss
 
 namespace {
@@ -895,6 +897,57 @@ int mss_adamw(const mss_adamw_args* a, void* stream) {
     if (e != hipSuccess) return hip_fail(e, "launching AdamW");
   }
   return MSS_OK;
+}
+
+
+int mss_embed_cm(const int64_t* tokens, int64_t T, const float* E, int32_t V, int32_t D, float* h, int64_t ldh,
+                 void* stream) {
+  if (!tokens || !E || !h || T <= 0 || T >= (1LL << 31) || V <= 0 || D <= 0 || ldh < T) return MSS_ERR_INVALID_ARGUMENT;
+  // (the grid: 64 x 64 tiles of 256 threads, fewer than 2^32 threads)
+  if (static_cast<long long>(D) * ldh >= (1LL << 40) || static_cast<long long>(V) * D >= (1LL << 40) ||
+      ((T + 63) / 64) * ((D + 63) / 64) >= (1LL << 24))
+    return MSS_ERR_UNSUPPORTED;
+  if (spans_overlap(h, D, 2 * ldh, 2 * T, E, V, 2LL * D, 2LL * D) || spans_overlap(h, D, 2 * ldh, 2 * T, tokens, 1, 0, 4 * T))
+    return MSS_ERR_INVALID_ARGUMENT;
+  mss::EmbedParams p{};
+  p.T = T;
+  p.V = V;
+  p.D = D;
+  p.ldh = ldh;
+  p.tokens = reinterpret_cast<const long long*>(tokens);
+  p.E = E;
+  p.h = h;
+  const hipError_t e = mss::launch_embed_cm(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching embedding gather");
+}
+
+int mss_embed_cm_backward(const float* dh, int64_t ldh, const int64_t* sorted_tokens, const int64_t* order, int64_t T,
+                          int32_t V, int32_t D, float* dE, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!dh || !sorted_tokens || !order || !dE || !workspace || T <= 0 || T >= (1LL << 31) || V <= 0 || D <= 0 ||
+      ldh < T)
+    return MSS_ERR_INVALID_ARGUMENT;
+  if (D % 4 != 0 || D > mss::kEmbedMaxD) return MSS_ERR_UNSUPPORTED;
+  if (static_cast<long long>(D) * ldh >= (1LL << 40) || static_cast<long long>(V) * D >= (1LL << 40) ||
+      ((T + 63) / 64) * ((D + 63) / 64) >= (1LL << 24))
+    return MSS_ERR_UNSUPPORTED;
+  if (!aligned16(dE) || !aligned16(workspace) || workspace_bytes < 4 * T * D) return MSS_ERR_INVALID_ARGUMENT;
+  // dE (float32, 2 bf16-sized units per element) against dh and the workspace.
+  if (spans_overlap(dE, V, 2LL * D, 2LL * D, dh, D, 2 * ldh, 2 * T) ||
+      spans_overlap(dE, V, 2LL * D, 2LL * D, workspace, 1, 0, 2 * T * D) ||
+      spans_overlap(workspace, 1, 0, 2 * T * D, dh, D, 2 * ldh, 2 * T))
+    return MSS_ERR_INVALID_ARGUMENT;
+  mss::EmbedParams p{};
+  p.T = T;
+  p.V = V;
+  p.D = D;
+  p.ldh = ldh;
+  p.dh = dh;
+  p.sorted_tokens = reinterpret_cast<const long long*>(sorted_tokens);
+  p.order = reinterpret_cast<const long long*>(order);
+  p.work = static_cast<float*>(workspace);
+  p.dE = dE;
+  const hipError_t e = mss::launch_embed_cm_backward(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MSS_OK : hip_fail(e, "launching embedding gradient");
 }
 
 

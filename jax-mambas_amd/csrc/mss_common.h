@@ -398,6 +398,22 @@ struct AdamWParams {
   float lr, beta1, beta2, eps, weight_decay;
 };
 
+// Token embedding into a channel-major stream and its gradient (mss_embed_cm*).
+constexpr int kEmbedMaxD = 1024;  // backward: model width limit (16 KB of LDS partial rows)
+struct EmbedParams {
+  long long T;
+  int V, D;
+  long long ldh;                    // row stride of h / dh (>= T)
+  const long long* tokens;          // [T]
+  const float* E;                   // [V][D]
+  float* h;                         // [D][ldh]
+  const float* dh;                  // [D][ldh]
+  const long long* sorted_tokens;   // [T], ascending (stable sort of tokens)
+  const long long* order;           // [T], positions of sorted_tokens
+  float* work;                      // [T][D]
+  float* dE;                        // [V][D], accumulated
+};
+
 struct StepParams {
   int batch, dim, dstate, delta_softplus;
   long long io_sb, io_sd, bc_sb, bc_sn;

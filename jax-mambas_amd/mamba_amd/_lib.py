@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 14
+MSS_ABI_VERSION = 15
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -71,6 +71,8 @@ EXPORTED_SYMBOLS = (
     "mss_wgrad",
     "mss_shadow_refresh",
     "mss_adamw",
+    "mss_embed_cm",
+    "mss_embed_cm_backward",
     "mss_strerror",
     "mss_last_hip_error",
     "mss_abi_version",
@@ -270,6 +272,11 @@ def register_hip_kernel(library_path=None):
     lib.mss_shadow_refresh.restype = ctypes.c_int
     lib.mss_adamw.argtypes = [ctypes.POINTER(AdamWArgs), _p]
     lib.mss_adamw.restype = ctypes.c_int
+    lib.mss_embed_cm.argtypes = [_p, ctypes.c_int64, _p, _i32, _i32, _p, ctypes.c_int64, _p]
+    lib.mss_embed_cm.restype = ctypes.c_int
+    lib.mss_embed_cm_backward.argtypes = [_p, ctypes.c_int64, _p, _p, ctypes.c_int64, _i32, _i32, _p, _p, ctypes.c_int64,
+                                          _p]
+    lib.mss_embed_cm_backward.restype = ctypes.c_int
     lib.mss_strerror.argtypes = [ctypes.c_int]
     lib.mss_strerror.restype = ctypes.c_char_p
     lib.mss_last_hip_error.argtypes = []

@@ -9,7 +9,11 @@ x = rmsnorm(hn) * weight in out_dtype (mamba/mamba1.py:300-337, nnx.RMSNorm(epsi
 ``cross_entropy(logits, targets) -> mean loss`` — logits (rows, vocab) bfloat16, targets
 (rows,) int64; fp32 math; the backward writes bf16 logit gradients in one pass.
 
-Both are differentiable; there is no CPU path.
+``embed_cm(table, tokens, holder=None) -> h`` — the input embedding gathered straight into
+the channel-major stream (D, T) (nnx.Embed, mamba/mamba1.py:378-380), its gradient summed
+per token deterministically, optionally into the tied head's gradient (GradHolder).
+
+All are differentiable; there is no CPU path.
 """
 from __future__ import annotations
 
@@ -18,7 +22,7 @@ import torch
 from . import _lib
 from .selective_scan_hip import _io_tag, _ptr, _require_gpu, _stream
 
-__all__ = ["add_rmsnorm", "cross_entropy"]
+__all__ = ["add_rmsnorm", "cross_entropy", "embed_cm", "GradHolder"]
 
 
 def _norm_args(hsrc, weight, eps, io):
@@ -154,3 +158,69 @@ def cross_entropy(logits, targets):
     if torch.is_grad_enabled() and logits.requires_grad and _fused_fits(logits):
         return _CrossEntropyFused.apply(logits, targets)
     return _CrossEntropy.apply(logits, targets)
+
+
+class GradHolder:
+    """Passes the tied output head's float32 gradient of the shared table to the embedding's
+    backward, which adds its own part in place and hands the sum to autograd as the table's
+    one gradient (instead of two dense gradients and an add). The head's backward runs first:
+    it belongs to the end of the forward."""
+
+    def __init__(self):
+        self.grad = None
+
+    def put(self, g):
+        self.grad = g
+
+    def take(self):
+        g, self.grad = self.grad, None
+        return g
+
+
+class _EmbedCM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, table, tokens, holder):
+        lib = _lib.register_hip_kernel()
+        V, D = table.shape
+        T = tokens.numel()
+        h = torch.empty(D, T, dtype=torch.float32, device=table.device)
+        _lib.check(lib.mss_embed_cm(tokens.data_ptr(), T, table.data_ptr(), V, D, h.data_ptr(), T, _stream(table)),
+                   "mss_embed_cm")
+        ctx.save_for_backward(tokens)
+        ctx.holder, ctx.shape = holder, table.shape
+        return h
+
+    @staticmethod
+    def backward(ctx, dh):
+        (tokens,) = ctx.saved_tensors
+        de = ctx.holder.take() if ctx.holder is not None else None
+        if de is None:
+            de = torch.zeros(ctx.shape, dtype=torch.float32, device=dh.device)
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        dh = dh.contiguous()
+        V, D = ctx.shape
+        T = tokens.numel()
+        st, order = torch.sort(tokens, stable=True)
+        work = torch.empty(T, D, dtype=torch.float32, device=dh.device)
+        lib = _lib.register_hip_kernel()
+        _lib.check(lib.mss_embed_cm_backward(dh.data_ptr(), dh.stride(0), st.data_ptr(), order.data_ptr(), T, V, D,
+                                             de.data_ptr(), work.data_ptr(), work.numel() * 4, _stream(dh)),
+                   "mss_embed_cm_backward")
+        return de, None, None
+
+
+def embed_cm(table, tokens, holder=None):
+    """h (D, T) float32 = table[tokens].T: the embedding rows of the flattened int64 tokens as
+    the columns of a channel-major stream (HIP gather through LDS tiles; a token outside the
+    table gives a column of NaN). Differentiable in `table`: the gradient is summed per token
+    in a fixed association (deterministic); `holder` (GradHolder) carries a gradient of the
+    same table from elsewhere (the tied head) to add to. Float32 tables, width a multiple of 4
+    up to 1024 for the gradient."""
+    _require_gpu(table, tokens)
+    if table.dtype != torch.float32 or table.dim() != 2 or not table.is_contiguous():
+        raise ValueError("embed_cm takes a contiguous float32 (vocab, width) table")
+    tokens = tokens.reshape(-1)
+    if tokens.dtype != torch.int64:
+        raise ValueError("embed_cm takes int64 tokens")
+    return _EmbedCM.apply(table, tokens.contiguous(), holder)

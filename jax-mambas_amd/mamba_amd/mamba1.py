@@ -31,7 +31,7 @@ import torch.nn.functional as F
 from . import _lib
 from .decode import (causal_conv1d_update, gemv, gemv_conv_update, gemv_state_update, norm_gemv_conv_update,
                      selective_state_update)
-from .lm_ops import add_rmsnorm
+from .lm_ops import GradHolder, add_rmsnorm, embed_cm
 from .proj import proj, proj_fits, wgrad, wgrad_fits
 from .selective_scan_hip import _io_tag, _ptr, _stream, selective_scan_fn
 
@@ -98,11 +98,13 @@ class _WeightMM(torch.autograd.Function):
 
 class _TiedHeadMM(torch.autograd.Function):
     """logits = x^T E_act^T for x (features, tokens) and the tied embedding E (vocab,
-    features); dE in float32 for the master embedding."""
+    features); dE in float32 for the master embedding, handed to the embedding gather's
+    backward through `holder` when given (one gradient edge for the shared table)."""
 
     @staticmethod
-    def forward(ctx, x, e, e_act):
+    def forward(ctx, x, e, e_act, holder=None):
         ctx.save_for_backward(x, e_act)
+        ctx.holder = holder
         return x.t() @ e_act.t()
 
     @staticmethod
@@ -110,7 +112,10 @@ class _TiedHeadMM(torch.autograd.Function):
         x, e_act = ctx.saved_tensors
         dx = e_act.t() @ dy.t() if ctx.needs_input_grad[0] else None
         de = _mm_fp32(dy.t(), x.t()) if ctx.needs_input_grad[1] else None
-        return dx, de, None
+        if de is not None and ctx.holder is not None:
+            ctx.holder.put(de)  # the embedding's backward adds its part and returns the sum
+            de = None
+        return dx, de, None, None
 
 
 class ShadowWeights:
@@ -264,10 +269,10 @@ class ShadowWeights:
             return w.to(x.dtype) @ x
         return _WeightMM.apply(x, w, self.by_id[id(w)], self.stacked_t(w))
 
-    def head(self, x, e):
+    def head(self, x, e, holder=None):
         if x.dtype == torch.float32 or not self.by_id:
             return x.t() @ e.to(x.dtype).t()
-        return _TiedHeadMM.apply(x, e, self.by_id[id(e)])
+        return _TiedHeadMM.apply(x, e, self.by_id[id(e)], holder)
 
 
 def _uniform_(t, bound):
@@ -603,12 +608,18 @@ class MambaLM(nn.Module):
         if act_dtype != torch.float32 and shadow_weights:
             self._shadows.refresh(act_dtype)
             weights = self._shadows
-        h = self.embedding[tokens.reshape(-1)].t().contiguous()   # (d_model, B*L) fp32
+        holder = None
+        d_model = self.embedding.shape[1]
+        if tokens.is_cuda and d_model % 4 == 0 and d_model <= 1024:
+            holder = GradHolder()
+            h = embed_cm(self.embedding, tokens, holder)             # (d_model, B*L) fp32
+        else:
+            h = self.embedding[tokens.reshape(-1)].t().contiguous()
         delta = None
         for blk, A in zip(self.blocks, self.a_matrices()):
             h, delta = blk(h, delta, batch, seq_lens, act_dtype, weights, A)
         _, hn = self.final_norm(h, delta, act_dtype)
-        return weights.head(hn, self.embedding)
+        return weights.head(hn, self.embedding, holder)
 
     def a_matrices(self):
         """Every block's S6 state matrix. Real A = -exp(A_log) of all blocks in one batched op
