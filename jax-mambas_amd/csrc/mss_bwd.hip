@@ -343,6 +343,10 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
           if (lane == 0) __hip_atomic_store(&s_done[w], gi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           continue;
         }
+        // The wave holding an accumulator row issues ahead of the waves still polling, so the
+        // row is handed on sooner (measured on MI355X, interleaved: backward 868 -> 845 us at
+        // c3, 343 -> 334 us at a c5 layer, 3109 -> 3036 us at c4; c2's 12-wave plan within 1 %).
+        __builtin_amdgcn_s_setprio(1);
         const float An = s_A[w][n];
         const float a2 = An * kLog2e;
         const float mu = s_mu[cl][n];
@@ -409,6 +413,7 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         for (int j = 0; j < kT; ++j) accn[j * 128] = accB[j];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's row writes have landed
         if (lane == 0) __hip_atomic_store(&s_done[w], gi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __builtin_amdgcn_s_setprio(0);
         dA_pend = dA_l;
         n_pend = n;
       }
