@@ -135,7 +135,8 @@ def gpu_step_setup(torch, cfg):
                   io_dtype=io, bc_dtype=io, u=P("u"), delta=P("delta"), A=P("A"), B=P("B"), C=P("C"),
                   D=P("D"), z=P("z"), delta_bias=P("delta_bias"), seq_lens=P("seq_lens"))
     fa = _lib.FwdArgs(**common, out=P("out"), last_state=P("last"), carries=P("carries"), y_pre=P("y_pre"))
-    ba = _lib.BwdArgs(**common, carries=P("carries"), y_pre=P("y_pre"), dout=P("dout"), dlast_state=P("dlast"),
+    ba = _lib.BwdArgs(**common, carries=P("carries"), y_pre=P("y_pre"), out=P("out"), dout=P("dout"),
+                      dlast_state=P("dlast"),
                       du=P("du"), ddelta=P("ddelta"), dA=P("dA"), dB=P("dB"), dC=P("dC"), dD=P("dD"), dz=P("dz"),
                       ddelta_bias=P("ddelta_bias"))
     ws_bytes = int(lib.mss_bwd_workspace_bytes(ba))

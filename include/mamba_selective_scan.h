@@ -20,7 +20,8 @@
  *   carries                               : [batch][dim][dstate][ceil(seqlen/8)] float32
  *                                           state h entering every 8-step segment
  *                                           (segment 0: initial_state)
- *   y_pre                                 : [batch][dim][seqlen] y before the z gate
+ *   y_pre                                 : [batch][dim][seqlen] y before the z gate (real A:
+ *                                           only where |z| < 1e-20; other elements unwritten)
  *   (carries and y_pre are residuals for the backward: with seq_lens, their values in
  *   512-step chunks past a row's length are unspecified; the backward does not read them)
  *
@@ -47,7 +48,7 @@
 extern "C" {
 #endif
 
-#define MSS_ABI_VERSION 15
+#define MSS_ABI_VERSION 16
 /* dstate limits (MSS_ERR_UNSUPPORTED beyond, MSS_ERR_INVALID_ARGUMENT beyond 256):
  * MSS_MAX_DSTATE_WIDE for the float32 real-A scans — mss_fwd / mss_bwd / mss_bwd_noalloc with
  * io and bc dtype MSS_F32, and the reference-signature mss_scan_* entry points (whose C
@@ -107,7 +108,9 @@ typedef struct mss_fwd_args {
   float* last_state; /* optional */
   float* carries;    /* optional; required by mss_bwd */
   void* y_pre;       /* optional [B][D][L] (io dtype, io strides): y before the silu(z)
-                        gate, the residual mss_bwd needs when z is given */
+                        gate, the residual mss_bwd needs when z is given. Real A: written
+                        only where |z| < 1e-20 (mss_bwd takes y sigma(z) from out / z
+                        elsewhere); complex A (mss_cfwd): written everywhere */
   mss_strides strides;
 } mss_fwd_args;
 
@@ -132,6 +135,7 @@ typedef struct mss_bwd_args {
   const int32_t* seq_lens;
   const float* carries;     /* from mss_fwd with the same inputs; required */
   const void* y_pre;        /* from mss_fwd; required iff z given */
+  const void* out;          /* mss_fwd's out; required iff z given (real A; unused by mss_cbwd) */
   const void* dout;
   const float* dlast_state; /* optional cotangent of last_state */
   void* du;

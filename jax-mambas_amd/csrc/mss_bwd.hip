@@ -279,16 +279,22 @@ __global__ __launch_bounds__(kW * 64) void bwd_kernel(BwdParams p) {
         load_seg<kT>(static_cast<const io_t*>(p.u) + row, tl, L, fast, uu);
         load_seg<kT>(static_cast<const io_t*>(p.dout) + row, tl, L, fast, g);
         if constexpr (kHasZ) {
-          // g = dout * silu(z); dz = dout * y * sigmoid(z) * (1 + z * (1 - sigmoid(z))),
-          // y the pre-gate output kept by the forward.
+          // g = dout * silu(z); dz = dout * y * sigmoid(z) * (1 + z * (1 - sigmoid(z))). With the
+          // forward's out = y z sigmoid(z): dz = dout * out * (1 / z + 1 - sigmoid(z)), and where
+          // |z| < kZTiny (out / z imprecise) y itself, which the forward kept there.
           float zr[kT], yp[kT];
           load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zr);
-          load_seg<kT>(static_cast<const io_t*>(p.y_pre) + row, tl, L, fast, yp);
+          load_seg<kT>(static_cast<const io_t*>(p.out) + row, tl, L, fast, yp);
+          const io_t* __restrict__ ykept = static_cast<const io_t*>(p.y_pre) + row;
 #pragma unroll
           for (int j = 0; j < kT; ++j) {
-            const float go = tl + j < len ? g[j] : 0.f;
+            const bool valid = tl + j < len;
+            const float go = valid ? g[j] : 0.f;
             const float sz = sigmoid(zr[j]);
-            yp[j] = go * yp[j] * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
+            float d = go * yp[j] * (fast_rcp(zr[j]) + (1.f - sz));
+            if (valid && __builtin_fabsf(zr[j]) < kZTiny)
+              d = go * to_f32(ykept[tl + j]) * sz * __builtin_fmaf(zr[j], 1.f - sz, 1.f);
+            yp[j] = valid ? d : 0.f;
             g[j] = go * zr[j] * sz;
           }
           if (active && has_dz) store_seg<kT>(static_cast<io_t*>(p.dz) + row, tl, L, fast, yp);

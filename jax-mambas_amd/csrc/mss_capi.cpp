@@ -202,7 +202,7 @@ int validate_bwd(const mss_bwd_args* a, bool cplx = false) {
   if (!a->u || !a->delta || !a->A || !a->B || !a->C || !a->carries || !a->dout) return MSS_ERR_INVALID_ARGUMENT;
   if (!a->du || !a->ddelta || !a->dA || !a->dB || !a->dC) return MSS_ERR_INVALID_ARGUMENT;
   if (a->D && !a->dD) return MSS_ERR_INVALID_ARGUMENT;
-  if (a->z && (!a->dz || !a->y_pre)) return MSS_ERR_INVALID_ARGUMENT;
+  if (a->z && (!a->dz || !a->y_pre || (!cplx && !a->out))) return MSS_ERR_INVALID_ARGUMENT;
   if (a->delta_bias && !a->ddelta_bias) return MSS_ERR_INVALID_ARGUMENT;
   Strides st;
   return resolve_strides(a->strides, a->batch, a->dim, a->seqlen, a->dstate, &st);
@@ -271,7 +271,7 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   const size_t bc_row = static_cast<size_t>(a->seqlen) * bc_e;
   p.vec_io = strides_aligned(st.io_sb, st.io_sd, io_e) && aligned16(a->u) && aligned16(a->delta) &&
              aligned16(a->z) && aligned16(a->dout) && aligned16(a->du) && aligned16(a->ddelta) &&
-             aligned16(a->dz) && aligned16(a->y_pre);
+             aligned16(a->dz) && aligned16(a->y_pre) && aligned16(a->out);
   p.vec_bc = (bc_row % 16 == 0) && strides_aligned(st.bc_sb, st.bc_sn, bc_e) && aligned16(a->B) &&
              aligned16(a->C);
   p.n_seg = n_seg_of(a->seqlen);
@@ -290,6 +290,7 @@ mss::BwdParams pack_bwd(const mss_bwd_args* a, const BwdLayout& l, char* ws) {
   p.seq_lens = a->seq_lens;
   p.carries = a->carries;
   p.y_pre = a->y_pre;
+  p.out = a->z ? a->out : nullptr;
   p.dout = a->dout;
   p.dlast = a->dlast_state;
   p.du = a->du;

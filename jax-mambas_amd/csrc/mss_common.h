@@ -502,6 +502,10 @@ struct FwdParams {
   void* y_pre;
 };
 
+// The silu(z) gate's backward needs y sigma(z); out = y z sigma(z) gives it as out / z wherever
+// z is not tiny, so the real-A forward keeps y itself (y_pre) only where |z| < kZTiny.
+constexpr float kZTiny = 1e-20f;
+
 // Backward launch shape: waves per workgroup and channels per workgroup.
 struct BwdPlan {
   int waves, chan_per_block;
@@ -528,7 +532,8 @@ struct BwdParams {
   const float* x0;
   const int* seq_lens;
   const float* carries;  // [B][D][N][n_seg] from the forward
-  const void* y_pre;
+  const void* y_pre;     // real A: y where |z| < kZTiny (elsewhere unwritten); complex A: y
+  const void* out;       // real A with z: the forward's gated output
   const void* dout;
   const float* dlast;
   void* du;

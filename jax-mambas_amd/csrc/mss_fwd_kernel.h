@@ -291,12 +291,6 @@ void fwd_kernel(FwdParams p) {
 
     if (active && p.out) {
       if (p.z) {
-        if (p.y_pre) {
-          float yp[kT];
-#pragma unroll
-          for (int j = 0; j < kT; ++j) yp[j] = (tl + j < len) ? y[j] : 0.f;
-          store_seg<kT>(static_cast<io_t*>(p.y_pre) + row, tl, L, fast, yp);
-        }
         float zv[kT];
         if (kZLds && z_lds) {
           // the wave's own copies, completed at the first round barrier
@@ -323,6 +317,14 @@ void fwd_kernel(FwdParams p) {
           }
         } else {
           load_seg<kT>(static_cast<const io_t*>(p.z) + row, tl, L, fast, zv);
+        }
+        if (p.y_pre) {
+          // The backward takes y sigma(z) from out / z; y itself is kept only where z is too
+          // small for that (rare: nothing else of the row is written).
+          io_t* __restrict__ yrow = static_cast<io_t*>(p.y_pre) + row;
+#pragma unroll
+          for (int j = 0; j < kT; ++j)
+            if (tl + j < len && __builtin_fabsf(zv[j]) < kZTiny) store_as(yrow + tl + j, y[j]);
         }
 #pragma unroll
         for (int j = 0; j < kT; ++j) y[j] *= zv[j] * sigmoid(zv[j]);

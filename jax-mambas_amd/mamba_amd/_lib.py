@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIBRARY_NAME = "libmamba_selective_scan_hip.so"
 
-MSS_ABI_VERSION = 15
+MSS_ABI_VERSION = 16
 MSS_OK = 0
 MSS_ERR_INVALID_ARGUMENT = 1
 MSS_ERR_UNSUPPORTED = 2
@@ -105,7 +105,7 @@ class BwdArgs(ctypes.Structure):
         ("discretization", _i32), ("delta_softplus", _i32), ("io_dtype", _i32), ("bc_dtype", _i32),
         ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
         ("D", _p), ("z", _p), ("delta_bias", _p), ("initial_state", _p), ("seq_lens", _p),
-        ("carries", _p), ("y_pre", _p), ("dout", _p), ("dlast_state", _p),
+        ("carries", _p), ("y_pre", _p), ("out", _p), ("dout", _p), ("dlast_state", _p),
         ("du", _p), ("ddelta", _p), ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("dz", _p),
         ("ddelta_bias", _p), ("dinitial_state", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
@@ -315,7 +315,7 @@ def bwd_plan(batch, dim, dstate, seqlen=2048, varlen=False, zoh=False, io_bf16=F
                 io_dtype=MSS_BF16 if io_bf16 else MSS_F32, bc_dtype=MSS_BF16 if bc_bf16 else MSS_F32,
                 u=256, delta=256, A=256, B=256, C=256, carries=256, dout=256, du=256, ddelta=256, dA=256,
                 dB=256, dC=256, seq_lens=256 if varlen else None, z=256 if z else None,
-                y_pre=256 if z else None, dz=256 if z else None)
+                y_pre=256 if z else None, out=256 if z else None, dz=256 if z else None)
     if strides is not None:
         a.strides = strides
     w, c = _i32(), _i32()

@@ -443,7 +443,7 @@ class _MambaMixer(torch.autograd.Function):
                           last_state=rv(last), carries=rv(carries), y_pre=y_pre.data_ptr(), strides=st)
         _lib.check((lib.mss_cfwd if cplx else lib.mss_fwd)(fa, stream), "scan forward")
         ctx.save_for_backward(x, xz, u, x_dbl, dt, carries, y_pre, A, D, dt_bias, conv_w, conv_b,
-                              w_xz_act, w_x_act, w_dt_act, seq_lens, w_xz_t)
+                              w_xz_act, w_x_act, w_dt_act, seq_lens, w_xz_t, y)
         ctx.batch, ctx.zoh, ctx.dims = batch, zoh, (di, r, n, L)
         ctx.mark_non_differentiable(last, xz)
         ctx.set_materialize_grads(False)  # no zero-filled gradients for last / xz
@@ -453,7 +453,7 @@ class _MambaMixer(torch.autograd.Function):
     def backward(ctx, dy, _dlast, _dxz):
         lib = _lib.register_hip_kernel()
         (x, xz, u, x_dbl, dt, carries, y_pre, A, D, dt_bias, conv_w, conv_b, w_xz_act, w_x_act, w_dt_act,
-         seq_lens, w_xz_t) = ctx.saved_tensors
+         seq_lens, w_xz_t, y) = ctx.saved_tensors
         di, r, n, L = ctx.dims
         batch = ctx.batch
         T = x.shape[1]
@@ -476,7 +476,8 @@ class _MambaMixer(torch.autograd.Function):
                           io_dtype=io, bc_dtype=io, u=u.data_ptr(), delta=dt.data_ptr(), A=rv(A),
                           B=x_dbl[r].data_ptr(), C=x_dbl[r + n].data_ptr(), D=_ptr(D), z=xz[di].data_ptr(),
                           delta_bias=dt_bias.data_ptr(), seq_lens=_ptr(seq_lens), carries=rv(carries),
-                          y_pre=y_pre.data_ptr(), dout=dy.data_ptr(), du=du.data_ptr(), ddelta=ddt.data_ptr(),
+                          y_pre=y_pre.data_ptr(), out=y.data_ptr(), dout=dy.data_ptr(), du=du.data_ptr(),
+                          ddelta=ddt.data_ptr(),
                           dA=rv(dA), dB=dx_dbl[r].data_ptr(), dC=dx_dbl[r + n].data_ptr(), dD=_ptr(dD),
                           dz=dxz[di].data_ptr(), ddelta_bias=dbias.data_ptr(), strides=st)
         ws_bytes = int((lib.mss_cbwd_workspace_bytes if cplx else lib.mss_bwd_workspace_bytes)(ba))

@@ -256,8 +256,8 @@ def _bwd_outputs(u, A, B, D, z, delta_bias, initial_state):
 def _scan_bwd_op(u: torch.Tensor, delta: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
                  D: Optional[torch.Tensor], z: Optional[torch.Tensor], delta_bias: Optional[torch.Tensor],
                  initial_state: Optional[torch.Tensor], seq_lens: Optional[torch.Tensor],
-                 carries: torch.Tensor, y_pre: torch.Tensor, dout: torch.Tensor, dlast: Optional[torch.Tensor],
-                 delta_softplus: bool, zoh: bool
+                 carries: torch.Tensor, y_pre: torch.Tensor, out: Optional[torch.Tensor], dout: torch.Tensor,
+                 dlast: Optional[torch.Tensor], delta_softplus: bool, zoh: bool
                  ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                             torch.Tensor, torch.Tensor, torch.Tensor]:
     """mss_bwd (mss_cbwd for a complex A): returns (du, ddelta, dA, dB, dC, dD, dz,
@@ -267,6 +267,7 @@ def _scan_bwd_op(u: torch.Tensor, delta: torch.Tensor, A: torch.Tensor, B: torch
     delta, z, dout = _conform(delta, io_layout), _conform(z, io_layout), _conform(dout.to(u.dtype), io_layout)
     C = _conform(C, bc_layout)
     y_pre = _conform(y_pre, io_layout) if z is not None else None
+    out = _conform(out, io_layout) if z is not None and out is not None else None
     dlast = None if dlast is None else dlast.to(_state_dtype(A)).contiguous()
     batch, dim, length = u.shape
     du, ddelta, dA, dB, dC, dD, dz, dbias, dinit = _bwd_outputs(u, A, B, D, z, delta_bias, initial_state)
@@ -277,7 +278,7 @@ def _scan_bwd_op(u: torch.Tensor, delta: torch.Tensor, A: torch.Tensor, B: torch
         io_dtype=_io_tag(u.dtype, "u"), bc_dtype=_io_tag(B.dtype, "B"),
         u=_ptr(u), delta=_ptr(delta), A=_rv(A), B=_ptr(B), C=_ptr(C), D=_ptr(D), z=_ptr(z),
         delta_bias=_ptr(delta_bias), initial_state=_rv(initial_state), seq_lens=_ptr(seq_lens),
-        carries=_rv(carries), y_pre=_ptr(y_pre), dout=_ptr(dout), dlast_state=_rv(dlast),
+        carries=_rv(carries), y_pre=_ptr(y_pre), out=_ptr(out), dout=_ptr(dout), dlast_state=_rv(dlast),
         du=_ptr(du), ddelta=_ptr(ddelta), dA=_rv(dA), dB=_ptr(dB), dC=_ptr(dC), dD=opt(dD, D),
         dz=opt(dz, z), ddelta_bias=opt(dbias, delta_bias), dinitial_state=opt(dinit, initial_state),
         strides=_strides(u, io_layout, B, bc_layout),
@@ -293,24 +294,26 @@ def _scan_bwd_op(u: torch.Tensor, delta: torch.Tensor, A: torch.Tensor, B: torch
 
 
 @_scan_bwd_op.register_fake
-def _(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre, dout, dlast,
+def _(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre, out, dout, dlast,
       delta_softplus, zoh):
     return _bwd_outputs(u, A, B, D, z, delta_bias, initial_state)
 
 
 def _scan_setup_context(ctx, inputs, output):
     u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, delta_softplus, zoh = inputs
-    _, _, carries, y_pre = output
-    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre)
+    out, _, carries, y_pre = output
+    # (the gate's backward reads the output itself: y sigma(z) = out / z)
+    out = out if z is not None else None
+    ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre, out)
     ctx.delta_softplus, ctx.zoh = delta_softplus, zoh
 
 
 def _scan_backward(ctx, dout, dlast, _dcarries, _dy_pre):
-    u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre = ctx.saved_tensors
+    u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens, carries, y_pre, out = ctx.saved_tensors
     if dout is None:
         dout = torch.zeros_like(u)
     g = torch.ops.mamba_amd.selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, initial_state, seq_lens,
-                                               carries, y_pre, dout, dlast, ctx.delta_softplus, ctx.zoh)
+                                               carries, y_pre, out, dout, dlast, ctx.delta_softplus, ctx.zoh)
     du, ddelta, dA, dB, dC, dD, dz, dbias, dinit = g
     pick = lambda t, given: t if given is not None else None
     return (du, ddelta, dA, dB, dC, pick(dD, D), pick(dz, z), pick(dbias, delta_bias),

@@ -165,6 +165,7 @@ def bwd_args(**kw):
 @pytest.mark.parametrize("kw", [
     dict(carries=None), dict(dout=None), dict(dB=None), dict(D=1), dict(z=1), dict(delta_bias=1),
     dict(seqlen=0), dict(discretization=5),
+    dict(z=1, dz=1, y_pre=1),  # z without the forward's out (dz comes from out / z)
 ])
 def test_bwd_validation(lib, kw):
     assert lib.mss_bwd(bwd_args(**kw), None) == _lib.MSS_ERR_INVALID_ARGUMENT
@@ -444,8 +445,8 @@ def _fake_scan(cplx, layout, with_extras):
         z = u if with_extras else None
         x0 = torch.empty(b, d, n, device="cuda", dtype=A.dtype) if with_extras else None
         fw = torch.ops.mamba_amd.selective_scan_fwd(u, u, A, B, B, D, z, D, x0, None, True, False)
-        bw = torch.ops.mamba_amd.selective_scan_bwd(u, u, A, B, B, D, z, D, x0, None, fw[2], fw[3], fw[0],
-                                                    fw[1], True, False)
+        bw = torch.ops.mamba_amd.selective_scan_bwd(u, u, A, B, B, D, z, D, x0, None, fw[2], fw[3],
+                                                    fw[0] if z is not None else None, fw[0], fw[1], True, False)
         return u, B, A, fw, bw
 
 

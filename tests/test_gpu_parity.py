@@ -330,6 +330,29 @@ def test_fused_no_extras_no_softplus():
     check_fused(ts, out, last, fw, g)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("lens", [None, [600, 333]])
+def test_gate_near_zero_z(dtype, lens):
+    """The gate's backward takes y sigmoid(z) as out / z except where |z| < 1e-20, where it reads
+    y itself, kept by the forward for those elements only: exact zeros of both signs, |z| of
+    1e-30 and 9e-21 (kept y), 2e-20 and 1e-6 (out / z), the zero of the gate's slope (z ~ -1.2785)
+    and |z| up to 100, scattered over every row, with and without lengths. Per element against
+    the oracle."""
+    log(f"case gate near zero z {dtype} lens={lens}")
+    x, dout, dlast = fused_case(77, 2, 24, 600, 16, dtype, lens=lens)
+    flat = x["z"].reshape(-1)
+    specials = np.array([0.0, -0.0, 1e-30, -1e-30, 9e-21, -9e-21, 2e-20, -2e-20, 1e-6, -1e-6, -1.2785, 30.0,
+                         -30.0, -100.0], np.float32)
+    pos = (np.arange(0, flat.size, 7) * 131) % flat.size
+    flat[pos] = specials[np.arange(pos.size) % specials.size]
+    if dtype == "bf16":
+        from mamba_amd.configs import round_to_bf16
+        x["z"] = round_to_bf16(x["z"])
+    ts, out, last = run_fused(x, dout, dlast, dtype, False)
+    fw, g = oracle_fused(x, dout, dlast, False)
+    check_fused(ts, out, last, fw, g, *tol(dtype))
+
+
 @pytest.mark.parametrize("lens", [[3000, 1025, 1, 0], [512, 2047, 2048, 2049]])
 def test_varlen_fp32(lens):
     log(f"case varlen lens={lens}")

@@ -45,13 +45,13 @@ def _forward(lib, x, b, d, l, n):
                       initial_state=p(x["initial_state"]), seq_lens=p(x["seq_lens"]), out=p(out),
                       last_state=p(last), carries=p(carries), y_pre=p(y_pre))
     _lib.check(lib.mss_fwd(fa, None), "mss_fwd")
-    return carries, y_pre
+    return carries, y_pre, out
 
 
 GRADS = ("du", "ddelta", "dA", "dB", "dC", "dD", "dz", "ddelta_bias", "dinitial_state")
 
 
-def _backward(lib, fn, x, carries, y_pre, dout, dlast, b, d, l, n, workspace=None):
+def _backward(lib, fn, x, carries, y_pre, out, dout, dlast, b, d, l, n, workspace=None):
     """Runs `fn` (mss_bwd or mss_bwd_noalloc) into NaN-filled outputs; returns them."""
     shapes = dict(du=(b, d, l), ddelta=(b, d, l), dA=(d, n), dB=(b, n, l), dC=(b, n, l), dD=(d,), dz=(b, d, l),
                   ddelta_bias=(d,), dinitial_state=(b, d, n))
@@ -61,7 +61,7 @@ def _backward(lib, fn, x, carries, y_pre, dout, dlast, b, d, l, n, workspace=Non
                       io_dtype=_lib.MSS_F32, bc_dtype=_lib.MSS_F32, u=p(x["u"]), delta=p(x["delta"]), A=p(x["A"]),
                       B=p(x["B"]), C=p(x["C"]), D=p(x["D"]), z=p(x["z"]), delta_bias=p(x["delta_bias"]),
                       initial_state=p(x["initial_state"]), seq_lens=p(x["seq_lens"]), carries=p(carries),
-                      y_pre=p(y_pre), dout=p(dout), dlast_state=p(dlast),
+                      y_pre=p(y_pre), out=p(out), dout=p(dout), dlast_state=p(dlast),
                       du=p(o["du"]), ddelta=p(o["ddelta"]), dA=p(o["dA"]), dB=p(o["dB"]), dC=p(o["dC"]),
                       dD=p(o["dD"]), dz=p(o["dz"]), ddelta_bias=p(o["ddelta_bias"]),
                       dinitial_state=p(o["dinitial_state"]))
@@ -80,13 +80,13 @@ def test_noalloc_backward_matches_workspace_backward():
                                      (3, (2, 48, 600, 32), [600, 257])):
         log(f"case noalloc b={b} d={d} l={l} n={n} lens={lens}")
         x, dout, dlast = _inputs(seed, b, d, l, n, lens)
-        carries, y_pre = _forward(lib, x, b, d, l, n)
+        carries, y_pre, out = _forward(lib, x, b, d, l, n)
         probe = _lib.BwdArgs(batch=b, dim=d, seqlen=l, dstate=n, seq_lens=None if lens is None else 1)
         ws_bytes = int(lib.mss_bwd_workspace_bytes(probe))
         assert 0 < ws_bytes <= _lib.MSS_NOALLOC_SCRATCH_BYTES
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        want = _backward(lib, lib.mss_bwd, x, carries, y_pre, dout, dlast, b, d, l, n, workspace=ws)
-        got = _backward(lib, lib.mss_bwd_noalloc, x, carries, y_pre, dout, dlast, b, d, l, n)
+        want = _backward(lib, lib.mss_bwd, x, carries, y_pre, out, dout, dlast, b, d, l, n, workspace=ws)
+        got = _backward(lib, lib.mss_bwd_noalloc, x, carries, y_pre, out, dout, dlast, b, d, l, n)
         for k in GRADS:
             assert bool(torch.isfinite(want[k]).all()), k
             assert torch.equal(got[k], want[k]), k
