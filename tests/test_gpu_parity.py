@@ -353,6 +353,24 @@ def test_gate_near_zero_z(dtype, lens):
     check_fused(ts, out, last, fw, g, *tol(dtype))
 
 
+def test_gate_output_changed_in_place_raises():
+    """With z the backward reads the forward's output (dz from out / z), so an in-place change
+    of that output before backward must raise torch's saved-tensor version error instead of
+    giving a wrong dz; without z the output is not saved and the same change is allowed."""
+    log("case gate output changed in place")
+    x, dout, _ = fused_case(78, 1, 8, 256, 4)
+    ts = {k: T(v).requires_grad_(True) for k, v in x.items() if k in ("u", "delta", "A", "B", "C", "z")}
+    out = selective_scan_fn(ts["u"], ts["delta"], ts["A"], ts["B"], ts["C"], z=ts["z"], delta_softplus=True)
+    out.mul_(2.0)
+    with pytest.raises(RuntimeError, match="inplace"):
+        (out * T(dout)).sum().backward()
+    out = selective_scan_fn(ts["u"], ts["delta"], ts["A"], ts["B"], ts["C"], delta_softplus=True)
+    out.mul_(2.0)
+    (out * T(dout)).sum().backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(ts["u"].grad).all()
+
+
 @pytest.mark.parametrize("lens", [[3000, 1025, 1, 0], [512, 2047, 2048, 2049]])
 def test_varlen_fp32(lens):
     log(f"case varlen lens={lens}")
