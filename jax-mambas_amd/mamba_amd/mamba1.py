@@ -105,7 +105,10 @@ class _TiedHeadMM(torch.autograd.Function):
     def forward(ctx, x, e, e_act, holder=None):
         ctx.save_for_backward(x, e_act)
         ctx.holder = holder
-        return x.t() @ e_act.t()
+        # From a token-major copy of x: hipBLASLt's product with both operands K-contiguous
+        # took 1.128 ms against 1.420 from the features-major view at the 130M shape (16384
+        # tokens, 768 features, 50280 words; MI355X), and the copy 0.054 ms.
+        return x.t().contiguous() @ e_act.t()
 
     @staticmethod
     def backward(ctx, dy):
