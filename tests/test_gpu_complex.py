@@ -166,6 +166,24 @@ def test_complex_fused(l, n, zoh):
     check(x, dout, dlast, zoh)
 
 
+@pytest.mark.parametrize("dtype,lens", [("f32", None), ("f32", [600, 317]), ("bf16", None)])
+def test_complex_gate_near_zero_z(dtype, lens):
+    """The complex backward takes y sigmoid(z) as out / z except where |z| < 1e-20, where it
+    reads y itself, kept by the forward there only: exact zeros of both signs, |z| just under
+    and over 1e-20, the zero of the gate's slope and |z| up to 100, scattered over every row."""
+    log(f"case complex gate near zero z {dtype} lens={lens}")
+    x, dout, dlast = complex_case(79, 2, 13, 600, 8, dtype, lens=lens)
+    flat = x["z"].reshape(-1)
+    specials = np.array([0.0, -0.0, 1e-30, -1e-30, 9e-21, -9e-21, 2e-20, -2e-20, 1e-6, -1e-6, -1.2785, 30.0,
+                         -30.0, -100.0], np.float32)
+    pos = (np.arange(0, flat.size, 7) * 131) % flat.size
+    flat[pos] = specials[np.arange(pos.size) % specials.size]
+    if dtype == "bf16":
+        from mamba_amd.configs import round_to_bf16
+        x["z"] = round_to_bf16(x["z"])
+    check(x, dout, dlast, False, dtype)
+
+
 @pytest.mark.parametrize("zoh", [False, True])
 def test_complex_varlen(zoh):
     log(f"case complex varlen zoh={zoh}")
